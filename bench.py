@@ -1,0 +1,305 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X HIP backend on Clove's hot path.
+
+One "step" is one pass of the fused elementwise chain y = gelu(a*b + c) * d
+over the four 16,777,216-element f32 inputs of configuration 2 (the workload
+the headline metric is quoted on), with every input already resident in HBM.
+Rank 0 prints ONE JSON line on stdout:
+
+  value        whole-job algorithmic HBM GB/s of the step (5 x 64 MiB per step)
+  roofline     the chain kernel: algorithmic bytes / mean kernel duration
+               (HIP events around every launch of the timed region) vs the
+               8 TB/s HBM3E peak; `traffic` is the measured HBM bytes per
+               launch when a rocprof counter summary is supplied (--traffic)
+  cpu_baseline the CPU restatement of Clove's Rayon kernels (oracle/), four
+               unfused passes as Clove's eager CPU path runs them, timed on
+               this host's cores
+  parts        the other configurations measured in the same run: the
+               broadcast chain, softmax and layer norm (GB/s), 4096^3 and
+               skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s) and
+               the MLP plan (us per forward), each with its roofline fraction
+               and a sampled CPU baseline.
+Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
+exits with a message.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, AMD published
+FP32_MFMA_PEAK_TFS = 157.3   # MI355X dense FP32 matrix, AMD published
+METRIC = "fused-op HBM GB/s (% of peak); f32 GEMM TFLOP/s; paged-decode tokens/s"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def timed(ca, launch, steps, warmup):
+    """Runs `launch` warmup + steps times.  Returns (wall ms per step,
+    per-launch kernel ms from events recorded between launches)."""
+    for _ in range(warmup):
+        launch()
+    ca.synchronize()
+    ca.event_reset()
+    t0 = time.perf_counter()
+    evs = [ca.event_record()]
+    keep = []
+    for _ in range(steps):
+        keep.append(launch())
+        evs.append(ca.event_record())
+    ca.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    per = np.array([ca.event_elapsed(evs[i], evs[i + 1]) for i in range(steps)])
+    del keep
+    return wall, per
+
+
+def cpu_time(fn, reps=3):
+    best = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        best.append(time.perf_counter() - t0)
+    return float(np.median(best))
+
+
+def roofline(bound, achieved, peak, unit, traffic=None):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------------------
+# parts
+# ---------------------------------------------------------------------------
+
+CHAIN = [("mul", -1, -2), ("add", 0, -3), ("gelu", 1), ("mul", 2, -4)]
+
+
+def bench_chain(ca, args, broadcast=False):
+    n = 4096 * 4096
+    ins = [ca.empty((4096, 4096)).fill_normal(1 + i) for i in range(4)]
+    if broadcast:
+        ins[2] = ca.empty((4096,)).fill_normal(3)
+    nbytes = 4 * n * 5 if not broadcast else 4 * n * 4 + 4 * 4096
+    wall, per = timed(ca, lambda: ca.fused_chain(CHAIN, ins), args.steps, args.warmup)
+    return ins, nbytes, wall, per
+
+
+def cpu_chain(oracle, ins_host):
+    a, b, c, d = ins_host
+    return lambda: oracle.mul(oracle.gelu(oracle.add(oracle.mul(a, b), c)), d)
+
+
+def bench_rows(ca, oracle, args, out):
+    g = np.random.Generator(np.random.PCG64(2))
+    x = ca.empty((8192, 4096)).fill_normal(2, 0.0, 2.0)
+    gam = ca.tensor(g.uniform(0.5, 1.5, 4096).astype(np.float32))
+    bet = ca.tensor(g.uniform(-0.1, 0.1, 4096).astype(np.float32))
+    n = 8192 * 4096
+    for name, launch, nbytes in (
+            ("softmax", lambda: ca.softmax(x), 2 * 4 * n),
+            ("layer_norm", lambda: ca.layer_norm(x, gam, bet), 2 * 4 * n + 2 * 4 * 4096)):
+        wall, per = timed(ca, launch, args.steps, args.warmup)
+        gbs = nbytes / (per.mean() * 1e-3) / 1e9
+        part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
+                "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        if not args.no_cpu:
+            rows = 1024  # sample: 1/8 of the rows
+            xs = x.read(0, rows * 4096).reshape(rows, 4096)
+            gh, bh = gam.numpy(), bet.numpy()
+            fn = (lambda: oracle.softmax(xs)) if name == "softmax" else \
+                (lambda: oracle.layer_norm(xs, gh, bh))
+            t = cpu_time(fn) * (8192 / rows)
+            part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": f"{rows} of 8192 rows, scaled"}
+        out[name] = part
+        log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), {per.mean() * 1e3:.1f} us")
+
+
+def bench_matmul(ca, oracle, args, out):
+    K = 4096
+    a = ca.empty((4096, K)).fill_normal(3, 0.0, 1 / 64)
+    b = ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64)
+    a32 = ca.empty((32, K)).fill_normal(333, 0.0, 1 / 64)
+    steps = max(5, args.steps // 10)
+    wall, per = timed(ca, lambda: ca.matmul(a, b), steps, max(2, args.warmup // 5))
+    flops = 2.0 * 4096 ** 3
+    tf = flops / (per.mean() * 1e-3) / 1e12
+    part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
+            "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
+    if not args.no_cpu:
+        rows = 128
+        ah = a.read(0, rows * K).reshape(rows, K)
+        bh = b.numpy()
+        # rayon_matmul transposes B once, then computes rows; time both and
+        # scale only the row part to 4096 rows.
+        t_t = cpu_time(lambda: oracle.matmul(ah, bh, rows=(0, 0)), reps=1)
+        t_s = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
+        t = t_t + max(t_s - t_t, 0.0) * (4096 / rows)
+        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                "cores": oracle.threads(), "kind": "port",
+                                "sample": f"{rows} of 4096 output rows plus the B transpose, "
+                                          "row time scaled to 4096"}
+    out["matmul_4096"] = part
+    log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
+        f"{per.mean():.3f} ms")
+    wall, per = timed(ca, lambda: ca.matmul(a32, b), args.steps, args.warmup)
+    nbytes = 4 * (32 * K + K * 4096 + 32 * 4096)
+    gbs = nbytes / (per.mean() * 1e-3) / 1e9
+    tfs = 2.0 * 32 * K * 4096 / (per.mean() * 1e-3) / 1e12
+    out["matmul_skinny_32"] = {"value": round(tfs, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
+                               "gbs": round(gbs, 1),
+                               "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    log(f"matmul 32x4096x4096: {tfs:.2f} TFLOP/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
+        f"{per.mean() * 1e3:.1f} us")
+
+
+def bench_paged(ca, oracle, args, out):
+    from clove_amd import workloads
+
+    P = workloads.PAGED
+    B, H, D, bs, nb = P["num_seqs"], P["num_heads"], P["head_dim"], P["block_size"], P["pool_blocks"]
+    ctx, bt = workloads.paged_layout(4)
+    kv = ca.empty((2, nb, bs, H, D)).fill_normal(4)
+    q = ca.tensor(np.random.Generator(np.random.PCG64(4)).standard_normal((B, H * D), dtype=np.float32))
+    tbt, tcl = ca.tensor(bt), ca.tensor(ctx)
+    wall, per = timed(ca, lambda: ca.paged_attention(q, None, None, kv, tbt, tcl), args.steps,
+                      args.warmup)
+    nbytes = workloads.paged_bytes(ctx, H, D, bs)
+    sec = per.mean() * 1e-3
+    gbs = nbytes / sec / 1e9
+    part = {"value": round(B / sec, 1), "unit": "tokens/s", "ms": round(per.mean(), 4),
+            "gbs": round(gbs, 1), "bytes": nbytes, "context_tokens": int(ctx.sum()),
+            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    if not args.no_cpu:
+        seqs = [0, 1, 2, 3]
+        plane, blk = nb * bs * H * D, bs * H * D
+        pool, sbt, scl = workloads.compact_pool(
+            lambda p, b: kv.read(p * plane + b * blk, blk).reshape(bs, H, D), bt, ctx, seqs, bs)
+        qh = q.numpy()[seqs]
+        t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl))
+        t_full = t * ctx.sum() / scl.sum()
+        part["cpu_baseline"] = {"value": round(B / t_full, 2), "unit": "tokens/s",
+                                "cores": oracle.threads(), "kind": "port",
+                                "sample": "4 of 32 sequences (all heads), scaled by context tokens"}
+    out["paged_decode"] = part
+    log(f"paged decode: {B / sec:.0f} tokens/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM), "
+        f"{per.mean() * 1e3:.1f} us")
+    del kv
+
+
+def bench_mlp(ca, oracle, args, out):
+    from clove_amd import workloads
+
+    x, w1, b1, w2, b2 = workloads.mlp_inputs(0)
+    g = ca.Graph()
+    ids = [g.input("64,784"), g.input("784,128"), g.input("1,128"), g.input("128,10"),
+           g.input("1,10")]
+    h = g.op("relu", g.op("add", g.op("matmul", ids[0], ids[1]), ids[2]))
+    y = g.op("softmax", g.op("add", g.op("matmul", h, ids[3]), ids[4]))
+    model = g.compile([y])
+    ins = [ca.tensor(v) for v in (x, w1, b1, w2, b2)]
+    wall, per = timed(ca, lambda: model.execute(ins), args.steps, args.warmup)
+    part = {"value": round(wall * 1e3, 2), "unit": "us/forward (wall, plan of "
+            f"{model.num_steps} steps)", "gpu_us": round(per.mean() * 1e3, 2)}
+    if not args.no_cpu:
+        t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5)
+        part["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/forward",
+                                "cores": oracle.threads(), "kind": "port", "sample": "full"}
+    out["mlp_forward"] = part
+    log(f"mlp plan: {wall * 1e3:.1f} us/forward wall, {per.mean() * 1e3:.1f} us GPU")
+
+
+# ---------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--parts", default="all",
+                    help="comma list of chain,bcast,rows,matmul,paged,mlp or 'all' / 'none'")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--traffic", default=None,
+                    help="JSON file with measured HBM bytes per chain launch (rocprof counters)")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
+              "build (see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+
+    import clove_amd as ca
+
+    ca.init(0)
+    parts = {"chain", "bcast", "rows", "matmul", "paged", "mlp"} if args.parts == "all" else \
+        set() if args.parts == "none" else set(args.parts.split(","))
+    oracle = None
+    if not args.no_cpu:
+        import oracle as oracle_mod
+        oracle = oracle_mod
+
+    # --- the headline step: config 2 chain ---
+    ins, nbytes, wall, per = bench_chain(ca, args)
+    kernel_ms = float(per.mean())
+    value = nbytes / (wall * 1e-3) / 1e9
+    achieved = nbytes / (kernel_ms * 1e-3) / 1e9
+    traffic = None
+    if args.traffic and os.path.exists(args.traffic):
+        with open(args.traffic) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+    log(f"chain gelu(a*b+c)*d: {value:.0f} GB/s wall, kernel {kernel_ms * 1e3:.1f} us -> "
+        f"{achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%} of peak)")
+    result = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(wall, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (splitmix64 normal(0,1) streams, seeds 1-4)",
+        "config": {"workload": "config 2: fused chain y = gelu(a*b+c)*d, 4 x [4096,4096] f32",
+                   "elements": 4096 * 4096, "bytes_per_step": nbytes},
+        "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s", traffic),
+    }
+    if oracle is not None:
+        host = [ins[i].numpy() for i in range(4)]
+        t = cpu_time(cpu_chain(oracle, host))
+        result["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                  "cores": oracle.threads(), "kind": "port",
+                                  "sample": "full config 2 workload, 4 unfused passes "
+                                            "(Clove's eager CPU path), median of 3"}
+        del host
+    del ins
+
+    out = {}
+    if "bcast" in parts:
+        bins, bbytes, bwall, bper = bench_chain(ca, args, broadcast=True)
+        gbs = bbytes / (bper.mean() * 1e-3) / 1e9
+        out["chain_broadcast"] = {"value": round(gbs, 1), "unit": "GB/s",
+                                  "ms": round(bper.mean(), 4), "bytes": bbytes,
+                                  "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"chain broadcast: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+        del bins
+    if "rows" in parts:
+        bench_rows(ca, oracle, args, out)
+    if "matmul" in parts:
+        bench_matmul(ca, oracle, args, out)
+    if "paged" in parts:
+        bench_paged(ca, oracle, args, out)
+    if "mlp" in parts:
+        bench_mlp(ca, oracle, args, out)
+    if out:
+        result["parts"] = out
+    ca.synchronize()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,501 @@
+// graph.cpp -- lazy tracing, planning and execution for the hot-path IR.
+//
+// The counterpart of Clove's LazyBackend tracer (lazy.rs:36-1153),
+// compile() (lazy.rs:4273-5302) and CompiledModel::execute
+// (lazy.rs:2545-4271), restricted to the opcodes of the hot path:
+// Input, MatMul, the elementwise ops, Softmax, LayerNorm, PagedAttention.
+//
+// Passes, in the reference's order:
+//   1. dead-code elimination from the requested outputs (lazy.rs:1553-1571);
+//   2. constant folding of ScalarMul(1.0) (lazy.rs:1573-1598), skipping
+//      nodes without an operand (the reference indexes dependencies[0] of
+//      such nodes, e.g. the ones() seed of backward, and panics);
+//   3. planning (lazy.rs:1610-2496): consecutive elementwise nodes with the
+//      same element count form one fused chain; MatMul, Softmax, LayerNorm
+//      and PagedAttention are barriers that flush the chain.  Every chain
+//      value consumed outside its chain or requested as an output is stored
+//      (the reference stores only the chain's last value, lazy.rs:1823);
+//   4. liveness (lazy.rs:2500-2535): step outputs share virtual buffers
+//      whose last reader has already run; buffers live in the model and grow
+//      on demand (the reference reallocates at 2x, lazy.rs:2585-2607).
+// Execution binds inputs in Input-node creation order (the reference binds
+// by node id, which coincides for inputs traced first, lazy.rs:2618-2619),
+// evaluates symbolic shapes with the S0..S3 environment, and returns fresh
+// tensors for the requested outputs, so results never alias model buffers.
+#include <algorithm>
+#include <cctype>
+#include <cmath>
+#include <map>
+#include <memory>
+#include <set>
+#include <sstream>
+
+#include "common.hpp"
+#include "graph.hpp"
+#include "runtime.hpp"
+
+namespace clove {
+
+// ---- SymInt ------------------------------------------------------------------
+
+int64_t SymExpr::eval(const int64_t *env) const {
+    switch (kind) {
+    case CONST: return value;
+    case SYM: return env ? env[value] : 1;  // backend.rs:43: unknown symbol -> 1
+    case ADD: return a->eval(env) + b->eval(env);
+    case SUB: {  // backend.rs:45: saturating_sub
+        const int64_t x = a->eval(env), y = b->eval(env);
+        return x > y ? x - y : 0;
+    }
+    default: return a->eval(env) * b->eval(env);
+    }
+}
+
+std::string SymExpr::str() const {
+    switch (kind) {
+    case CONST: return std::to_string(value);
+    case SYM: return "S" + std::to_string(value);
+    case ADD: return "(" + a->str() + "+" + b->str() + ")";
+    case SUB: return "(" + a->str() + "-" + b->str() + ")";
+    default: return "(" + a->str() + "*" + b->str() + ")";
+    }
+}
+
+SymPtr SymExpr::constant(int64_t v) {
+    auto e = std::make_shared<SymExpr>();
+    e->kind = CONST;
+    e->value = v;
+    return e;
+}
+
+SymPtr SymExpr::binop(int kind, SymPtr a, SymPtr b) {
+    auto e = std::make_shared<SymExpr>();
+    e->kind = kind;
+    e->a = std::move(a);
+    e->b = std::move(b);
+    return e;
+}
+
+namespace {
+
+struct Parser {
+    const std::string &s;
+    size_t i = 0;
+    explicit Parser(const std::string &src) : s(src) {}
+    void ws() {
+        while (i < s.size() && std::isspace((unsigned char)s[i])) ++i;
+    }
+    [[noreturn]] void bad(const std::string &why) {
+        fail(CLOVE_HIP_ERR_INVALID, "shape \"" + s + "\": " + why + " at offset " + std::to_string(i));
+    }
+    SymPtr factor() {
+        ws();
+        if (i < s.size() && s[i] == '(') {
+            ++i;
+            SymPtr e = expr();
+            ws();
+            if (i >= s.size() || s[i] != ')') bad("expected ')'");
+            ++i;
+            return e;
+        }
+        if (i < s.size() && s[i] == 'S') {
+            ++i;
+            if (i >= s.size() || s[i] < '0' || s[i] > '3') bad("symbols are S0..S3");
+            auto e = std::make_shared<SymExpr>();
+            e->kind = SymExpr::SYM;
+            e->value = s[i++] - '0';
+            return e;
+        }
+        if (i < s.size() && std::isdigit((unsigned char)s[i])) {
+            int64_t v = 0;
+            while (i < s.size() && std::isdigit((unsigned char)s[i])) v = v * 10 + (s[i++] - '0');
+            return SymExpr::constant(v);
+        }
+        bad("expected a number, S0..S3 or '('");
+    }
+    SymPtr term() {
+        SymPtr e = factor();
+        for (;;) {
+            ws();
+            if (i < s.size() && s[i] == '*') {
+                ++i;
+                e = SymExpr::binop(SymExpr::MUL, e, factor());
+            } else {
+                return e;
+            }
+        }
+    }
+    SymPtr expr() {
+        SymPtr e = term();
+        for (;;) {
+            ws();
+            if (i < s.size() && (s[i] == '+' || s[i] == '-')) {
+                const int k = s[i++] == '+' ? SymExpr::ADD : SymExpr::SUB;
+                e = SymExpr::binop(k, e, term());
+            } else {
+                return e;
+            }
+        }
+    }
+};
+
+SymPtr product(const std::vector<SymPtr> &shape) {
+    if (shape.empty()) return SymExpr::constant(1);
+    SymPtr e = shape[0];
+    for (size_t i = 1; i < shape.size(); ++i) e = SymExpr::binop(SymExpr::MUL, e, shape[i]);
+    return e;
+}
+
+std::string shape_key(const std::vector<SymPtr> &shape) { return product(shape)->str(); }
+
+const char *op_name(int op) {
+    switch (op) {
+    case CLOVE_OP_INPUT: return "Input";
+    case CLOVE_OP_MATMUL: return "MatMul";
+    case CLOVE_OP_ADD: return "Add";
+    case CLOVE_OP_SUB: return "Sub";
+    case CLOVE_OP_MUL: return "Mul";
+    case CLOVE_OP_SCALAR_MUL: return "ScalarMul";
+    case CLOVE_OP_FLATTEN: return "Flatten";
+    case CLOVE_OP_RELU: return "ReLU";
+    case CLOVE_OP_GELU: return "GELU";
+    case CLOVE_OP_SIN: return "Sin";
+    case CLOVE_OP_COS: return "Cos";
+    case CLOVE_OP_SOFTMAX: return "Softmax";
+    case CLOVE_OP_LAYER_NORM: return "LayerNorm";
+    case CLOVE_OP_DROPOUT: return "Dropout";
+    case CLOVE_OP_RELU_GRAD: return "ReluGrad";
+    case CLOVE_OP_GELU_GRAD: return "GeluGrad";
+    case CLOVE_OP_CAST: return "Cast";
+    case CLOVE_OP_SIGMOID: return "Sigmoid";
+    case CLOVE_OP_TANH: return "Tanh";
+    case CLOVE_OP_PAGED_ATTENTION: return "PagedAttention";
+    default: return "?";
+    }
+}
+
+}  // namespace
+
+std::vector<SymPtr> parse_shape(const std::string &spec) {
+    std::vector<SymPtr> dims;
+    std::string cur;
+    std::stringstream ss(spec);
+    while (std::getline(ss, cur, ',')) {
+        Parser p(cur);
+        SymPtr e = p.expr();
+        p.ws();
+        if (p.i != cur.size()) p.bad("trailing characters");
+        dims.push_back(e);
+    }
+    CLOVE_REQUIRE(!dims.empty(), CLOVE_HIP_ERR_INVALID, "empty shape");
+    return dims;
+}
+
+// ---- tracing -----------------------------------------------------------------
+
+int Graph::add_input(const std::string &spec) {
+    Node n;
+    n.id = (int)nodes.size();
+    n.op = CLOVE_OP_INPUT;
+    n.shape = parse_shape(spec);
+    nodes.push_back(n);
+    input_order.push_back(n.id);
+    return n.id;
+}
+
+int Graph::add_op(int op, const std::vector<int> &deps, float param) {
+    for (int d : deps)
+        CLOVE_REQUIRE(d >= 0 && d < (int)nodes.size(), CLOVE_HIP_ERR_INVALID,
+                      std::string(op_name(op)) + ": operand " + std::to_string(d) + " does not exist");
+    Node n;
+    n.id = (int)nodes.size();
+    n.op = op;
+    n.deps = deps;
+    n.param = param;
+    auto want = [&](size_t k) {
+        CLOVE_REQUIRE(deps.size() == k, CLOVE_HIP_ERR_INVALID,
+                      std::string(op_name(op)) + " takes " + std::to_string(k) + " operands");
+    };
+    const int ar = ew_arity(op);
+    if (ar > 0) {
+        want((size_t)ar);
+        if (op == CLOVE_OP_FLATTEN)  // lazy.rs:571-580: [1, numel]
+            n.shape = {SymExpr::constant(1), product(nodes[deps[0]].shape)};
+        else
+            n.shape = nodes[deps[0]].shape;  // lazy.rs:206: the first operand's shape
+    } else if (op == CLOVE_OP_MATMUL) {   // lazy.rs:266-277
+        want(2);
+        const auto &bs = nodes[deps[1]].shape;
+        CLOVE_REQUIRE(bs.size() == 2, CLOVE_HIP_ERR_SHAPE, "MatMul: b must be 2-d");
+        n.shape = nodes[deps[0]].shape;
+        n.shape.back() = bs[1];
+    } else if (op == CLOVE_OP_SOFTMAX) {
+        want(1);
+        n.shape = nodes[deps[0]].shape;
+    } else if (op == CLOVE_OP_LAYER_NORM) {
+        want(3);
+        n.shape = nodes[deps[0]].shape;
+    } else if (op == CLOVE_OP_PAGED_ATTENTION) {  // lazy.rs:860-886: q's shape
+        want(6);
+        n.shape = nodes[deps[0]].shape;
+    } else {
+        fail(CLOVE_HIP_ERR_INVALID, "opcode " + std::to_string(op) + " is not on the hot path");
+    }
+    nodes.push_back(n);
+    return n.id;
+}
+
+// ---- compile -----------------------------------------------------------------
+
+Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inputs(g.input_order), outputs(outs) {
+    for (int o : outs)
+        CLOVE_REQUIRE(o >= 0 && o < (int)nodes.size(), CLOVE_HIP_ERR_INVALID,
+                      "output node " + std::to_string(o) + " does not exist");
+    CLOVE_REQUIRE(!outs.empty(), CLOVE_HIP_ERR_INVALID, "no outputs requested");
+
+    // 1. dead-code elimination
+    std::vector<char> alive(nodes.size(), 0);
+    std::vector<int> stack(outs.begin(), outs.end());
+    while (!stack.empty()) {
+        const int id = stack.back();
+        stack.pop_back();
+        if (alive[id]) continue;
+        alive[id] = 1;
+        for (int d : nodes[id].deps) stack.push_back(d);
+    }
+    // 2. constant folding: x * 1.0 is x.  A folded node that is itself an
+    // output stays (it must produce a buffer).
+    std::vector<int> alias(nodes.size());
+    for (size_t i = 0; i < nodes.size(); ++i) alias[i] = (int)i;
+    std::set<int> out_set(outs.begin(), outs.end());
+    for (auto &n : nodes) {
+        if (!alive[n.id]) continue;
+        for (int &d : n.deps) d = alias[d];
+        if (n.op == CLOVE_OP_SCALAR_MUL && !n.deps.empty() &&
+            std::fabs(n.param - 1.0f) < 1.1920929e-7f && !out_set.count(n.id)) {
+            alias[n.id] = n.deps[0];
+            alive[n.id] = 0;
+            ++folded;
+        }
+    }
+    for (const Node &n : nodes)
+        if (alive[n.id]) ++live_nodes;
+
+    // Consumers of each node, for deciding what a chain must store.
+    std::vector<std::vector<int>> users(nodes.size());
+    for (const Node &n : nodes)
+        if (alive[n.id])
+            for (int d : n.deps) users[d].push_back(n.id);
+
+    // 3. planning
+    std::vector<int> group;
+    auto flush = [&]() {
+        if (group.empty()) return;
+        Step st;
+        st.kind = Step::FUSED;
+        std::set<int> members(group.begin(), group.end());
+        std::map<int, int> pos;  // node id -> index in chain
+        for (size_t i = 0; i < group.size(); ++i) pos[group[i]] = (int)i;
+        for (size_t i = 0; i < group.size(); ++i) {
+            const Node &n = nodes[group[i]];
+            ChainOp op;
+            op.opcode = n.op;
+            op.param = n.param;
+            int srcs[2] = {0, 0};
+            for (size_t j = 0; j < n.deps.size(); ++j) {
+                const int d = n.deps[j];
+                if (members.count(d)) {
+                    srcs[j] = pos[d];
+                } else {
+                    auto it = std::find(st.in.begin(), st.in.end(), d);
+                    int k = (int)(it - st.in.begin());
+                    if (it == st.in.end()) st.in.push_back(d);
+                    srcs[j] = -(k + 1);
+                }
+            }
+            op.src0 = srcs[0];
+            op.src1 = srcs[1];
+            bool escapes = out_set.count(n.id) > 0;
+            for (int u : users[n.id])
+                if (!members.count(u)) escapes = true;
+            op.store = escapes || i + 1 == group.size();
+            if (op.store) st.out.push_back(n.id);
+            st.chain.push_back(op);
+        }
+        st.numel = product(nodes[group.back()].shape);
+        steps.push_back(st);
+        group.clear();
+    };
+    for (const Node &n : nodes) {
+        if (!alive[n.id] || n.op == CLOVE_OP_INPUT) continue;
+        if (ew_arity(n.op) > 0) {
+            if (!group.empty() &&
+                (shape_key(nodes[group.back()].shape) != shape_key(n.shape) ||
+                 (int)group.size() >= 32))
+                flush();
+            group.push_back(n.id);
+            continue;
+        }
+        flush();
+        Step st;
+        switch (n.op) {
+        case CLOVE_OP_MATMUL: st.kind = Step::MATMUL; break;
+        case CLOVE_OP_SOFTMAX: st.kind = Step::SOFTMAX; break;
+        case CLOVE_OP_LAYER_NORM: st.kind = Step::LAYER_NORM; break;
+        default: st.kind = Step::PAGED; break;
+        }
+        st.in = n.deps;
+        st.out = {n.id};
+        steps.push_back(st);
+    }
+    flush();
+
+    // 4. liveness: a virtual buffer is released after the last step reading it.
+    std::map<int, int> last_use;
+    for (size_t i = 0; i < steps.size(); ++i)
+        for (int d : steps[i].in) last_use[d] = (int)i;
+    std::vector<int> free_list;
+    for (size_t i = 0; i < steps.size(); ++i) {
+        for (int o : steps[i].out) {
+            if (!free_list.empty()) {
+                vbuf[o] = free_list.back();
+                free_list.pop_back();
+            } else {
+                vbuf[o] = num_vbufs++;
+            }
+        }
+        for (int d : steps[i].in) {
+            auto it = vbuf.find(d);
+            if (it != vbuf.end() && last_use[d] == (int)i && !out_set.count(d))
+                free_list.push_back(it->second);
+        }
+    }
+}
+
+std::string Model::describe() const {
+    std::ostringstream s;
+    for (const Step &st : steps) {
+        switch (st.kind) {
+        case Step::FUSED: {
+            s << "Fused[";
+            for (size_t i = 0; i < st.chain.size(); ++i)
+                s << (i ? "," : "") << op_name(st.chain[i].opcode);
+            s << "]";
+            break;
+        }
+        case Step::MATMUL: s << "MatMul"; break;
+        case Step::SOFTMAX: s << "Softmax"; break;
+        case Step::LAYER_NORM: s << "LayerNorm"; break;
+        default: s << "PagedAttention"; break;
+        }
+        s << " in=(";
+        for (size_t i = 0; i < st.in.size(); ++i) s << (i ? "," : "") << st.in[i];
+        s << ") out=(";
+        for (size_t i = 0; i < st.out.size(); ++i) s << (i ? "," : "") << st.out[i];
+        s << ")\n";
+    }
+    s << "vbufs=" << num_vbufs << " folded=" << folded << " live=" << live_nodes << "\n";
+    return s.str();
+}
+
+// ---- execute -----------------------------------------------------------------
+
+std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const int64_t *env) {
+    CLOVE_REQUIRE(in.size() == inputs.size(), CLOVE_HIP_ERR_INVALID,
+                  "model has " + std::to_string(inputs.size()) + " inputs, got " +
+                      std::to_string(in.size()));
+    std::map<int, const Tensor *> bound;
+    for (size_t i = 0; i < inputs.size(); ++i) {
+        CLOVE_REQUIRE(in[i] != nullptr, CLOVE_HIP_ERR_INVALID, "input " + std::to_string(i) + " is NULL");
+        const Node &n = nodes[inputs[i]];
+        const int64_t want = product(n.shape)->eval(env);
+        CLOVE_REQUIRE((int64_t)in[i]->numel == want, CLOVE_HIP_ERR_SHAPE,
+                      "input " + std::to_string(i) + " has " + std::to_string(in[i]->numel) +
+                          " elements, the graph expects " + std::to_string(want));
+        bound[inputs[i]] = in[i].get();
+    }
+
+    // Evaluate shapes and size the virtual buffers.
+    auto eval_shape = [&](int id) {
+        std::vector<size_t> s;
+        for (const SymPtr &d : nodes[id].shape) s.push_back((size_t)std::max<int64_t>(0, d->eval(env)));
+        return s;
+    };
+    std::vector<size_t> need(num_vbufs, 0);
+    for (const auto &kv : vbuf) need[kv.second] = std::max(need[kv.second], numel_of(eval_shape(kv.first)));
+    if (buffers.size() < (size_t)num_vbufs) buffers.resize(num_vbufs);
+    for (int v = 0; v < num_vbufs; ++v) {
+        if (!buffers[v] || buffers[v]->numel < need[v]) {
+            const size_t cap = need[v] < 256 ? 256 : need[v] * 2;
+            buffers[v] = new_tensor({cap}, CLOVE_HIP_F32);
+        }
+    }
+    // Views of the virtual buffers with each node's shape.
+    std::map<int, std::unique_ptr<Tensor>> views;
+    auto view_of = [&](int id) -> Tensor * {
+        auto it = views.find(id);
+        if (it != views.end()) return it->second.get();
+        auto t = std::make_unique<Tensor>();
+        t->owned = false;
+        t->dtype = CLOVE_HIP_F32;
+        t->shape = eval_shape(id);
+        t->numel = numel_of(t->shape);
+        const Tensor &buf = *buffers[vbuf.at(id)];
+        t->data = buf.data;
+        t->bytes = buf.bytes;
+        Tensor *raw = t.get();
+        views[id] = std::move(t);
+        return raw;
+    };
+    auto arg = [&](int id) -> const Tensor * {
+        auto it = bound.find(id);
+        if (it != bound.end()) return it->second;
+        return view_of(id);
+    };
+
+    for (const Step &st : steps) {
+        switch (st.kind) {
+        case Step::FUSED: {
+            std::vector<const Tensor *> ins;
+            for (int d : st.in) ins.push_back(arg(d));
+            std::vector<Tensor *> outs;
+            for (int o : st.out) outs.push_back(view_of(o));
+            const int64_t n = st.numel->eval(env);
+            run_chain(st.chain, ins, outs, (size_t)std::max<int64_t>(0, n));
+            break;
+        }
+        case Step::MATMUL:
+            HipBackend::matmul_into(*arg(st.in[0]), *arg(st.in[1]), *view_of(st.out[0]));
+            break;
+        case Step::SOFTMAX:
+            HipBackend::softmax_into(*arg(st.in[0]), *view_of(st.out[0]));
+            break;
+        case Step::LAYER_NORM:
+            HipBackend::layer_norm_into(*arg(st.in[0]), *arg(st.in[1]), *arg(st.in[2]),
+                                        *view_of(st.out[0]));
+            break;
+        case Step::PAGED: {
+            const Tensor *q = arg(st.in[0]);
+            const int D = (int)arg(st.in[3])->shape.back();
+            HipBackend::paged_attention_into(*q, arg(st.in[1]), arg(st.in[2]), *arg(st.in[3]),
+                                             *arg(st.in[4]), *arg(st.in[5]),
+                                             1.0f / std::sqrt((float)D), *view_of(st.out[0]));
+            break;
+        }
+        }
+    }
+
+    // Fresh tensors for the outputs (device-to-device copies on the stream).
+    std::vector<TensorNode> result;
+    for (int o : outputs) {
+        const Tensor *src = arg(o);
+        TensorNode t = new_tensor(src->shape, src->dtype);
+        if (src->numel)
+            CLOVE_HIP_CHECK(hipMemcpyAsync(t->data, src->data, src->numel * 4,
+                                           hipMemcpyDeviceToDevice, ctx().stream));
+        result.push_back(t);
+    }
+    return result;
+}
+
+}  // namespace clove

@@ -1,0 +1,297 @@
+// jit.cpp -- runtime code generation for fused elementwise chains.
+//
+// The MI355X counterpart of Clove's `flush_fused` WGSL generator
+// (lazy.rs:1694-1838): a chain of elementwise IR nodes becomes one kernel.
+// The generated source is a short HIP body (one line per op) dropped into a
+// fixed kernel skeleton (kernels/ew_chain_kernel.h) that streams 16-byte
+// vectors; it is compiled for gfx950 with hipRTC, loaded with
+// hipModuleLoadData and launched with hipModuleLaunchKernel.  Kernels are
+// cached by signature: the op structure plus each input's broadcast class.
+// Op parameters (ScalarMul factors, dropout scales) are kernel arguments, so
+// they never cause a recompile.
+//
+// Differences from the reference generator, on purpose:
+//   - every op with `store` set is written, not only the last one
+//     (lazy.rs:1823 drops intermediates that escape the group);
+//   - an opcode the generator does not know is an error, not silently
+//     skipped (lazy.rs:1820 `_ => {}`);
+//   - indices are 64-bit and vectorised; the reference dispatches one thread
+//     per element with 32-bit indices and a `%` per operand per element.
+#include <hip/hiprtc.h>
+
+#include <cstring>
+#include <sstream>
+#include <unordered_map>
+
+#include "common.hpp"
+#include "kernels/ew_abi.h"
+#include "runtime.hpp"
+
+namespace clove {
+
+namespace {
+
+const char kAbiSrc[] =
+#include "ew_abi.inc"
+    ;
+const char kDeviceSrc[] =
+#include "ew_device.inc"
+    ;
+const char kKernelSrc[] =
+#include "ew_chain_kernel.inc"
+    ;
+
+struct Compiled {
+    hipModule_t module = nullptr;
+    hipFunction_t fn = nullptr;
+};
+
+std::unordered_map<std::string, Compiled> g_cache;
+
+const char *op_fn(int opcode) {
+    switch (opcode) {
+    case CLOVE_OP_ADD: return "cl_add";
+    case CLOVE_OP_SUB: return "cl_sub";
+    case CLOVE_OP_MUL: return "cl_mul";
+    case CLOVE_OP_RELU: return "cl_relu";
+    case CLOVE_OP_GELU: return "cl_gelu";
+    case CLOVE_OP_SIN: return "cl_sin";
+    case CLOVE_OP_COS: return "cl_cos";
+    case CLOVE_OP_SIGMOID: return "cl_sigmoid";
+    case CLOVE_OP_TANH: return "cl_tanh";
+    case CLOVE_OP_RELU_GRAD: return "cl_relu_grad";
+    case CLOVE_OP_GELU_GRAD: return "cl_gelu_grad";
+    case CLOVE_OP_SCALAR_MUL:
+    case CLOVE_OP_DROPOUT: return "cl_scale";
+    default: return nullptr;
+    }
+}
+
+// Granlund-Montgomery magic for 32-bit unsigned division by d >= 1:
+// l = ceil(log2 d), m = floor(2^32 (2^l - d) / d) + 1, shift = l - 1.
+void division_magic(uint64_t d, unsigned int *magic, unsigned int *shift) {
+    if (d <= 1 || d > 0xFFFFFFFFull) {
+        *magic = 0;
+        *shift = 0;
+        return;
+    }
+    unsigned int l = 0;
+    while ((1ull << l) < d) ++l;
+    const uint64_t m = ((1ull << 32) * ((1ull << l) - d)) / d + 1;
+    *magic = (unsigned int)m;
+    *shift = l - 1;
+}
+
+std::string operand_expr(int src) {
+    return src < 0 ? "x[" + std::to_string(-src - 1) + "]" : "n" + std::to_string(src);
+}
+
+std::string generate(const std::vector<ChainOp> &ops, const std::vector<int> &modes, bool wide,
+                     int nout) {
+    std::ostringstream s;
+    const int nin = (int)modes.size();
+    s << "#define CL_NIN " << nin << "\n#define CL_NOUT " << nout << "\n";
+    s << "#include \"ew_device.h\"\n";
+    s << "__device__ __forceinline__ void cl_load_all(const cl_chain_args &a, unsigned long long v, cl_f4 *x) {\n";
+    for (int k = 0; k < nin; ++k)
+        s << "    x[" << k << "] = cl_load4<" << modes[k] << ", " << (wide ? "true" : "false")
+          << ">(a.in[" << k << "], v);\n";
+    s << "}\n";
+    s << "__device__ __forceinline__ void cl_load_all(const cl_chain_args &a, unsigned long long i, float *x) {\n";
+    for (int k = 0; k < nin; ++k)
+        s << "    x[" << k << "] = cl_load1<" << modes[k] << ", " << (wide ? "true" : "false")
+          << ">(a.in[" << k << "], i);\n";
+    s << "}\n";
+    s << "template <typename T>\n__device__ __forceinline__ void cl_body(const T *x, const float *prm, T *y) {\n";
+    int o = 0;
+    for (size_t i = 0; i < ops.size(); ++i) {
+        const ChainOp &op = ops[i];
+        const std::string dst = "n" + std::to_string(i);
+        const std::string a0 = operand_expr(op.src0);
+        switch (op.opcode) {
+        case CLOVE_OP_FLATTEN:
+        case CLOVE_OP_CAST:
+            s << "    const T " << dst << " = " << a0 << ";\n";
+            break;
+        case CLOVE_OP_SCALAR_MUL:
+        case CLOVE_OP_DROPOUT:
+            s << "    const T " << dst << " = cl_scale(" << a0 << ", prm[" << i << "]);\n";
+            break;
+        default:
+            if (ew_arity(op.opcode) == 2)
+                s << "    const T " << dst << " = " << op_fn(op.opcode) << "(" << a0 << ", "
+                  << operand_expr(op.src1) << ");\n";
+            else
+                s << "    const T " << dst << " = " << op_fn(op.opcode) << "(" << a0 << ");\n";
+        }
+        if (op.store || i + 1 == ops.size()) s << "    y[" << o++ << "] = " << dst << ";\n";
+    }
+    s << "    (void)prm;\n}\n#include \"ew_chain_kernel.h\"\n";
+    return s.str();
+}
+
+std::string signature(const std::vector<ChainOp> &ops, const std::vector<int> &modes, bool wide) {
+    std::ostringstream s;
+    for (size_t i = 0; i < ops.size(); ++i)
+        s << ops[i].opcode << '(' << ops[i].src0 << ',' << ops[i].src1 << ')'
+          << ((ops[i].store || i + 1 == ops.size()) ? "s" : "") << ';';
+    s << "|m";
+    for (int m : modes) s << m;
+    s << (wide ? "|w" : "|n");
+    return s.str();
+}
+
+Compiled compile(const std::string &src) {
+    hiprtcProgram prog;
+    const char *headers[] = {kAbiSrc, kDeviceSrc, kKernelSrc};
+    const char *names[] = {"ew_abi.h", "ew_device.h", "ew_chain_kernel.h"};
+    if (hiprtcCreateProgram(&prog, src.c_str(), "clove_chain.hip", 3, headers, names) !=
+        HIPRTC_SUCCESS)
+        fail(CLOVE_HIP_ERR_JIT, "hiprtcCreateProgram failed");
+    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++17",
+                          // packed f32 arithmetic stays off (see the build notes in Makefile)
+                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+    hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        if (n) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        fail(CLOVE_HIP_ERR_JIT, std::string("hipRTC compile failed: ") + log + "\n--- source ---\n" + src);
+    }
+    size_t code_size = 0;
+    hiprtcGetCodeSize(prog, &code_size);
+    std::vector<char> code(code_size);
+    hiprtcGetCode(prog, code.data());
+    hiprtcDestroyProgram(&prog);
+    Compiled c;
+    CLOVE_HIP_CHECK(hipModuleLoadData(&c.module, code.data()));
+    CLOVE_HIP_CHECK(hipModuleGetFunction(&c.fn, c.module, "cl_chain"));
+    return c;
+}
+
+}  // namespace
+
+int ew_arity(int opcode) {
+    switch (opcode) {
+    case CLOVE_OP_ADD:
+    case CLOVE_OP_SUB:
+    case CLOVE_OP_MUL:
+    case CLOVE_OP_RELU_GRAD:
+    case CLOVE_OP_GELU_GRAD:
+        return 2;
+    case CLOVE_OP_SCALAR_MUL:
+    case CLOVE_OP_FLATTEN:
+    case CLOVE_OP_RELU:
+    case CLOVE_OP_GELU:
+    case CLOVE_OP_SIN:
+    case CLOVE_OP_COS:
+    case CLOVE_OP_DROPOUT:
+    case CLOVE_OP_CAST:
+    case CLOVE_OP_SIGMOID:
+    case CLOVE_OP_TANH:
+        return 1;
+    default:
+        return 0;
+    }
+}
+
+void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *> &inputs,
+               const std::vector<Tensor *> &outs, size_t numel) {
+    Context &c = ctx();
+    CLOVE_REQUIRE(!ops.empty(), CLOVE_HIP_ERR_INVALID, "empty chain");
+    CLOVE_REQUIRE((int)ops.size() <= CL_MAX_OPS, CLOVE_HIP_ERR_INVALID,
+                  "chain longer than " + std::to_string(CL_MAX_OPS) + " ops");
+    CLOVE_REQUIRE((int)inputs.size() <= CL_MAX_IN && !inputs.empty(), CLOVE_HIP_ERR_INVALID,
+                  "a chain takes 1.." + std::to_string(CL_MAX_IN) + " inputs");
+    int nstore = 0;
+    for (size_t i = 0; i < ops.size(); ++i) {
+        const ChainOp &op = ops[i];
+        const int ar = ew_arity(op.opcode);
+        CLOVE_REQUIRE(ar > 0, CLOVE_HIP_ERR_INVALID,
+                      "opcode " + std::to_string(op.opcode) + " is not elementwise");
+        const int srcs[2] = {op.src0, op.src1};
+        for (int j = 0; j < ar; ++j) {
+            const int s = srcs[j];
+            CLOVE_REQUIRE(s < (int)i && -s - 1 < (int)inputs.size(), CLOVE_HIP_ERR_INVALID,
+                          "op " + std::to_string(i) + " operand " + std::to_string(s) +
+                              " is neither an earlier op nor an input");
+        }
+        if (op.store || i + 1 == ops.size()) ++nstore;
+    }
+    CLOVE_REQUIRE(nstore == (int)outs.size() && nstore <= CL_MAX_OUT, CLOVE_HIP_ERR_INVALID,
+                  "chain stores " + std::to_string(nstore) + " values but " +
+                      std::to_string(outs.size()) + " outputs were given");
+    if (numel == 0) return;
+
+    const bool wide = numel > 0xFFFFFFFFull;
+    cl_chain_args args;
+    std::memset(&args, 0, sizeof(args));
+    std::vector<int> modes(inputs.size());
+    bool aligned = true;
+    for (size_t k = 0; k < inputs.size(); ++k) {
+        const Tensor *t = inputs[k];
+        CLOVE_REQUIRE(t && t->dtype == CLOVE_HIP_F32, CLOVE_HIP_ERR_INVALID,
+                      "chain input " + std::to_string(k) + " must be an f32 tensor");
+        CLOVE_REQUIRE(t->numel > 0, CLOVE_HIP_ERR_SHAPE,
+                      "chain input " + std::to_string(k) + " is empty");
+        const uint64_t n = t->numel;
+        int m;
+        if (n >= numel) m = CL_BCAST_FULL;
+        else if (n == 1) m = CL_BCAST_SCALAR;
+        else if (n % 4 == 0) m = CL_BCAST_MODVEC;
+        else m = CL_BCAST_MODELEM;
+        modes[k] = m;
+        args.in[k].p = t->f32();
+        args.in[k].n = n;
+        division_magic(n, &args.in[k].magic, &args.in[k].shift);
+        if ((reinterpret_cast<uintptr_t>(t->data) & 15) != 0 &&
+            (m == CL_BCAST_FULL || m == CL_BCAST_MODVEC))
+            aligned = false;
+    }
+    for (size_t o = 0; o < outs.size(); ++o) {
+        CLOVE_REQUIRE(outs[o]->dtype == CLOVE_HIP_F32 && outs[o]->numel >= numel,
+                      CLOVE_HIP_ERR_SHAPE, "chain output too small");
+        args.out[o] = outs[o]->f32();
+        if ((reinterpret_cast<uintptr_t>(outs[o]->data) & 15) != 0) aligned = false;
+    }
+    for (size_t i = 0; i < ops.size(); ++i) {
+        float p = ops[i].param;
+        // Dropout in a fused group scales by 1/(1-rate) computed in f32
+        // (lazy.rs:1795-1803).
+        if (ops[i].opcode == CLOVE_OP_DROPOUT) p = 1.0f / (1.0f - ops[i].param);
+        args.param[i] = p;
+    }
+    args.numel = numel;
+    args.nvec = aligned ? numel / 4 : 0;
+
+    const std::string sig = signature(ops, modes, wide);
+    auto it = g_cache.find(sig);
+    if (it == g_cache.end()) {
+        Compiled comp = compile(generate(ops, modes, wide, nstore));
+        it = g_cache.emplace(sig, comp).first;
+    }
+
+    // Grid: enough 256-thread blocks to cover the vectors once with an
+    // unroll of 4, capped at 32 blocks per CU (a grid-stride loop covers the
+    // rest).
+    const uint64_t per_block = 256ull * 4;
+    uint64_t blocks = (args.nvec + per_block - 1) / per_block;
+    if (blocks == 0) blocks = (numel + 255) / 256;
+    const uint64_t cap = (uint64_t)c.num_cus * 32;
+    if (blocks > cap) blocks = cap;
+    if (blocks == 0) blocks = 1;
+    void *params[] = {&args};
+    CLOVE_HIP_CHECK(hipModuleLaunchKernel(it->second.fn, (unsigned)blocks, 1, 1, 256, 1, 1, 0,
+                                          c.stream, params, nullptr));
+}
+
+void jit_shutdown() {
+    for (auto &kv : g_cache) (void)hipModuleUnload(kv.second.module);
+    g_cache.clear();
+}
+
+int jit_compiled_count() { return (int)g_cache.size(); }
+
+}  // namespace clove

@@ -1,0 +1,237 @@
+// gemm_f32.hip -- C = A.B in f32 on CDNA4 matrix cores.
+//
+// Reference: rayon_matmul (backend.rs:266-287) on the CPU and the 16x16
+// LDS-tiled WGSL kernel (backend.rs:302-343, lazy.rs:4630-4659) on the GPU,
+// which computes one output per thread with two LDS reads per FMA.
+//
+// Here each wavefront owns a WM x WN sub-tile built from 32x32 blocks of
+// v_mfma_f32_32x32x2_f32 (64 cycles per instruction, 4096 FLOP), so one A
+// and one B register feed 4096 FLOP.  A workgroup of four waves owns a
+// BM x BN tile of C.  K advances in slabs of BK staged through LDS with two
+// buffers: while the waves multiply slab s out of one buffer, the global
+// loads of slab s+1 are already in flight and land in the other buffer, so a
+// single barrier per slab orders the two.
+//
+// Operand layout.  v_mfma_f32_32x32x2_f32 reads, in lane l, A[l%32][l/32]
+// and B[l/32][l%32], and returns D[8*(i/4) + 4*(l/32) + i%4][l%32] in
+// accumulator element i.  The sum over k is order-free, so a K-group of 8 is
+// split as k = 8g + 4h + t: lane half h = l/32 supplies the four k values
+// 4h..4h+3 of the group from ONE 16-byte LDS read of A (A is kept row-major
+// in LDS), and MFMA step t (t = 0..3) consumes component t.  B is kept
+// k-major in LDS and read one float per step.
+//
+// Shapes: the fast path needs 16-byte aligned rows (K % 4 == 0 and
+// N % 4 == 0); everything else, and every tile that crosses the edge of C,
+// uses bounds-checked loads that fill zeros.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "launch.hpp"
+
+namespace clove {
+namespace k {
+
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+
+template <int BM, int BN, int BK, int WM, int WN>
+struct GemmCfg {
+    static constexpr int kThreads = 256;
+    static constexpr int kWavesN = BN / WN;
+    static constexpr int kWavesM = BM / WM;
+    static_assert(kWavesM * kWavesN == 4, "four waves per workgroup");
+    static constexpr int kBlocksM = WM / 32;
+    static constexpr int kBlocksN = WN / 32;
+    static constexpr int kPitchA = BK + 4;    // floats; 16-byte aligned, breaks bank aliasing
+    static constexpr int kPitchB = BN + 4;
+    static constexpr int kSizeA = BM * kPitchA;
+    static constexpr int kSizeB = BK * kPitchB;
+    static constexpr int kLoadsA = BM * BK / 4 / kThreads;  // 16-byte loads per thread
+    static constexpr int kLoadsB = BK * BN / 4 / kThreads;
+    static_assert(kLoadsA >= 1 && kLoadsB >= 1, "tile too small for 256 threads");
+    static_assert(BK % 8 == 0, "K slab is a whole number of 8-groups");
+};
+
+// Loads one slab of A (rows m0.., cols k0..) and B (rows k0.., cols n0..)
+// into registers.  EDGE enables bounds checks; VEC selects 16-byte loads
+// (only legal when K % 4 == 0 and N % 4 == 0).
+template <class C, int BK, int BN, bool EDGE, bool VEC>
+__device__ __forceinline__ void load_slab(const float *__restrict__ A, const float *__restrict__ B,
+                                          int M, int N, int K, int m0, int n0, int k0, f4 *ra,
+                                          f4 *rb) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::kLoadsA; ++i) {
+        const int idx = tid + i * C::kThreads;
+        const int r = idx / (BK / 4), kq = idx % (BK / 4);
+        const int gm = m0 + r, gk = k0 + 4 * kq;
+        const float *p = A + (size_t)gm * K + gk;
+        if (!EDGE) {
+            ra[i] = *reinterpret_cast<const f4 *>(p);
+        } else if (VEC) {
+            ra[i] = (gm < M && gk < K) ? *reinterpret_cast<const f4 *>(p) : (f4){0.f, 0.f, 0.f, 0.f};
+        } else {
+            f4 v;
+            v.x = (gm < M && gk + 0 < K) ? p[0] : 0.f;
+            v.y = (gm < M && gk + 1 < K) ? p[1] : 0.f;
+            v.z = (gm < M && gk + 2 < K) ? p[2] : 0.f;
+            v.w = (gm < M && gk + 3 < K) ? p[3] : 0.f;
+            ra[i] = v;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < C::kLoadsB; ++i) {
+        const int idx = tid + i * C::kThreads;
+        const int r = idx / (BN / 4), nq = idx % (BN / 4);
+        const int gk = k0 + r, gn = n0 + 4 * nq;
+        const float *p = B + (size_t)gk * N + gn;
+        if (!EDGE) {
+            rb[i] = *reinterpret_cast<const f4 *>(p);
+        } else if (VEC) {
+            rb[i] = (gk < K && gn < N) ? *reinterpret_cast<const f4 *>(p) : (f4){0.f, 0.f, 0.f, 0.f};
+        } else {
+            f4 v;
+            v.x = (gk < K && gn + 0 < N) ? p[0] : 0.f;
+            v.y = (gk < K && gn + 1 < N) ? p[1] : 0.f;
+            v.z = (gk < K && gn + 2 < N) ? p[2] : 0.f;
+            v.w = (gk < K && gn + 3 < N) ? p[3] : 0.f;
+            rb[i] = v;
+        }
+    }
+}
+
+template <class C, int BK, int BN>
+__device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, const f4 *rb) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < C::kLoadsA; ++i) {
+        const int idx = tid + i * C::kThreads;
+        const int r = idx / (BK / 4), kq = idx % (BK / 4);
+        *reinterpret_cast<f4 *>(sA + r * C::kPitchA + 4 * kq) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < C::kLoadsB; ++i) {
+        const int idx = tid + i * C::kThreads;
+        const int r = idx / (BN / 4), nq = idx % (BN / 4);
+        *reinterpret_cast<f4 *>(sB + r * C::kPitchB + 4 * nq) = rb[i];
+    }
+}
+
+template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC>
+__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float *__restrict__ A,
+                                                            const float *__restrict__ B,
+                                                            float *__restrict__ C, int M, int N,
+                                                            int K, int tiles_n) {
+    using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
+    __shared__ __attribute__((aligned(16))) float smem[2 * (Cfg::kSizeA + Cfg::kSizeB)];
+
+    const int tile = blockIdx.x;
+    const int m0 = (tile / tiles_n) * BM;
+    const int n0 = (tile % tiles_n) * BN;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm0 = (wave / Cfg::kWavesN) * WM;
+    const int wn0 = (wave % Cfg::kWavesN) * WN;
+    const int l32 = lane & 31;
+    const int h = lane >> 5;
+
+    f16v acc[Cfg::kBlocksM][Cfg::kBlocksN];
+#pragma unroll
+    for (int i = 0; i < Cfg::kBlocksM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::kBlocksN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    f4 ra[Cfg::kLoadsA], rb[Cfg::kLoadsB];
+    const int slabs = (K + BK - 1) / BK;
+
+    load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, 0, ra, rb);
+    store_slab<Cfg, BK, BN>(smem, smem + Cfg::kSizeA, ra, rb);
+    __syncthreads();
+
+    for (int s = 0; s < slabs; ++s) {
+        float *sA = smem + (s & 1) * (Cfg::kSizeA + Cfg::kSizeB);
+        float *sB = sA + Cfg::kSizeA;
+        const bool more = s + 1 < slabs;
+        if (more) load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, (s + 1) * BK, ra, rb);
+
+#pragma unroll
+        for (int g = 0; g < BK / 8; ++g) {
+            f4 a[Cfg::kBlocksM];
+            float b[Cfg::kBlocksN][4];
+#pragma unroll
+            for (int i = 0; i < Cfg::kBlocksM; ++i)
+                a[i] = *reinterpret_cast<const f4 *>(sA + (wm0 + 32 * i + l32) * Cfg::kPitchA +
+                                                     8 * g + 4 * h);
+#pragma unroll
+            for (int j = 0; j < Cfg::kBlocksN; ++j)
+#pragma unroll
+                for (int t = 0; t < 4; ++t)
+                    b[j][t] = sB[(8 * g + 4 * h + t) * Cfg::kPitchB + wn0 + 32 * j + l32];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+#pragma unroll
+                for (int i = 0; i < Cfg::kBlocksM; ++i)
+#pragma unroll
+                    for (int j = 0; j < Cfg::kBlocksN; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i][t], b[j][t],
+                                                                         acc[i][j], 0, 0, 0);
+        }
+
+        if (more) {
+            float *nA = smem + ((s + 1) & 1) * (Cfg::kSizeA + Cfg::kSizeB);
+            store_slab<Cfg, BK, BN>(nA, nA + Cfg::kSizeA, ra, rb);
+        }
+        __syncthreads();
+    }
+
+    // Epilogue: accumulator element e of block (i, j) is C[row][col] with
+    // row = 8*(e/4) + 4*h + e%4 and col = l%32 inside the 32x32 block.
+#pragma unroll
+    for (int i = 0; i < Cfg::kBlocksM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::kBlocksN; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
+                const int col = n0 + wn0 + 32 * j + l32;
+                if (!EDGE || (row < M && col < N)) C[(size_t)row * N + col] = acc[i][j][e];
+            }
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+void launch_cfg(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s) {
+    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+    const bool vec = (K % 4 == 0) && (N % 4 == 0) &&
+                     ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) == 0;
+    const bool interior = vec && (M % BM == 0) && (N % BN == 0) && (K % BK == 0);
+    const dim3 grid((unsigned)(tm * tn));
+    if (interior)
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
+    else if (vec)
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
+    else
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
+}
+
+}  // namespace
+
+void gemm_f32(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s) {
+    if (M <= 0 || N <= 0) return;
+    if (K <= 0) {
+        (void)hipMemsetAsync(C, 0, (size_t)M * N * sizeof(float), s);
+        return;
+    }
+    if (M <= 64)
+        launch_cfg<64, 64, 16, 32, 32>(A, B, C, M, N, K, s);
+    else
+        launch_cfg<128, 128, 16, 64, 64>(A, B, C, M, N, K, s);
+}
+
+}  // namespace k
+}  // namespace clove

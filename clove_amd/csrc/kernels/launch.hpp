@@ -1,0 +1,54 @@
+// launch.hpp -- host-side launchers of the ahead-of-time gfx950 kernels.
+// Each launcher validates nothing: shape checks happen in ops.cpp before a
+// launcher is called, so every launcher assumes its arguments are in range.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace clove {
+namespace k {
+
+// fill.hip -- seeded synthetic data (counter-based splitmix64 stream).
+void fill_normal(float *p, size_t n, uint64_t seed, float mean, float stddev, hipStream_t s);
+void fill_uniform(float *p, size_t n, uint64_t seed, float lo, float hi, hipStream_t s);
+
+// rowwise.hip -- one wavefront per row, the row held in registers.
+void softmax_rows(const float *x, float *y, size_t rows, size_t cols, hipStream_t s);
+void layer_norm_rows(const float *x, const float *gamma, const float *beta, float *y,
+                     size_t rows, size_t cols, float eps, hipStream_t s);
+
+// gemm_f32.hip -- C[M,N] = A[M,K] . B[K,N], row-major f32, MFMA f32 accumulate.
+void gemm_f32(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s);
+
+// paged_attention.hip
+struct PagedArgs {
+    const float *q;        // [B, H, D]
+    const float *k_new;    // [B, H, D] or nullptr
+    const float *v_new;    // [B, H, D] or nullptr
+    const float *k_cache;  // [num_blocks, block_size, H, D]
+    const float *v_cache;  // [num_blocks, block_size, H, D]
+    const int32_t *block_tables;  // [B, max_blocks]
+    const int32_t *context_lens;  // [B]
+    float *out;            // [B, H, D]
+    float *partials;       // workspace: [B, H, max_parts, D + 2]
+    int32_t *err_flag;     // set to 1 when a table entry used lies outside the pool
+    int64_t num_blocks;    // blocks in the pool (bounds for table entries)
+    int num_seqs, num_heads, head_dim, block_size, max_blocks, max_parts;
+    int part_tokens;       // tokens per partition (multiple of block_size)
+    float scale;
+};
+// Workspace floats needed for a given shape (0 when one partition suffices).
+size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max_ctx,
+                              int part_tokens);
+int paged_part_tokens(int head_dim, int block_size);
+// Head dims 64/128/256 and block sizes 8/16/32 have kernels.
+bool paged_supported(int head_dim, int block_size);
+void paged_attention(const PagedArgs &a, hipStream_t s);
+void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,
+                 int num_seqs, int max_blocks, int block_size, int max_ctx, hipStream_t s);
+
+}  // namespace k
+}  // namespace clove

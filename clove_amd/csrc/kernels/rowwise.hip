@@ -1,0 +1,202 @@
+// rowwise.hip -- row softmax and row layer norm.
+//
+// Reference: the CPU kernels (softmax backend.rs:2102-2125, layer_norm
+// backend.rs:2380-2405) and the lazy WGSL (lazy.rs:4718-4737, 4786-4806),
+// which runs ONE THREAD PER ROW and reads each row three times with a 16 KiB
+// stride between neighbouring threads.
+//
+// Here a whole wavefront owns a row: lanes read 16-byte vectors so a wave
+// instruction covers 1 KiB of contiguous row, the row stays in VGPRs between
+// the passes (so HBM sees exactly one read and one write per element), and
+// the max / sum / mean / variance reductions are wave64 butterflies with no
+// LDS and no barriers.  Rows whose width is not a multiple of 4, or wider
+// than 8192, go through a looped wave-per-row kernel that re-reads the row.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "launch.hpp"
+#include "wave.h"
+
+namespace clove {
+namespace k {
+
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // one row per wave, 4 waves per block
+
+template <int VPT>
+__global__ void __launch_bounds__(256) softmax_wave_kernel(const float *__restrict__ x,
+                                                           float *__restrict__ y, int rows,
+                                                           int cols) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nvec = cols >> 2;
+    const cl_f4 *xr = reinterpret_cast<const cl_f4 *>(x + row * (long)cols);
+    cl_f4 *yr = reinterpret_cast<cl_f4 *>(y + row * (long)cols);
+    cl_f4 v[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < nvec ? __builtin_nontemporal_load(xr + c)
+                        : (cl_f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) m = fmaxf(m, hmax4(v[i]));
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        if (lane + 64 * i < nvec) {
+            v[i] = (cl_f4){expf(v[i].x - m), expf(v[i].y - m), expf(v[i].z - m), expf(v[i].w - m)};
+            s += hsum4(v[i]);
+        }
+    }
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nvec) __builtin_nontemporal_store(v[i] / s, yr + c);
+    }
+}
+
+template <int VPT>
+__global__ void __launch_bounds__(256) layer_norm_wave_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ gamma,
+                                                              const float *__restrict__ beta,
+                                                              float *__restrict__ y, int rows,
+                                                              int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nvec = cols >> 2;
+    const cl_f4 *xr = reinterpret_cast<const cl_f4 *>(x + row * (long)cols);
+    cl_f4 *yr = reinterpret_cast<cl_f4 *>(y + row * (long)cols);
+    const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(gamma);
+    const cl_f4 *b4 = reinterpret_cast<const cl_f4 *>(beta);
+    cl_f4 v[VPT];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < nvec ? __builtin_nontemporal_load(xr + c) : (cl_f4){0.f, 0.f, 0.f, 0.f};
+        s += hsum4(v[i]);
+    }
+    const float n = (float)cols;
+    const float mean = wave_sum(s) / n;
+    float q = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        if (lane + 64 * i < nvec) {
+            const cl_f4 d = v[i] - mean;
+            q += hsum4(d * d);
+        }
+    }
+    const float var = wave_sum(q) / n;
+    const float sd = sqrtf(var + eps);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nvec) {
+            const cl_f4 o = ((v[i] - mean) / sd) * g4[c] + b4[c];
+            __builtin_nontemporal_store(o, yr + c);
+        }
+    }
+}
+
+// Any width: one wave per row, the row re-read from memory on each pass.
+__global__ void __launch_bounds__(256) softmax_loop_kernel(const float *__restrict__ x,
+                                                           float *__restrict__ y, int rows,
+                                                           int cols) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * (long)cols;
+    float *yr = y + row * (long)cols;
+    // pass 1: running (max, sum of exp) per lane, then merged across lanes
+    float m = -INFINITY, s = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        const float xv = xr[c];
+        const float nm = fmaxf(m, xv);
+        s = (m == -INFINITY ? 0.0f : s * expf(m - nm)) + expf(xv - nm);
+        m = nm;
+    }
+    const float gm = wave_max(m);
+    s = (m == -INFINITY) ? 0.0f : s * expf(m - gm);
+    s = wave_sum(s);
+    for (int c = lane; c < cols; c += 64) yr[c] = expf(xr[c] - gm) / s;
+}
+
+__global__ void __launch_bounds__(256) layer_norm_loop_kernel(const float *__restrict__ x,
+                                                              const float *__restrict__ gamma,
+                                                              const float *__restrict__ beta,
+                                                              float *__restrict__ y, int rows,
+                                                              int cols, float eps) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *xr = x + row * (long)cols;
+    float *yr = y + row * (long)cols;
+    const float n = (float)cols;
+    float s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s += xr[c];
+    const float mean = wave_sum(s) / n;
+    float q = 0.0f;
+    for (int c = lane; c < cols; c += 64) {
+        const float d = xr[c] - mean;
+        q += d * d;
+    }
+    const float sd = sqrtf(wave_sum(q) / n + eps);
+    for (int c = lane; c < cols; c += 64) yr[c] = ((xr[c] - mean) / sd) * gamma[c] + beta[c];
+}
+
+int pick_vpt(int cols) {
+    if (cols % 4 != 0) return 0;
+    const int need = (cols / 4 + 63) / 64;
+    int v = 1;
+    while (v < need) v <<= 1;
+    return v <= 32 ? v : 0;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+void softmax_rows(const float *x, float *y, size_t rows, size_t cols, hipStream_t s) {
+    if (!rows || !cols) return;
+    const unsigned grid = (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int r = (int)rows, c = (int)cols;
+    const int vpt = (aligned16(x) && aligned16(y)) ? pick_vpt(c) : 0;
+    switch (vpt) {
+    case 1: softmax_wave_kernel<1><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    case 2: softmax_wave_kernel<2><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    case 4: softmax_wave_kernel<4><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    case 8: softmax_wave_kernel<8><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    case 16: softmax_wave_kernel<16><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    case 32: softmax_wave_kernel<32><<<grid, 256, 0, s>>>(x, y, r, c); break;
+    default: softmax_loop_kernel<<<grid, 256, 0, s>>>(x, y, r, c); break;
+    }
+}
+
+void layer_norm_rows(const float *x, const float *gamma, const float *beta, float *y,
+                     size_t rows, size_t cols, float eps, hipStream_t s) {
+    if (!rows || !cols) return;
+    const unsigned grid = (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int r = (int)rows, c = (int)cols;
+    const bool al = aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
+    const int vpt = al ? pick_vpt(c) : 0;
+    switch (vpt) {
+    case 1: layer_norm_wave_kernel<1><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 2: layer_norm_wave_kernel<2><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 4: layer_norm_wave_kernel<4><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 8: layer_norm_wave_kernel<8><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 16: layer_norm_wave_kernel<16><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 32: layer_norm_wave_kernel<32><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    default: layer_norm_loop_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    }
+}
+
+}  // namespace k
+}  // namespace clove

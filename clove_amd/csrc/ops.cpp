@@ -1,0 +1,273 @@
+// ops.cpp -- the eager HIP backend: the hot-path methods of Clove's
+// `trait Backend` (backend.rs:171-257) with the shape rules of WgpuBackend,
+// lowered to the gfx950 kernels.  Every op allocates its output through the
+// caching allocator and enqueues its kernels on the context stream; nothing
+// here synchronises.
+//
+// Elementwise ops run as one-op fused chains (jit.cpp), the same kernels the
+// lazy planner emits for longer chains, so eager and fused results are
+// produced by identical device code.
+#include <cmath>
+
+#include "common.hpp"
+#include "kernels/launch.hpp"
+#include "runtime.hpp"
+
+namespace clove {
+
+namespace {
+
+const Tensor &need(const TensorNode &t, const char *what) {
+    CLOVE_REQUIRE(t != nullptr, CLOVE_HIP_ERR_INVALID, std::string(what) + " is NULL");
+    return *t;
+}
+
+void need_f32(const Tensor &t, const char *what) {
+    CLOVE_REQUIRE(t.dtype == CLOVE_HIP_F32, CLOVE_HIP_ERR_INVALID,
+                  std::string(what) + " must be an f32 tensor");
+}
+
+}  // namespace
+
+TensorNode HipBackend::new_cpu(const float *data, const std::vector<size_t> &shape) {
+    TensorNode t = new_tensor(shape, CLOVE_HIP_F32);
+    if (data) upload(*t, data, 0, t->numel);
+    return t;
+}
+
+// backend.rs:1483-1493 (add), :1748-1758 (sub), :1598-1617 (mul): the output
+// has a's shape and b is read as b[i % numel(b)].
+TensorNode HipBackend::binary(int opcode, const TensorNode &a_, const TensorNode &b_) {
+    const Tensor &a = need(a_, "a");
+    const Tensor &b = need(b_, "b");
+    need_f32(a, "a");
+    need_f32(b, "b");
+    CLOVE_REQUIRE(b.numel > 0 || a.numel == 0, CLOVE_HIP_ERR_SHAPE,
+                  "broadcast operand b is empty");
+    TensorNode out = new_tensor(a.shape, CLOVE_HIP_F32);
+    if (a.numel == 0) return out;
+    ChainOp op;
+    op.opcode = opcode;
+    op.src0 = -1;
+    op.src1 = -2;
+    run_chain({op}, {&a, &b}, {out.get()}, a.numel);
+    return out;
+}
+
+TensorNode HipBackend::unary(int opcode, const TensorNode &a_, float param) {
+    const Tensor &a = need(a_, "a");
+    need_f32(a, "a");
+    TensorNode out = new_tensor(a.shape, CLOVE_HIP_F32);
+    if (a.numel == 0) return out;
+    ChainOp op;
+    op.opcode = opcode;
+    op.src0 = -1;
+    op.param = param;
+    run_chain({op}, {&a}, {out.get()}, a.numel);
+    return out;
+}
+
+TensorNode HipBackend::add(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_ADD, a, b); }
+TensorNode HipBackend::sub(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_SUB, a, b); }
+TensorNode HipBackend::mul(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_MUL, a, b); }
+TensorNode HipBackend::mul_scalar(const TensorNode &a, float s) { return unary(CLOVE_OP_SCALAR_MUL, a, s); }
+TensorNode HipBackend::relu(const TensorNode &a) { return unary(CLOVE_OP_RELU, a); }
+TensorNode HipBackend::gelu(const TensorNode &a) { return unary(CLOVE_OP_GELU, a); }
+TensorNode HipBackend::sigmoid(const TensorNode &a) { return unary(CLOVE_OP_SIGMOID, a); }
+TensorNode HipBackend::tanh(const TensorNode &a) { return unary(CLOVE_OP_TANH, a); }
+TensorNode HipBackend::sin(const TensorNode &a) { return unary(CLOVE_OP_SIN, a); }
+TensorNode HipBackend::cos(const TensorNode &a) { return unary(CLOVE_OP_COS, a); }
+
+// ---- row reductions --------------------------------------------------------
+
+static void row_dims(const Tensor &a, size_t *rows, size_t *cols) {
+    CLOVE_REQUIRE(!a.shape.empty(), CLOVE_HIP_ERR_SHAPE, "row op needs at least 1 dimension");
+    *cols = a.shape.back();
+    *rows = *cols ? a.numel / *cols : 0;
+    CLOVE_REQUIRE(*rows < (1ull << 31) && *cols < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "row op dimensions exceed 2^31");
+}
+
+void HipBackend::softmax_into(const Tensor &a, Tensor &out) {
+    need_f32(a, "a");
+    size_t rows, cols;
+    row_dims(a, &rows, &cols);
+    k::softmax_rows(a.f32(), out.f32(), rows, cols, ctx().stream);
+}
+
+// backend.rs:2102-2125: rows = shape[0], cols = shape[1]; here the last
+// dimension is the row, which is the same thing for the 2-d tensors Clove
+// passes and extends it to N-d.
+TensorNode HipBackend::softmax(const TensorNode &a_) {
+    const Tensor &a = need(a_, "a");
+    TensorNode out = new_tensor(a.shape, CLOVE_HIP_F32);
+    softmax_into(a, *out);
+    return out;
+}
+
+void HipBackend::layer_norm_into(const Tensor &a, const Tensor &g, const Tensor &b, Tensor &out) {
+    need_f32(a, "a");
+    need_f32(g, "gamma");
+    need_f32(b, "beta");
+    size_t rows, cols;
+    row_dims(a, &rows, &cols);
+    // backend.rs:2401-2403 indexes gamma[j] and beta[j] for j < cols.
+    CLOVE_REQUIRE(g.numel >= cols && b.numel >= cols, CLOVE_HIP_ERR_SHAPE,
+                  "gamma/beta need at least " + std::to_string(cols) + " elements");
+    k::layer_norm_rows(a.f32(), g.f32(), b.f32(), out.f32(), rows, cols, 1e-5f, ctx().stream);
+}
+
+TensorNode HipBackend::layer_norm(const TensorNode &a_, const TensorNode &g_, const TensorNode &b_) {
+    const Tensor &a = need(a_, "a");
+    TensorNode out = new_tensor(a.shape, CLOVE_HIP_F32);
+    layer_norm_into(a, need(g_, "gamma"), need(b_, "beta"), *out);
+    return out;
+}
+
+// ---- matmul ------------------------------------------------------------------
+
+static void matmul_dims(const Tensor &a, const Tensor &b, size_t *m, size_t *k, size_t *n) {
+    CLOVE_REQUIRE(!a.shape.empty(), CLOVE_HIP_ERR_SHAPE, "matmul: a needs at least 1 dimension");
+    CLOVE_REQUIRE(b.shape.size() == 2, CLOVE_HIP_ERR_SHAPE,
+                  "matmul: b must be 2-d, got " + shape_str(b.shape));
+    *k = a.shape.back();
+    *m = 1;
+    for (size_t i = 0; i + 1 < a.shape.size(); ++i) *m *= a.shape[i];
+    *n = b.shape[1];
+    CLOVE_REQUIRE(b.shape[0] == *k, CLOVE_HIP_ERR_SHAPE,
+                  "matmul: inner dimensions differ, a " + shape_str(a.shape) + " b " +
+                      shape_str(b.shape));
+    CLOVE_REQUIRE(*m < (1ull << 31) && *n < (1ull << 31) && *k < (1ull << 31),
+                  CLOVE_HIP_ERR_SHAPE, "matmul dimensions exceed 2^31");
+}
+
+void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out) {
+    need_f32(a, "a");
+    need_f32(b, "b");
+    size_t m, kk, n;
+    matmul_dims(a, b, &m, &kk, &n);
+    k::gemm_f32(a.f32(), b.f32(), out.f32(), (int)m, (int)n, (int)kk, ctx().stream);
+}
+
+// backend.rs:1282-1306: m = prod(a.shape[..last]), k = a.shape[last],
+// n = b.shape[1]; the output keeps a's leading dims with the last set to n.
+TensorNode HipBackend::matmul(const TensorNode &a_, const TensorNode &b_) {
+    const Tensor &a = need(a_, "a");
+    const Tensor &b = need(b_, "b");
+    size_t m, kk, n;
+    matmul_dims(a, b, &m, &kk, &n);
+    std::vector<size_t> shape = a.shape;
+    shape.back() = n;
+    TensorNode out = new_tensor(shape, CLOVE_HIP_F32);
+    matmul_into(a, b, *out);
+    return out;
+}
+
+// ---- paged attention -----------------------------------------------------------
+
+void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const Tensor *vn,
+                                      const Tensor &kv, const Tensor &bt, const Tensor &cl,
+                                      float scale, Tensor &out) {
+    need_f32(q, "q");
+    need_f32(kv, "kv_cache");
+    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
+                  "block_tables and context_lens must be int32 tensors");
+    CLOVE_REQUIRE(kv.shape.size() == 5 && kv.shape[0] == 2, CLOVE_HIP_ERR_SHAPE,
+                  "kv_cache must be [2, num_blocks, block_size, heads, head_dim], got " +
+                      shape_str(kv.shape));
+    const size_t nb = kv.shape[1], bs = kv.shape[2], H = kv.shape[3], D = kv.shape[4];
+    CLOVE_REQUIRE(k::paged_supported((int)D, (int)bs), CLOVE_HIP_ERR_SHAPE,
+                  "paged attention supports head_dim 64/128/256 and block_size 8/16/32, got " +
+                      std::to_string(D) + "/" + std::to_string(bs));
+    const size_t B = cl.numel;
+    CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == B, CLOVE_HIP_ERR_SHAPE,
+                  "block_tables must be [num_seqs, max_blocks] with num_seqs = numel(context_lens)");
+    const size_t max_blocks = bt.shape[1];
+    CLOVE_REQUIRE(q.numel == B * H * D, CLOVE_HIP_ERR_SHAPE,
+                  "q must hold num_seqs*heads*head_dim = " + std::to_string(B * H * D) +
+                      " elements, got " + std::to_string(q.numel));
+    CLOVE_REQUIRE((kn == nullptr) == (vn == nullptr), CLOVE_HIP_ERR_INVALID,
+                  "pass both k and v, or neither");
+    if (kn) {
+        need_f32(*kn, "k");
+        need_f32(*vn, "v");
+        CLOVE_REQUIRE(kn->numel == q.numel && vn->numel == q.numel, CLOVE_HIP_ERR_SHAPE,
+                      "k and v must have q's number of elements");
+    }
+    CLOVE_REQUIRE(out.numel >= q.numel, CLOVE_HIP_ERR_SHAPE, "output too small");
+    CLOVE_REQUIRE(max_blocks * bs < (1ull << 31) && nb * bs < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "context capacity exceeds 2^31 tokens");
+    if (B == 0) return;
+    Context &c = ctx();
+
+    k::PagedArgs a{};
+    a.q = q.f32();
+    a.k_new = kn ? kn->f32() : nullptr;
+    a.v_new = vn ? vn->f32() : nullptr;
+    a.k_cache = kv.f32();
+    a.v_cache = kv.f32() + nb * bs * H * D;
+    a.block_tables = bt.i32();
+    a.context_lens = cl.i32();
+    a.out = out.f32();
+    a.err_flag = device_error_flag();
+    a.num_blocks = (int64_t)nb;
+    a.num_seqs = (int)B;
+    a.num_heads = (int)H;
+    a.head_dim = (int)D;
+    a.block_size = (int)bs;
+    a.max_blocks = (int)max_blocks;
+    a.part_tokens = k::paged_part_tokens((int)D, (int)bs);
+    const int cap = (int)(max_blocks * bs);
+    a.max_parts = std::max(1, (cap + a.part_tokens - 1) / a.part_tokens);
+    a.scale = scale;
+    const size_t ws = k::paged_workspace_floats((int)B, (int)H, (int)D, cap, a.part_tokens);
+    TensorNode work;
+    if (ws) {
+        work = new_tensor({ws}, CLOVE_HIP_F32);
+        a.partials = work->f32();
+    }
+    k::paged_attention(a, c.stream);
+    // `work` returns to the allocator here; later users of the block are
+    // ordered after these kernels on the same stream.
+}
+
+TensorNode HipBackend::paged_attention(const TensorNode &q_, const TensorNode &k_,
+                                       const TensorNode &v_, const TensorNode &kv_,
+                                       const TensorNode &bt_, const TensorNode &cl_, float scale) {
+    const Tensor &q = need(q_, "q");
+    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
+    paged_attention_into(q, k_.get(), v_.get(), need(kv_, "kv_cache"), need(bt_, "block_tables"),
+                         need(cl_, "context_lens"), scale, *out);
+    return out;
+}
+
+TensorNode HipBackend::paged_gather_indices(const TensorNode &bt_, const TensorNode &cl_,
+                                            int block_size, int max_ctx) {
+    const Tensor &bt = need(bt_, "block_tables");
+    const Tensor &cl = need(cl_, "context_lens");
+    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
+                  "block_tables and context_lens must be int32 tensors");
+    CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == cl.numel, CLOVE_HIP_ERR_SHAPE,
+                  "block_tables must be [num_seqs, max_blocks]");
+    CLOVE_REQUIRE(block_size > 0 && max_ctx >= 0, CLOVE_HIP_ERR_INVALID,
+                  "block_size must be > 0 and max_ctx >= 0");
+    const size_t B = cl.numel;
+    TensorNode out = new_tensor({B, (size_t)max_ctx}, CLOVE_HIP_I32);
+    k::paged_slots(bt.i32(), cl.i32(), out->i32(), (int)B, (int)bt.shape[1], block_size, max_ctx,
+                   ctx().stream);
+    return out;
+}
+
+// ---- synthetic data -----------------------------------------------------------
+
+void fill_normal(Tensor &t, uint64_t seed, float mean, float stddev) {
+    need_f32(t, "tensor");
+    k::fill_normal(t.f32(), t.numel, seed, mean, stddev, ctx().stream);
+}
+
+void fill_uniform(Tensor &t, uint64_t seed, float lo, float hi) {
+    need_f32(t, "tensor");
+    k::fill_uniform(t.f32(), t.numel, seed, lo, hi, ctx().stream);
+}
+
+}  // namespace clove

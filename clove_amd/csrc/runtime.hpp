@@ -1,0 +1,92 @@
+// runtime.hpp -- context lifecycle, transfers and events (runtime.cpp), and
+// the entry points of the fused-chain JIT (jit.cpp), the eager backend
+// (ops.cpp) and the lazy planner (graph.cpp).
+#pragma once
+
+#include <string>
+#include <vector>
+
+#include "common.hpp"
+
+namespace clove {
+
+const std::string &last_error();
+void init(int device);
+void shutdown();
+void synchronize();
+void set_stream(void *s);
+int32_t *device_error_flag();
+
+void upload(Tensor &t, const void *src, size_t offset, size_t count);
+void download(const Tensor &t, void *dst, size_t offset, size_t count);
+
+int event_record();
+float event_elapsed(int a, int b);
+void event_reset();
+
+void fill_normal(Tensor &t, uint64_t seed, float mean, float stddev);
+void fill_uniform(Tensor &t, uint64_t seed, float lo, float hi);
+
+// ---- fused elementwise chains (jit.cpp) ----------------------------------
+
+// One op of a chain; operands >= 0 name earlier ops, < 0 name input -(x+1).
+struct ChainOp {
+    int opcode;
+    int src0 = 0, src1 = 0;
+    bool store = false;
+    float param = 0.f;
+};
+
+// Number of operands an elementwise opcode reads (1 or 2); 0 if the opcode
+// is not elementwise.
+int ew_arity(int opcode);
+
+// Evaluates `ops` over the index space [0, numel) and writes the stored ops
+// into `outs` (one pre-allocated f32 tensor of at least numel elements per
+// stored op, in op order).
+void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *> &inputs,
+               const std::vector<Tensor *> &outs, size_t numel);
+void jit_shutdown();
+// Diagnostics for tests: number of chains compiled so far.
+int jit_compiled_count();
+
+// ---- eager backend (ops.cpp): mirrors trait Backend (backend.rs:171-257) --
+
+struct HipBackend {
+    static TensorNode new_cpu(const float *data, const std::vector<size_t> &shape);
+    static TensorNode binary(int opcode, const TensorNode &a, const TensorNode &b);
+    static TensorNode unary(int opcode, const TensorNode &a, float param = 0.f);
+    static TensorNode add(const TensorNode &a, const TensorNode &b);
+    static TensorNode sub(const TensorNode &a, const TensorNode &b);
+    static TensorNode mul(const TensorNode &a, const TensorNode &b);
+    static TensorNode mul_scalar(const TensorNode &a, float s);
+    static TensorNode relu(const TensorNode &a);
+    static TensorNode gelu(const TensorNode &a);
+    static TensorNode sigmoid(const TensorNode &a);
+    static TensorNode tanh(const TensorNode &a);
+    static TensorNode sin(const TensorNode &a);
+    static TensorNode cos(const TensorNode &a);
+    static TensorNode softmax(const TensorNode &a);
+    static TensorNode layer_norm(const TensorNode &a, const TensorNode &gamma,
+                                 const TensorNode &beta);
+    static TensorNode matmul(const TensorNode &a, const TensorNode &b);
+    static TensorNode paged_attention(const TensorNode &q, const TensorNode &k,
+                                      const TensorNode &v, const TensorNode &kv_cache,
+                                      const TensorNode &block_tables,
+                                      const TensorNode &context_lens, float scale);
+    static TensorNode paged_gather_indices(const TensorNode &block_tables,
+                                           const TensorNode &context_lens, int block_size,
+                                           int max_ctx);
+
+    // Launch-only forms writing into caller-provided outputs (used by the
+    // planner, whose buffers are pre-assigned).
+    static void softmax_into(const Tensor &a, Tensor &out);
+    static void layer_norm_into(const Tensor &a, const Tensor &gamma, const Tensor &beta,
+                                Tensor &out);
+    static void matmul_into(const Tensor &a, const Tensor &b, Tensor &out);
+    static void paged_attention_into(const Tensor &q, const Tensor *k, const Tensor *v,
+                                     const Tensor &kv_cache, const Tensor &block_tables,
+                                     const Tensor &context_lens, float scale, Tensor &out);
+};
+
+}  // namespace clove

@@ -1,0 +1,242 @@
+/*
+ * clove_hip.h -- C ABI of the MI355X (gfx950) backend for Clove's hot path.
+ *
+ * This is the drop-in boundary: a Rust `impl Backend for HipBackend` (or any
+ * other FFI caller) binds these symbols the way Clove's own C bridge binds
+ * `WgpuBackend` (reference src/ffi.rs).  Every entry takes plain pointers,
+ * sizes and opaque handles; no C++ or torch types cross it.
+ *
+ * Conventions
+ *   - A CTensor is an opaque handle to one device allocation (f32 or int32)
+ *     plus its shape, mirroring ffi.rs:35 `pub type CTensor = *mut c_void`.
+ *   - Ops return a NEW handle that the caller frees with clove_hip_tensor_free
+ *     (ffi.rs:119-266).  On any error they return NULL and record a message
+ *     for clove_hip_last_error(); functions returning int return 0 (CLOVE_HIP_OK)
+ *     or a CLOVE_HIP_ERR_* code.  The reference aborts on errors (panic with
+ *     panic = "abort", Cargo.toml:43); status codes replace that.
+ *   - All device work is ordered on ONE HIP stream.  Ops only enqueue work;
+ *     clove_hip_tensor_data / clove_hip_tensor_read / clove_hip_synchronize
+ *     are the synchronisation points (the counterpart of to_cpu,
+ *     backend.rs:1056-1090).
+ *   - The API is thread-safe: one global lock orders host-side calls.
+ */
+#ifndef CLOVE_HIP_H
+#define CLOVE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *CTensor;                       /* ffi.rs:35 */
+typedef struct clove_hip_graph clove_hip_graph; /* lazy.rs:30-33 GLOBAL_GRAPH, made explicit */
+typedef struct clove_hip_model clove_hip_model; /* lazy.rs:2545 CompiledModel */
+
+enum clove_hip_status {
+    CLOVE_HIP_OK = 0,
+    CLOVE_HIP_ERR_INVALID = 1,   /* null handle / bad argument */
+    CLOVE_HIP_ERR_SHAPE = 2,     /* shapes do not satisfy the op's rule */
+    CLOVE_HIP_ERR_HIP = 3,       /* a HIP runtime call failed */
+    CLOVE_HIP_ERR_JIT = 4,       /* runtime compilation of a fused chain failed */
+    CLOVE_HIP_ERR_OOM = 5,       /* device allocation failed */
+    CLOVE_HIP_ERR_NOT_INIT = 6,  /* clove_hip_init was not called */
+    CLOVE_HIP_ERR_RANGE = 7      /* an index (block table, context length) is out of range */
+};
+
+enum clove_hip_dtype { CLOVE_HIP_F32 = 0, CLOVE_HIP_I32 = 1 };
+
+/* Opcodes: the hot-path subset of Clove's IR (backend.rs:85-127), used by the
+ * fused-chain entry and by the graph builder. */
+enum clove_hip_opcode {
+    CLOVE_OP_INPUT = 0,
+    CLOVE_OP_MATMUL = 1,
+    CLOVE_OP_ADD = 2,
+    CLOVE_OP_SUB = 3,
+    CLOVE_OP_MUL = 4,
+    CLOVE_OP_SCALAR_MUL = 5,   /* param = factor */
+    CLOVE_OP_FLATTEN = 6,      /* identity on data */
+    CLOVE_OP_RELU = 7,
+    CLOVE_OP_GELU = 8,
+    CLOVE_OP_SIN = 9,
+    CLOVE_OP_COS = 10,
+    CLOVE_OP_SOFTMAX = 11,
+    CLOVE_OP_LAYER_NORM = 12,  /* deps: x, gamma, beta */
+    CLOVE_OP_DROPOUT = 13,     /* param = rate; fused form scales by 1/(1-rate), lazy.rs:1795-1803 */
+    CLOVE_OP_RELU_GRAD = 14,   /* deps: x, grad_out */
+    CLOVE_OP_GELU_GRAD = 15,   /* deps: x, grad_out */
+    CLOVE_OP_CAST = 16,        /* identity on f32 data, lazy.rs:1808-1814 */
+    CLOVE_OP_SIGMOID = 17,
+    CLOVE_OP_TANH = 18,
+    CLOVE_OP_PAGED_ATTENTION = 19 /* deps: q, k, v, kv_cache, block_tables, context_lens */
+};
+
+/* ---------------------------------------------------------------------- */
+/* Device lifecycle.  Replaces EngineDevice::init (device.rs:79-150).      */
+/* ---------------------------------------------------------------------- */
+
+int clove_hip_init(int device_ordinal);
+int clove_hip_shutdown(void);
+/* Message of the last failed call on this thread ("" when none). */
+const char *clove_hip_last_error(void);
+/* Status code of the last call on this thread (CLOVE_HIP_OK when it succeeded);
+ * lets handle-returning entries report why they returned NULL. */
+int clove_hip_last_status(void);
+int clove_hip_synchronize(void);
+/* Use a caller-owned hipStream_t (passed as void*) for all later work;
+ * NULL restores the library's own stream. */
+int clove_hip_set_stream(void *hip_stream);
+void *clove_hip_get_stream(void);
+/* Return cached free device blocks to the driver. */
+int clove_hip_empty_cache(void);
+/* Bytes currently held by the caching allocator (in use + cached). */
+size_t clove_hip_memory_reserved(void);
+
+/* ---------------------------------------------------------------------- */
+/* Tensor lifecycle.  ffi.rs:71-113.                                      */
+/* ---------------------------------------------------------------------- */
+
+/* ffi.rs:71-87 clove_tensor_create(data, rows, cols): copies host data. */
+CTensor clove_hip_tensor_create(const float *data, size_t rows, size_t cols);
+/* N-d f32 / int32 tensors (block tables and context lengths are int32). */
+CTensor clove_hip_tensor_create_nd(const float *data, const size_t *shape, size_t ndim);
+CTensor clove_hip_tensor_create_i32(const int32_t *data, const size_t *shape, size_t ndim);
+/* Uninitialised device tensor of the given dtype. */
+CTensor clove_hip_tensor_empty(const size_t *shape, size_t ndim, int dtype);
+/* Non-owning view of caller-owned device memory (freed by the caller). */
+CTensor clove_hip_tensor_wrap(void *device_ptr, const size_t *shape, size_t ndim, int dtype);
+/* ffi.rs:89-97 clove_tensor_free.  NULL is ignored. */
+void clove_hip_tensor_free(CTensor t);
+/* ffi.rs:99-113 clove_tensor_data: downloads all elements (f32 tensors). */
+int clove_hip_tensor_data(CTensor t, float *out);
+/* Element-range download / upload for either dtype (offset and count in elements). */
+int clove_hip_tensor_read(CTensor t, void *out, size_t offset, size_t count);
+int clove_hip_tensor_write(CTensor t, const void *src, size_t offset, size_t count);
+size_t clove_hip_tensor_ndim(CTensor t);
+int clove_hip_tensor_shape(CTensor t, size_t *shape_out);
+size_t clove_hip_tensor_numel(CTensor t);
+int clove_hip_tensor_dtype(CTensor t);
+void *clove_hip_tensor_device_ptr(CTensor t);
+/* Seeded synthetic data on the device (counter-based splitmix64 stream,
+ * Box-Muller for normals).  Used to build benchmark-sized inputs without a
+ * host round trip; tests download the bytes before comparing. */
+int clove_hip_tensor_fill_normal(CTensor t, uint64_t seed, float mean, float stddev);
+int clove_hip_tensor_fill_uniform(CTensor t, uint64_t seed, float lo, float hi);
+
+/* ---------------------------------------------------------------------- */
+/* Eager ops: the hot-path methods of `trait Backend` (backend.rs:171-257) */
+/* as exported by ffi.rs.  Broadcast rule for add/sub/mul: b is read as    */
+/* b[i % numel(b)] (backend.rs:1489, :1623, :1754).                        */
+/* ---------------------------------------------------------------------- */
+
+CTensor clove_hip_add(CTensor a, CTensor b);          /* ffi.rs:119-122, backend.rs:1483 */
+CTensor clove_hip_sub(CTensor a, CTensor b);          /* ffi.rs:124-127, backend.rs:1748 */
+CTensor clove_hip_mul(CTensor a, CTensor b);          /* ffi.rs:129-132, backend.rs:1598 */
+CTensor clove_hip_mul_scalar(CTensor a, float s);     /* ffi.rs:139-142, backend.rs:1686 */
+CTensor clove_hip_relu(CTensor a);                    /* ffi.rs:163-166, backend.rs:1815 */
+CTensor clove_hip_gelu(CTensor a);                    /* ffi.rs:168-171, backend.rs:1917 */
+CTensor clove_hip_sigmoid(CTensor a);                 /* ffi.rs:173-176, backend.rs:2951 */
+CTensor clove_hip_tanh(CTensor a);                    /* ffi.rs:178-181, backend.rs:3008 */
+CTensor clove_hip_sin(CTensor a);                     /* ffi.rs:188-191, backend.rs:1986 */
+CTensor clove_hip_cos(CTensor a);                     /* ffi.rs:193-196, backend.rs:2044 */
+/* Row softmax over the last dimension (backend.rs:2102-2125 uses
+ * rows = shape[0], cols = shape[1]; identical for 2-d inputs). */
+CTensor clove_hip_softmax(CTensor a);                 /* ffi.rs:183-186 */
+/* Row layer norm over the last dimension, biased variance, eps 1e-5,
+ * out = ((x-mean)/sqrt(var+eps))*gamma[j] + beta[j] (backend.rs:2380-2405). */
+CTensor clove_hip_layer_norm(CTensor a, CTensor gamma, CTensor beta); /* ffi.rs:231-241 */
+/* C = A.B with m = prod(a.shape[..last]), k = a.shape[last], n = b.shape[1]
+ * (backend.rs:1282-1306); f32 accumulate on CDNA4 matrix cores. */
+CTensor clove_hip_matmul(CTensor a, CTensor b);       /* ffi.rs:134-137 */
+
+/* PagedAttention decode (backend.rs:249-256, ffi.rs:247-266).
+ *   q            f32 [B, H*D] (any shape with numel B*H*D)
+ *   k, v         f32 [B, H*D] freshly projected token, or NULL.  When given,
+ *                token ctx_b-1 of sequence b is read from them instead of
+ *                from the cache; when NULL every token comes from the cache.
+ *   kv_cache     f32 [2, num_blocks, block_size, H, D]: plane 0 keys,
+ *                plane 1 values (the per-plane layout of nn.rs:534)
+ *   block_tables int32 [B, max_blocks] (nn.rs:535)
+ *   context_lens int32 [B]
+ * Returns out f32 with q's shape: out = softmax(q.K^T / sqrt(D)) V per
+ * (sequence, head).  Fails with CLOVE_HIP_ERR_RANGE if a context length
+ * exceeds max_blocks*block_size or a table entry used lies outside the pool. */
+CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
+                                  CTensor block_tables, CTensor context_lens);
+/* Same with an explicit softmax scale (the reference uses 1/sqrt(D),
+ * lazy.rs:5267). */
+CTensor clove_hip_paged_attention_scaled(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
+                                         CTensor block_tables, CTensor context_lens,
+                                         float scale);
+/* Gather-index debug entry: int32 [B, max_ctx] of physical token slots
+ * bt[b][t/bs]*bs + t%bs (lazy.rs:5262-5270), -1 where t >= ctx_b.  Computed
+ * on the device by the same index code the attention kernel uses. */
+CTensor clove_hip_paged_gather_indices(CTensor block_tables, CTensor context_lens,
+                                       int block_size, int max_ctx);
+
+/* ---------------------------------------------------------------------- */
+/* Fused elementwise chain: the counterpart of Step::Fused                 */
+/* (codegen lazy.rs:1694-1838, broadcast rule lazy.rs:1600-1608).         */
+/* ---------------------------------------------------------------------- */
+
+typedef struct clove_hip_chain_op {
+    int32_t opcode;  /* CLOVE_OP_ADD .. CLOVE_OP_TANH (elementwise subset) */
+    int32_t src0;    /* operand: >= 0 earlier op of the chain, < 0 input -(src+1) */
+    int32_t src1;    /* second operand for binary ops, ignored otherwise */
+    int32_t store;   /* nonzero: materialise this op's value (last op always is) */
+    float param;     /* SCALAR_MUL factor or DROPOUT rate */
+} clove_hip_chain_op;
+
+/* Evaluates the chain per element of the output index space (numel of the
+ * last op = numel of its first operand chain), reading input k as
+ * input_k[idx % numel(input_k)].  Writes one new tensor per op with `store`
+ * set (and for the last op) into `outputs`, in op order; returns how many it
+ * wrote, or a negative status on error.  Chains are compiled once per
+ * structure with hipRTC for gfx950 and cached. */
+int clove_hip_fused_chain(const clove_hip_chain_op *ops, int n_ops, const CTensor *inputs,
+                          int n_inputs, CTensor *outputs);
+
+/* ---------------------------------------------------------------------- */
+/* Lazy graph: LazyBackend tracing (lazy.rs:36-1153), compile()           */
+/* (lazy.rs:4273-5302) and CompiledModel::execute (lazy.rs:2545-4271).    */
+/* ---------------------------------------------------------------------- */
+
+clove_hip_graph *clove_hip_graph_create(void);
+void clove_hip_graph_free(clove_hip_graph *g);
+/* Adds an Input node.  `shape` is a comma-separated list of SymInt
+ * expressions over integers and the symbols S0..S3 with + - * (for example
+ * "S0,784" or "S0*16,128"), mirroring SymInt (backend.rs:30-69).  Returns the
+ * node id or a negative status. */
+int clove_hip_graph_input(clove_hip_graph *g, const char *shape);
+/* Adds an op node over earlier node ids; the output shape follows the op's
+ * rule.  Returns the node id or a negative status. */
+int clove_hip_graph_op(clove_hip_graph *g, int opcode, const int *deps, int n_deps, float param);
+/* Dead-code elimination, constant folding, fusion planning, liveness-based
+ * buffer assignment and kernel compilation for the given outputs. */
+clove_hip_model *clove_hip_compile(clove_hip_graph *g, const int *outputs, int n_outputs);
+void clove_hip_model_free(clove_hip_model *m);
+/* Inputs are bound in Input-node creation order; env holds S0..S3 (NULL
+ * means all 1, as SymInt::eval defaults unknown symbols, backend.rs:43).
+ * Writes one new tensor per requested output. */
+int clove_hip_execute(clove_hip_model *m, const CTensor *inputs, int n_inputs,
+                      const int64_t *env, CTensor *outputs);
+/* Number of launched steps and a one-line-per-step description of the plan. */
+int clove_hip_model_num_steps(clove_hip_model *m);
+const char *clove_hip_model_describe(clove_hip_model *m);
+
+/* ---------------------------------------------------------------------- */
+/* Timing on the library's stream (for benchmarks).                        */
+/* ---------------------------------------------------------------------- */
+
+/* Records an event on the current stream; returns an id >= 0 or a negative status. */
+int clove_hip_event_record(void);
+/* Milliseconds between two recorded events (synchronises on the second). */
+int clove_hip_event_elapsed(int ev_start, int ev_end, float *ms);
+void clove_hip_event_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CLOVE_HIP_H */

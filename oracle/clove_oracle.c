@@ -1,0 +1,458 @@
+/*
+ * clove_oracle.c -- TEST INFRASTRUCTURE, NOT PRODUCT CODE.
+ *
+ * A CPU restatement of Clove's Rayon kernels (the eager CPU branch of
+ * `WgpuBackend`, /root/reference/src/backend.rs) plus a textbook paged-decode
+ * reference, used as the parity checker for the HIP backend and as the
+ * `cpu_baseline` leg of bench.py.  Only tests/, __graft_entry__.smoke() and
+ * bench.py's cpu_baseline may load this library; the product path never does.
+ *
+ * Rounding contract (so results match Rust's f32 code on x86-64 Linux):
+ *   - built with -ffp-contract=off and without -ffast-math: every `a*b + c`
+ *     rounds twice, as Rust does (it never contracts to FMA);
+ *   - sums are sequential left folds in f32, in the reference's loop order;
+ *   - transcendental calls go to glibc expf/tanhf/sinf/cosf, which is what
+ *     Rust's f32::exp/tanh/sin/cos lower to on this target; sqrt is the IEEE
+ *     sqrtss instruction (sqrtf); powi(2)/powi(3) are x*x and (x*x)*x.
+ *
+ * Threading mirrors Clove's Rayon pool sized to num_cpus::get()
+ * (reference src/device.rs:114-123): work is split over
+ * sysconf(_SC_NPROCESSORS_ONLN) POSIX threads unless oracle_set_threads()
+ * overrides it.  Per-element and per-row arithmetic does not depend on the
+ * split, so results are deterministic.
+ *
+ * Parity pins (tests/test_oracle.py): Clove's own known-answer tests
+ * (tests/engine_tests.rs:38-46, 697-706, 728-734), independent library
+ * implementations in float64 (numpy matmul, torch gelu(approximate="tanh"),
+ * torch softmax / layer_norm / scaled_dot_product_attention), closed forms
+ * (identity and permutation matmuls, constant rows, one-hot softmax,
+ * constant-V attention, ctx=1 attention) and brute-force gather indices.
+ */
+#define _GNU_SOURCE
+#include <math.h>
+#include <pthread.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------ */
+/* thread pool: a fork/join split of [0, n) into contiguous chunks     */
+/* ------------------------------------------------------------------ */
+
+static int g_threads = 0;
+
+int oracle_threads(void) {
+    if (g_threads > 0) return g_threads;
+    long n = sysconf(_SC_NPROCESSORS_ONLN);
+    return n > 0 ? (int)n : 1;
+}
+
+void oracle_set_threads(int n) { g_threads = n; }
+
+typedef void (*range_fn)(size_t begin, size_t end, void *ctx);
+
+typedef struct {
+    range_fn fn;
+    void *ctx;
+    size_t begin, end;
+} job_t;
+
+static void *job_run(void *p) {
+    job_t *j = (job_t *)p;
+    if (j->begin < j->end) j->fn(j->begin, j->end, j->ctx);
+    return NULL;
+}
+
+static void parallel_for(size_t n, range_fn fn, void *ctx) {
+    int t = oracle_threads();
+    if ((size_t)t > n) t = (int)(n ? n : 1);
+    if (t <= 1) {
+        fn(0, n, ctx);
+        return;
+    }
+    pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)t);
+    job_t *jobs = (job_t *)malloc(sizeof(job_t) * (size_t)t);
+    size_t chunk = (n + (size_t)t - 1) / (size_t)t;
+    for (int i = 0; i < t; ++i) {
+        size_t b = (size_t)i * chunk, e = b + chunk;
+        if (b > n) b = n;
+        if (e > n) e = n;
+        jobs[i].fn = fn;
+        jobs[i].ctx = ctx;
+        jobs[i].begin = b;
+        jobs[i].end = e;
+        if (i > 0) pthread_create(&th[i], NULL, job_run, &jobs[i]);
+    }
+    job_run(&jobs[0]);
+    for (int i = 1; i < t; ++i) pthread_join(th[i], NULL);
+    free(th);
+    free(jobs);
+}
+
+/* ------------------------------------------------------------------ */
+/* binary elementwise ops                                              */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const float *a, *b;
+    size_t nb;
+    float s;
+    float *out;
+    int op;
+} ew_ctx;
+
+enum { EW_ADD, EW_SUB, EW_MUL, EW_MUL_SCALAR, EW_RELU, EW_GELU, EW_SIGMOID,
+       EW_TANH, EW_SIN, EW_COS };
+
+/* sqrt(2/pi) computed in f32 exactly as backend.rs:1924 does:
+ * (2.0f32 / std::f32::consts::PI).sqrt() */
+static float gelu_c(void) { return sqrtf(2.0f / (float)3.14159265358979323846); }
+
+static void ew_body(size_t begin, size_t end, void *p) {
+    ew_ctx *c = (ew_ctx *)p;
+    const float *a = c->a, *b = c->b;
+    float *o = c->out;
+    const size_t nb = c->nb;
+    switch (c->op) {
+    case EW_ADD: /* backend.rs:1483-1493: a[i] + b[i % b_len] */
+        for (size_t i = begin; i < end; ++i) o[i] = a[i] + b[i % nb];
+        break;
+    case EW_SUB: /* backend.rs:1748-1758: a[i] - b[i % b_len] */
+        for (size_t i = begin; i < end; ++i) o[i] = a[i] - b[i % nb];
+        break;
+    case EW_MUL:
+        /* backend.rs:1598-1617 multiplies by b[0] when b has one element and
+         * by b[i] otherwise; the WGSL branch of the same op (:1623) reads
+         * b[idx % b_size].  The modulo form covers both, so it is used here. */
+        for (size_t i = begin; i < end; ++i) o[i] = a[i] * b[i % nb];
+        break;
+    case EW_MUL_SCALAR: /* backend.rs:1686-1697 */
+        for (size_t i = begin; i < end; ++i) o[i] = a[i] * c->s;
+        break;
+    case EW_RELU: /* backend.rs:1815-1826: if x > 0 { x } else { 0 } */
+        for (size_t i = begin; i < end; ++i) o[i] = a[i] > 0.0f ? a[i] : 0.0f;
+        break;
+    case EW_GELU: { /* backend.rs:1917-1928 */
+        const float k = gelu_c();
+        for (size_t i = begin; i < end; ++i) {
+            float x = a[i];
+            float x3 = (x * x) * x; /* powi(3) */
+            float inner = k * (x + 0.044715f * x3);
+            o[i] = 0.5f * x * (1.0f + tanhf(inner));
+        }
+        break;
+    }
+    case EW_SIGMOID: /* backend.rs:2951-2960: 1 / (1 + exp(-x)) */
+        for (size_t i = begin; i < end; ++i) o[i] = 1.0f / (1.0f + expf(-a[i]));
+        break;
+    case EW_TANH: /* backend.rs:3008-3016 */
+        for (size_t i = begin; i < end; ++i) o[i] = tanhf(a[i]);
+        break;
+    case EW_SIN: /* backend.rs:1986-1997 */
+        for (size_t i = begin; i < end; ++i) o[i] = sinf(a[i]);
+        break;
+    case EW_COS: /* backend.rs:2044-2055 */
+        for (size_t i = begin; i < end; ++i) o[i] = cosf(a[i]);
+        break;
+    }
+}
+
+static void ew_run(int op, const float *a, size_t n, const float *b, size_t nb,
+                   float s, float *out) {
+    ew_ctx c = {a, b, nb ? nb : 1, s, out, op};
+    parallel_for(n, ew_body, &c);
+}
+
+void oracle_add(const float *a, size_t n, const float *b, size_t nb, float *out) {
+    ew_run(EW_ADD, a, n, b, nb, 0.f, out);
+}
+void oracle_sub(const float *a, size_t n, const float *b, size_t nb, float *out) {
+    ew_run(EW_SUB, a, n, b, nb, 0.f, out);
+}
+void oracle_mul(const float *a, size_t n, const float *b, size_t nb, float *out) {
+    ew_run(EW_MUL, a, n, b, nb, 0.f, out);
+}
+void oracle_mul_scalar(const float *a, size_t n, float s, float *out) {
+    ew_run(EW_MUL_SCALAR, a, n, NULL, 1, s, out);
+}
+void oracle_relu(const float *a, size_t n, float *out) { ew_run(EW_RELU, a, n, NULL, 1, 0.f, out); }
+void oracle_gelu(const float *a, size_t n, float *out) { ew_run(EW_GELU, a, n, NULL, 1, 0.f, out); }
+void oracle_sigmoid(const float *a, size_t n, float *out) { ew_run(EW_SIGMOID, a, n, NULL, 1, 0.f, out); }
+void oracle_tanh(const float *a, size_t n, float *out) { ew_run(EW_TANH, a, n, NULL, 1, 0.f, out); }
+void oracle_sin(const float *a, size_t n, float *out) { ew_run(EW_SIN, a, n, NULL, 1, 0.f, out); }
+void oracle_cos(const float *a, size_t n, float *out) { ew_run(EW_COS, a, n, NULL, 1, 0.f, out); }
+
+/* ------------------------------------------------------------------ */
+/* row reductions                                                      */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const float *a, *g, *b;
+    size_t cols;
+    float *out;
+} row_ctx;
+
+/* backend.rs:2102-2125: max folded from -inf with f32::max, then
+ * e = exp(x - max) stored and summed sequentially, then out /= sum. */
+static void softmax_rows(size_t r0, size_t r1, void *p) {
+    row_ctx *c = (row_ctx *)p;
+    const size_t cols = c->cols;
+    for (size_t i = r0; i < r1; ++i) {
+        const float *x = c->a + i * cols;
+        float *o = c->out + i * cols;
+        float mx = -INFINITY;
+        for (size_t j = 0; j < cols; ++j) mx = fmaxf(mx, x[j]); /* f32::max ignores NaN like fmaxf */
+        float sum = 0.0f;
+        for (size_t j = 0; j < cols; ++j) {
+            float e = expf(x[j] - mx);
+            o[j] = e;
+            sum += e;
+        }
+        for (size_t j = 0; j < cols; ++j) o[j] /= sum;
+    }
+}
+
+void oracle_softmax(const float *a, size_t rows, size_t cols, float *out) {
+    row_ctx c = {a, NULL, NULL, cols, out};
+    parallel_for(rows, softmax_rows, &c);
+}
+
+/* backend.rs:2380-2405: mean = sum/n (Iterator::sum is a sequential fold
+ * starting at -0.0), var = sum((x-mean)^2)/n (biased, two-pass),
+ * std = sqrt(var + 1e-5), out = ((x - mean) / std) * gamma[j] + beta[j]. */
+static void layer_norm_rows(size_t r0, size_t r1, void *p) {
+    row_ctx *c = (row_ctx *)p;
+    const size_t cols = c->cols;
+    const float n = (float)cols;
+    for (size_t i = r0; i < r1; ++i) {
+        const float *x = c->a + i * cols;
+        float *o = c->out + i * cols;
+        float s = -0.0f;
+        for (size_t j = 0; j < cols; ++j) s += x[j];
+        const float mean = s / n;
+        float v = -0.0f;
+        for (size_t j = 0; j < cols; ++j) {
+            float d = x[j] - mean;
+            v += d * d; /* powi(2) */
+        }
+        const float var = v / n;
+        const float sd = sqrtf(var + 1e-5f);
+        for (size_t j = 0; j < cols; ++j) o[j] = ((x[j] - mean) / sd) * c->g[j] + c->b[j];
+    }
+}
+
+void oracle_layer_norm(const float *a, size_t rows, size_t cols, const float *gamma,
+                       const float *beta, float *out) {
+    row_ctx c = {a, gamma, beta, cols, out};
+    parallel_for(rows, layer_norm_rows, &c);
+}
+
+/* ------------------------------------------------------------------ */
+/* matmul                                                              */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const float *a, *bt;
+    size_t k, n;
+    float *c;
+} mm_ctx;
+
+static void mm_rows(size_t r0, size_t r1, void *p) {
+    mm_ctx *c = (mm_ctx *)p;
+    for (size_t i = r0; i < r1; ++i) {
+        const float *ra = c->a + i * c->k;
+        float *row = c->c + i * c->n;
+        for (size_t j = 0; j < c->n; ++j) {
+            const float *rb = c->bt + j * c->k;
+            float sum = 0.0f;
+            for (size_t q = 0; q < c->k; ++q) sum += ra[q] * rb[q];
+            row[j] = sum;
+        }
+    }
+}
+
+/* backend.rs:266-287 (rayon_matmul): B is transposed first, then each output
+ * row is computed in parallel; each element is a sequential f32 dot product
+ * over p = 0..k with separate multiply and add roundings.  `row_begin` and
+ * `row_end` restrict the rows computed (the bench times a bounded sample);
+ * pass 0 and m for the whole product. */
+void oracle_matmul_rows(const float *a, const float *b, size_t m, size_t k, size_t n,
+                        size_t row_begin, size_t row_end, float *c) {
+    (void)m;
+    float *bt = (float *)malloc(sizeof(float) * k * n);
+    for (size_t i = 0; i < k; ++i)
+        for (size_t j = 0; j < n; ++j) bt[j * k + i] = b[i * n + j];
+    mm_ctx ctx = {a + row_begin * k, bt, k, n, c + row_begin * n};
+    parallel_for(row_end - row_begin, mm_rows, &ctx);
+    free(bt);
+}
+
+void oracle_matmul(const float *a, const float *b, size_t m, size_t k, size_t n, float *c) {
+    oracle_matmul_rows(a, b, m, k, n, 0, m, c);
+}
+
+/* ------------------------------------------------------------------ */
+/* paged decode attention                                              */
+/* ------------------------------------------------------------------ */
+/*
+ * Clove has no CPU paged attention (backend.rs:2937-2948 panics, the WGSL at
+ * lazy.rs:5241-5275 is a placeholder), so this is the textbook definition on
+ * the layout Clove documents for its cache (nn.rs:534-535):
+ *   kv_cache  : two planes [2][num_blocks][block_size][H][D] (plane 0 = K,
+ *               plane 1 = V), f32
+ *   block_tables : int32 [B][max_blocks]
+ *   context_lens : int32 [B]
+ *   q, k_new, v_new, out : [B][H*D]
+ * For sequence b the context is tokens t = 0..ctx_b-1.  Token t lives in
+ * physical slot bt[b][t / block_size] * block_size + t % block_size.  When
+ * k_new/v_new are given, the last token (t = ctx_b-1) is taken from them
+ * instead of from the cache (the freshly projected token of nn.rs:540-546).
+ * out = sum_t softmax_t(scale * q.k_t) v_t; ctx_b == 0 gives zeros.
+ * The f32 variant follows Clove's softmax order (backend.rs:2107-2124):
+ * sequential dot, max fold, exp, sequential sum, divide, then a sequential
+ * weighted sum over t.
+ */
+
+typedef struct {
+    const float *q, *kn, *vn, *kv;
+    const int32_t *bt, *cl;
+    int64_t num_blocks;
+    int H, D, bs, max_blocks;
+    float scale;
+    float *out;
+    double *out64;
+} pa_ctx;
+
+static inline const float *pa_row(const pa_ctx *c, int plane, int b, int t, int h, int ctx) {
+    if (c->kn && t == ctx - 1) {
+        const float *src = plane ? c->vn : c->kn;
+        return src + ((size_t)b * c->H + h) * c->D;
+    }
+    int64_t blk = c->bt[(size_t)b * c->max_blocks + t / c->bs];
+    int64_t slot = blk * c->bs + t % c->bs;
+    size_t plane_off = (size_t)plane * (size_t)c->num_blocks * c->bs * c->H * c->D;
+    return c->kv + plane_off + ((size_t)slot * c->H + h) * c->D;
+}
+
+static void pa_body_f32(size_t p0, size_t p1, void *p) {
+    pa_ctx *c = (pa_ctx *)p;
+    float *s = NULL;
+    size_t s_cap = 0;
+    for (size_t pair = p0; pair < p1; ++pair) {
+        int b = (int)(pair / c->H), h = (int)(pair % c->H);
+        int ctx = c->cl[b];
+        const float *q = c->q + ((size_t)b * c->H + h) * c->D;
+        float *o = c->out + ((size_t)b * c->H + h) * c->D;
+        for (int d = 0; d < c->D; ++d) o[d] = 0.0f;
+        if (ctx <= 0) continue;
+        if ((size_t)ctx > s_cap) {
+            free(s);
+            s_cap = (size_t)ctx;
+            s = (float *)malloc(sizeof(float) * s_cap);
+        }
+        float mx = -INFINITY;
+        for (int t = 0; t < ctx; ++t) {
+            const float *k = pa_row(c, 0, b, t, h, ctx);
+            float dot = 0.0f;
+            for (int d = 0; d < c->D; ++d) dot += q[d] * k[d];
+            s[t] = dot * c->scale;
+            mx = fmaxf(mx, s[t]);
+        }
+        float sum = 0.0f;
+        for (int t = 0; t < ctx; ++t) {
+            s[t] = expf(s[t] - mx);
+            sum += s[t];
+        }
+        for (int t = 0; t < ctx; ++t) s[t] /= sum;
+        for (int t = 0; t < ctx; ++t) {
+            const float *v = pa_row(c, 1, b, t, h, ctx);
+            for (int d = 0; d < c->D; ++d) o[d] += s[t] * v[d];
+        }
+    }
+    free(s);
+}
+
+static void pa_body_f64(size_t p0, size_t p1, void *p) {
+    pa_ctx *c = (pa_ctx *)p;
+    double *s = NULL;
+    size_t s_cap = 0;
+    for (size_t pair = p0; pair < p1; ++pair) {
+        int b = (int)(pair / c->H), h = (int)(pair % c->H);
+        int ctx = c->cl[b];
+        const float *q = c->q + ((size_t)b * c->H + h) * c->D;
+        double *o = c->out64 + ((size_t)b * c->H + h) * c->D;
+        for (int d = 0; d < c->D; ++d) o[d] = 0.0;
+        if (ctx <= 0) continue;
+        if ((size_t)ctx > s_cap) {
+            free(s);
+            s_cap = (size_t)ctx;
+            s = (double *)malloc(sizeof(double) * s_cap);
+        }
+        double mx = -INFINITY;
+        for (int t = 0; t < ctx; ++t) {
+            const float *k = pa_row(c, 0, b, t, h, ctx);
+            double dot = 0.0;
+            for (int d = 0; d < c->D; ++d) dot += (double)q[d] * (double)k[d];
+            s[t] = dot * (double)c->scale;
+            if (s[t] > mx) mx = s[t];
+        }
+        double sum = 0.0;
+        for (int t = 0; t < ctx; ++t) {
+            s[t] = exp(s[t] - mx);
+            sum += s[t];
+        }
+        for (int t = 0; t < ctx; ++t) {
+            const float *v = pa_row(c, 1, b, t, h, ctx);
+            const double w = s[t] / sum;
+            for (int d = 0; d < c->D; ++d) o[d] += w * (double)v[d];
+        }
+    }
+    free(s);
+}
+
+/* Sequences [seq_begin, seq_end) are computed; rows of other sequences in
+ * `out` are left untouched (the bench times a bounded sample). */
+void oracle_paged_attention_f32(const float *q, const float *k_new, const float *v_new,
+                                const float *kv_cache, int64_t num_blocks,
+                                const int32_t *block_tables, int max_blocks,
+                                const int32_t *context_lens, int num_seqs, int num_heads,
+                                int head_dim, int block_size, float scale, int seq_begin,
+                                int seq_end, float *out) {
+    (void)num_seqs;
+    pa_ctx c = {q, k_new, v_new, kv_cache, block_tables, context_lens, num_blocks,
+                num_heads, head_dim, block_size, max_blocks, scale, out, NULL};
+    /* shift the base pointers so that pair index 0 is (seq_begin, head 0) */
+    size_t row = (size_t)seq_begin * num_heads * head_dim;
+    c.q = q + row;
+    c.kn = k_new ? k_new + row : NULL;
+    c.vn = v_new ? v_new + row : NULL;
+    c.bt = block_tables + (size_t)seq_begin * max_blocks;
+    c.cl = context_lens + seq_begin;
+    c.out = out + row;
+    parallel_for((size_t)(seq_end - seq_begin) * num_heads, pa_body_f32, &c);
+}
+
+void oracle_paged_attention_f64(const float *q, const float *k_new, const float *v_new,
+                                const float *kv_cache, int64_t num_blocks,
+                                const int32_t *block_tables, int max_blocks,
+                                const int32_t *context_lens, int num_seqs, int num_heads,
+                                int head_dim, int block_size, float scale, double *out) {
+    pa_ctx c = {q, k_new, v_new, kv_cache, block_tables, context_lens, num_blocks,
+                num_heads, head_dim, block_size, max_blocks, scale, NULL, out};
+    parallel_for((size_t)num_seqs * num_heads, pa_body_f64, &c);
+}
+
+/* Physical token slot of every logical token: slots[b][t] =
+ * bt[b][t / bs] * bs + t % bs for t < ctx_b, -1 beyond (the gather the
+ * reference WGSL performs at lazy.rs:5262-5270, with the table stride taken
+ * from the table's shape instead of the hard-coded 1024). */
+void oracle_paged_slots(const int32_t *block_tables, int max_blocks, const int32_t *context_lens,
+                        int num_seqs, int block_size, int max_ctx, int32_t *slots) {
+    for (int b = 0; b < num_seqs; ++b)
+        for (int t = 0; t < max_ctx; ++t)
+            slots[(size_t)b * max_ctx + t] =
+                t < context_lens[b]
+                    ? block_tables[(size_t)b * max_blocks + t / block_size] * block_size + t % block_size
+                    : -1;
+}

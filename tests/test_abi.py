@@ -1,0 +1,155 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every symbol the
+header declares, reports errors as status codes instead of aborting, and the
+lazy planner builds the expected plans (planning touches no device)."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import clove_amd as ca
+from conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "clove_hip.h")
+
+
+@pytest.fixture(scope="module", autouse=True)
+def built_library():
+    if not os.path.exists(ca.LIB_PATH):
+        import __graft_entry__
+
+        __graft_entry__.build()
+    return ca.lib()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(clove_hip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path():
+    names = declared_functions()
+    for required in ("clove_hip_init", "clove_hip_tensor_create", "clove_hip_tensor_data",
+                     "clove_hip_tensor_free", "clove_hip_add", "clove_hip_sub", "clove_hip_mul",
+                     "clove_hip_mul_scalar", "clove_hip_relu", "clove_hip_gelu",
+                     "clove_hip_sigmoid", "clove_hip_tanh", "clove_hip_sin", "clove_hip_cos",
+                     "clove_hip_softmax", "clove_hip_layer_norm", "clove_hip_matmul",
+                     "clove_hip_paged_attention", "clove_hip_paged_gather_indices",
+                     "clove_hip_fused_chain", "clove_hip_compile", "clove_hip_execute"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    out = subprocess.run(["nm", "-D", "--defined-only", ca.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\sT\s(clove_hip_\w+)", out))
+    missing = [n for n in declared_functions() if n not in exported]
+    assert not missing, f"declared but not exported: {missing}"
+    # ...and the Python binding declares a signature for each of them.
+    lib = ca.lib()
+    for n in declared_functions():
+        assert getattr(lib, n).argtypes is not None, n
+
+
+def test_calls_before_init_fail_with_status():
+    lib = ca.lib()
+    shape = (C.c_size_t * 2)(2, 3)
+    p = lib.clove_hip_tensor_empty(shape, 2, ca.F32)
+    assert not p
+    assert lib.clove_hip_last_status() == ca.ERR_NOT_INIT
+    assert "clove_hip_init" in ca.last_error()
+    assert lib.clove_hip_synchronize() == ca.ERR_NOT_INIT
+
+
+def test_null_handles_are_errors_not_crashes():
+    lib = ca.lib()
+    assert not lib.clove_hip_add(None, None)
+    assert lib.clove_hip_last_status() == ca.ERR_INVALID
+    assert not lib.clove_hip_tensor_create(None, 2, 2)        # ffi.rs:78-80
+    assert lib.clove_hip_tensor_data(None, None) == ca.ERR_INVALID
+    lib.clove_hip_tensor_free(None)                           # ffi.rs:91-96: ignored
+    assert not lib.clove_hip_paged_attention(None, None, None, None, None, None)
+
+
+# ---------------------------------------------------------------------------
+# planner (lazy.rs:1553-2535), CPU only
+# ---------------------------------------------------------------------------
+
+def steps(model):
+    return [line.split(" ")[0] for line in model.describe().strip().splitlines()[:-1]]
+
+
+def mlp_graph():
+    g = ca.Graph()
+    x = g.input("S0,784")
+    w1 = g.input("784,128")
+    b1 = g.input("1,128")
+    w2 = g.input("128,10")
+    b2 = g.input("1,10")
+    h = g.op("relu", g.op("add", g.op("matmul", x, w1), b1))
+    y = g.op("softmax", g.op("add", g.op("matmul", h, w2), b2))
+    return g, y
+
+
+def test_plan_mlp():
+    g, y = mlp_graph()
+    m = g.compile([y])
+    assert steps(m) == ["MatMul", "Fused[Add,ReLU]", "MatMul", "Fused[Add]", "Softmax"]
+    assert m.num_steps == 5
+    # liveness: the first matmul's buffer is free once the chain has read it
+    assert "vbufs=2" in m.describe() or "vbufs=3" in m.describe()
+
+
+def test_plan_dce_and_constant_folding():
+    g = ca.Graph()
+    a = g.input("4,4")
+    b = g.input("4,4")
+    dead = g.op("gelu", g.op("sin", a))             # not an output: removed
+    s = g.op("scalar_mul", a, param=1.0)            # x * 1.0: folded away
+    y = g.op("mul", g.op("add", s, b), b)
+    m = g.compile([y])
+    d = m.describe()
+    assert steps(m) == ["Fused[Add,Mul]"]
+    assert "folded=1" in d
+    assert "Sin" not in d and "GELU" not in d and "ScalarMul" not in d
+    del dead
+
+
+def test_plan_barriers_and_escaping_values():
+    g = ca.Graph()
+    x = g.input("8,16")
+    gam = g.input("16")
+    bet = g.input("16")
+    t = g.op("tanh", x)
+    u = g.op("mul_scalar" if False else "scalar_mul", t, param=2.0)
+    ln = g.op("layer_norm", u, gam, bet)
+    y = g.op("add", ln, t)            # t escapes the first chain
+    m = g.compile([y])
+    lines = m.describe().strip().splitlines()
+    assert steps(m) == ["Fused[Tanh,ScalarMul]", "LayerNorm", "Fused[Add]"]
+    assert re.search(rf"out=\({t},{u}\)", lines[0]), lines[0]
+
+
+def test_plan_splits_chains_on_shape_change():
+    g = ca.Graph()
+    a = g.input("4,8")
+    f = g.op("flatten", a)            # [1, 32]: same numel, joins the chain
+    b = g.input("3")
+    c = g.op("add", b, b)             # 3 elements: a new chain
+    m = g.compile([f, c])
+    assert steps(m) == ["Fused[Flatten]", "Fused[Add]"]
+
+
+def test_symbolic_shapes_parse_and_reject():
+    g = ca.Graph()
+    g.input("S0*16+2,(S1-1)*4")
+    for bad in ("", "S4", "3,,4", "2*", "x"):
+        with pytest.raises(ca.CloveError):
+            g.input(bad)
+    with pytest.raises(ca.CloveError):
+        g.op("matmul", 0)             # wrong operand count
+    with pytest.raises(ca.CloveError):
+        g.op("add", 0, 99)            # unknown node

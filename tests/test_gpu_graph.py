@@ -1,0 +1,85 @@
+"""GPU parity: plans built by the lazy planner (compile/execute).
+
+Config 1 (the 2-layer MLP) runs as one compiled plan and is compared with
+the eager CPU composition (Linear::forward, relu, softmax); the tolerance is
+the softmax one (1e-4 relative) since the softmax output is what is checked.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from clove_amd import workloads
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def mlp_graph(hip, batch="64"):
+    g = hip.Graph()
+    x = g.input(f"{batch},784")
+    w1, b1 = g.input("784,128"), g.input("1,128")
+    w2, b2 = g.input("128,10"), g.input("1,10")
+    h = g.op("relu", g.op("add", g.op("matmul", x, w1), b1))
+    y = g.op("softmax", g.op("add", g.op("matmul", h, w2), b2))
+    return g, y
+
+
+def test_config1_mlp_plan(hip):
+    x, w1, b1, w2, b2 = workloads.mlp_inputs(0)
+    g, y = mlp_graph(hip)
+    model = g.compile([y])
+    (out,) = model.execute([hip.tensor(v) for v in (x, w1, b1, w2, b2)])
+    assert out.shape == (64, 10)
+    assert_close(out.numpy(), oracle.mlp_forward(x, w1, b1, w2, b2), 1e-4, 1e-7, "mlp")
+    # the same plan again (buffers reused)
+    (out2,) = model.execute([hip.tensor(v) for v in (x, w1, b1, w2, b2)])
+    assert np.array_equal(out.numpy(), out2.numpy())
+
+
+def test_symbolic_batch(hip):
+    x, w1, b1, w2, b2 = workloads.mlp_inputs(0)
+    g, y = mlp_graph(hip, batch="S0")
+    model = g.compile([y])
+    for bsz in (1, 17, 64):
+        (out,) = model.execute([hip.tensor(v) for v in (x[:bsz], w1, b1, w2, b2)], env=[bsz])
+        assert_close(out.numpy(), oracle.mlp_forward(x[:bsz], w1, b1, w2, b2), 1e-4, 1e-7,
+                     f"batch {bsz}")
+    with pytest.raises(hip.CloveError):  # env says 5 rows, input has 17
+        model.execute([hip.tensor(v) for v in (x[:17], w1, b1, w2, b2)], env=[5])
+
+
+def test_chain_with_escaping_values_and_layer_norm(hip):
+    gg = rng(3)
+    xv = gg.standard_normal((16, 256)).astype(np.float32)
+    gam = gg.uniform(0.5, 1.5, 256).astype(np.float32)
+    bet = gg.uniform(-0.1, 0.1, 256).astype(np.float32)
+    g = hip.Graph()
+    x, gm, bt = g.input("16,256"), g.input("256"), g.input("256")
+    t = g.op("tanh", x)
+    u = g.op("scalar_mul", t, param=2.0)
+    ln = g.op("layer_norm", u, gm, bt)
+    y = g.op("add", ln, t)
+    m = g.compile([y, t])
+    out, tt = m.execute([hip.tensor(xv), hip.tensor(gam), hip.tensor(bet)])
+    t_ref = oracle.tanh(xv)
+    want = oracle.add(oracle.layer_norm(oracle.mul_scalar(t_ref, 2.0), gam, bet), t_ref)
+    assert_close(tt.numpy(), t_ref, 1e-5, 1e-6, "escaping tanh")
+    assert_close(out.numpy(), want, 1e-4, 1e-5, "chain + layer_norm")
+
+
+def test_paged_attention_in_graph(hip):
+    gg = rng(4)
+    B, H, D, bs, nb, mb = 2, 2, 64, 16, 32, 8
+    kv = gg.standard_normal((2, nb, bs, H, D)).astype(np.float32)
+    q, kn, vn = (gg.standard_normal((B, H * D)).astype(np.float32) for _ in range(3))
+    bt = gg.permutation(nb)[: B * mb].reshape(B, mb).astype(np.int32)
+    cl = np.array([37, 128], np.int32)
+    g = hip.Graph()
+    ids = [g.input(f"{B},{H * D}"), g.input(f"{B},{H * D}"), g.input(f"{B},{H * D}"),
+           g.input(f"2,{nb},{bs},{H},{D}"), g.input(f"{B},{mb}"), g.input(f"{B}")]
+    y = g.op("paged_attention", *ids)
+    z = g.op("scalar_mul", y, param=3.0)
+    m = g.compile([z])
+    (out,) = m.execute([hip.tensor(v) for v in (q, kn, vn, kv, bt, cl)])
+    want = oracle.mul_scalar(oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D), 3.0)
+    assert_close(out.numpy(), want, 2e-3, 1e-5, "paged in graph")

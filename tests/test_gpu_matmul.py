@@ -1,0 +1,70 @@
+"""GPU parity: f32 matmul on MFMA vs rayon_matmul restated (oracle).
+
+Tolerance (matmul, BASELINE): |g - c| <= atol + 2e-3 |c| with atol
+= 1e-4 * max|c|, i.e. a relative bound on the output scale for entries that
+cancel to ~0 (C entries are sums of K products of either sign).  Both sides
+accumulate in f32; only the summation order differs.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got, want, what):
+    atol = 1e-4 * float(np.abs(want).max() or 1.0)
+    assert_close(got, want, 2e-3, atol, what)
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (64, 784, 128), (64, 128, 10),
+                                   (130, 17, 129), (257, 64, 255), (128, 128, 128),
+                                   (256, 512, 384), (31, 4096, 96), (2, 3, 4)])
+def test_matmul_shapes(hip, m, k, n):
+    g = rng(m * 7 + k * 3 + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    got = hip.matmul(hip.tensor(a), hip.tensor(b))
+    assert got.shape == (m, n)
+    check(got.numpy(), oracle.matmul(a, b), f"matmul {m}x{k}x{n}")
+
+
+def test_matmul_leading_dims_and_errors(hip):
+    g = rng(5)
+    a = g.standard_normal((2, 3, 5)).astype(np.float32)
+    b = g.standard_normal((5, 4)).astype(np.float32)
+    got = hip.matmul(hip.tensor(a), hip.tensor(b))
+    assert got.shape == (2, 3, 4)
+    check(got.numpy(), oracle.matmul(a, b), "leading dims")
+    with pytest.raises(hip.CloveError):
+        hip.matmul(hip.tensor(a), hip.tensor(np.ones((4, 4), np.float32)))
+
+
+def test_matmul_identity_is_exact(hip):
+    a = rng(6).standard_normal((192, 256)).astype(np.float32)
+    got = hip.matmul(hip.tensor(a), hip.tensor(np.eye(256, dtype=np.float32))).numpy()
+    assert np.array_equal(got, a)
+
+
+def test_config4_full(hip):
+    """Config 4: C = A.B at M=N=K=4096 and the skinny M=32 case, A and B
+    normal(0, 1/sqrt(K)), seed 3.  The oracle checks sampled row blocks of
+    the square product (it is a sequential CPU kernel) and all of the
+    skinny one."""
+    g = rng(3)
+    K = 4096
+    a = g.normal(0, 1 / np.sqrt(K), (4096, K)).astype(np.float32)
+    b = g.normal(0, 1 / np.sqrt(K), (K, 4096)).astype(np.float32)
+    tb = hip.tensor(b)
+    got = hip.matmul(hip.tensor(a), tb).numpy()
+    for r0 in (0, 2048 + 64, 4096 - 32):
+        want = oracle.matmul(a, b, rows=(r0, r0 + 32))[r0:r0 + 32]
+        check(got[r0:r0 + 32], want, f"4096^3 rows {r0}..")
+    # every element against a float64 product, with a K-scaled bound
+    sub = slice(0, 4096, 97)
+    ref64 = a[sub].astype(np.float64) @ b.astype(np.float64)
+    assert np.max(np.abs(got[sub] - ref64)) < 1e-5
+    a32 = a[:32].copy()
+    check(hip.matmul(hip.tensor(a32), tb).numpy(), oracle.matmul(a32, b), "skinny 32x4096x4096")

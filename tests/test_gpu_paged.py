@@ -1,0 +1,123 @@
+"""GPU parity: PagedAttention decode and its block-table gather.
+
+Tolerance (attention, BASELINE): |g - c| <= 1e-5 + 2e-3 |c| against the f32
+CPU restatement; gather indices are compared bit for bit.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from clove_amd import workloads
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 2e-3, 1e-5
+
+
+def make(seed, B, H, D, bs, nb, max_blocks, ctx):
+    g = rng(seed)
+    kv = g.standard_normal((2, nb, bs, H, D), dtype=np.float32)
+    q = g.standard_normal((B, H * D), dtype=np.float32)
+    kn = g.standard_normal((B, H * D), dtype=np.float32)
+    vn = g.standard_normal((B, H * D), dtype=np.float32)
+    bt = g.permutation(nb)[: B * max_blocks].reshape(B, max_blocks).astype(np.int32)
+    return q, kn, vn, kv, bt, np.asarray(ctx, np.int32)
+
+
+def run(hip, q, kn, vn, kv, bt, cl, scale=None):
+    t = hip.tensor
+    out = hip.paged_attention(t(q), t(kn) if kn is not None else None,
+                              t(vn) if vn is not None else None, t(kv), t(bt), t(cl), scale)
+    return out.numpy()
+
+
+@pytest.mark.parametrize("D", [64, 128, 256])
+@pytest.mark.parametrize("bs", [8, 16, 32])
+def test_head_dims_and_block_sizes(hip, D, bs):
+    H, B, max_blocks = 2, 4, 1200 // bs + 1
+    ctx = [1, bs, 511 + bs, 1200]
+    q, kn, vn, kv, bt, cl = make(D + bs, B, H, D, bs, B * max_blocks + 3, max_blocks, ctx)
+    want = oracle.paged_attention(q, None, None, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs}")
+
+
+@pytest.mark.parametrize("ctx", [[1, 2, 15, 16], [17, 511, 512, 513], [1024, 1535, 2049, 0]])
+def test_context_edges_with_new_token(hip, ctx):
+    H, D, bs, mb = 4, 128, 16, 160
+    q, kn, vn, kv, bt, cl = make(sum(ctx), 4, H, D, bs, 4 * mb, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(4, H * D)
+    assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"ctx={ctx}")
+    want = oracle.paged_attention(q, None, None, kv, bt, cl).reshape(4, H * D)
+    assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"ctx={ctx} cached")
+
+
+def test_empty_context_writes_zeros(hip):
+    q, kn, vn, kv, bt, cl = make(5, 3, 2, 64, 16, 40, 8, [0, 3, 0])
+    out = run(hip, q, None, None, kv, bt, cl)
+    assert np.all(out[0] == 0) and np.all(out[2] == 0)
+
+
+def test_explicit_scale(hip):
+    q, kn, vn, kv, bt, cl = make(6, 2, 2, 64, 16, 40, 8, [100, 7])
+    want = oracle.paged_attention(q, None, None, kv, bt, cl, scale=0.3).reshape(2, 128)
+    assert_close(run(hip, q, None, None, kv, bt, cl, 0.3), want, RTOL, ATOL, "scale")
+
+
+def test_gather_indices_bit_exact(hip):
+    g = rng(7)
+    bt = g.permutation(5000)[: 8 * 300].reshape(8, 300).astype(np.int32)
+    cl = np.array([0, 1, 15, 16, 17, 4095, 4800, 2000], np.int32)
+    got = hip.paged_gather_indices(hip.tensor(bt), hip.tensor(cl), 16, 4810).numpy()
+    assert np.array_equal(got, oracle.paged_slots(bt, cl, 16, 4810))
+
+
+def test_bad_table_entry_is_reported_not_read(hip):
+    # An entry outside the pool must not be dereferenced; the kernel skips it
+    # and the next synchronising call reports CLOVE_HIP_ERR_RANGE.
+    q, kn, vn, kv, bt, cl = make(8, 2, 2, 64, 16, 20, 4, [40, 40])
+    bt[1, 1] = 1 << 30
+    out = hip.paged_attention(hip.tensor(q), None, None, hip.tensor(kv), hip.tensor(bt),
+                              hip.tensor(cl))
+    with pytest.raises(hip.CloveError) as e:
+        hip.synchronize()
+    assert e.value.code == hip.ERR_RANGE
+    want = oracle.paged_attention(q, None, None, kv, bt[:1], cl[:1]).reshape(1, 128)
+    assert_close(out.numpy()[:1], want, RTOL, ATOL, "unaffected sequence")
+    hip.synchronize()  # the flag was cleared by the report
+
+
+def test_shape_errors(hip):
+    q, kn, vn, kv, bt, cl = make(9, 2, 2, 48, 16, 20, 4, [5, 5])
+    with pytest.raises(hip.CloveError):  # head_dim 48 has no kernel
+        run(hip, q, None, None, kv, bt, cl)
+    q, kn, vn, kv, bt, cl = make(9, 2, 2, 64, 16, 20, 4, [5, 5])
+    with pytest.raises(hip.CloveError):  # q with the wrong element count
+        run(hip, q[:, :64], None, None, kv, bt, cl)
+
+
+def test_config5_full(hip):
+    """Config 5: B=32, H=32, D=128, block 16, ctx ~ U[512, 4096], tables from
+    a seeded permutation of a 16,384-block pool, Q/K/V normal(0,1), seed 4,
+    scale 1/sqrt(128).  The 8 GiB pool is filled on the device; the oracle
+    checks four whole sequences (all heads) on a compact copy of the blocks
+    they use, and every output is checked against the f64 evaluation for
+    finiteness and scale."""
+    P = workloads.PAGED
+    B, H, D, bs, nb = P["num_seqs"], P["num_heads"], P["head_dim"], P["block_size"], P["pool_blocks"]
+    ctx, bt = workloads.paged_layout(4)
+    kv = hip.empty((2, nb, bs, H, D)).fill_normal(4)
+    q = rng(4).standard_normal((B, H * D), dtype=np.float32)
+    tq, tbt, tcl = hip.tensor(q), hip.tensor(bt), hip.tensor(ctx)
+    out = hip.paged_attention(tq, None, None, kv, tbt, tcl).numpy()
+    assert np.all(np.isfinite(out))
+    plane = nb * bs * H * D
+    blk = bs * H * D
+
+    def read_block(p, b):
+        return kv.read(p * plane + b * blk, blk).reshape(bs, H, D)
+
+    seqs = [int(np.argmin(ctx)), int(np.argmax(ctx)), 7, 19]
+    pool, sbt, scl = workloads.compact_pool(read_block, bt, ctx, seqs, bs)
+    want = oracle.paged_attention(q[seqs], None, None, pool, sbt, scl).reshape(len(seqs), H * D)
+    assert_close(out[seqs], want, RTOL, ATOL, "config5 sampled sequences")

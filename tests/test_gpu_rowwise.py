@@ -1,0 +1,65 @@
+"""GPU parity: row softmax and layer norm vs the CPU oracle.
+
+Tolerance (reductions, BASELINE): |g - c| <= atol + 1e-4 |c|.  The CPU sums
+each row sequentially in f32 and the GPU with a wave64 butterfly; both stay
+well inside 1e-4 relative.  atol: 1e-9 for softmax (outputs are >= 0 and
+tiny values carry their own relative error), 1e-5 for layer norm (outputs
+cancel to ~0 after beta, on an O(1) scale).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [(1, 1), (3, 10), (7, 33), (5, 4), (9, 256), (33, 4096), (6, 4100), (2, 8192),
+          (3, 16384), (2, 3, 64)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_softmax(hip, shape):
+    x = rng(sum(shape)).normal(0, 2, shape).astype(np.float32)
+    got = hip.softmax(hip.tensor(x))
+    assert got.shape == shape
+    assert_close(got.numpy(), oracle.softmax(x), 1e-4, 1e-9, f"softmax {shape}")
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_layer_norm(hip, shape):
+    g = rng(sum(shape) + 1)
+    x = g.normal(0, 2, shape).astype(np.float32)
+    cols = shape[-1]
+    gam = g.uniform(0.5, 1.5, cols).astype(np.float32)
+    bet = g.uniform(-0.1, 0.1, cols).astype(np.float32)
+    got = hip.layer_norm(hip.tensor(x), hip.tensor(gam), hip.tensor(bet))
+    assert_close(got.numpy(), oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm {shape}")
+
+
+def test_config3_full(hip):
+    """Config 3: [8192, 4096] normal(0, 2), seed 2; gamma U[0.5, 1.5],
+    beta U[-0.1, 0.1]."""
+    g = rng(2)
+    x = g.normal(0, 2, (8192, 4096)).astype(np.float32)
+    gam = g.uniform(0.5, 1.5, 4096).astype(np.float32)
+    bet = g.uniform(-0.1, 0.1, 4096).astype(np.float32)
+    tx = hip.tensor(x)
+    assert_close(hip.softmax(tx).numpy(), oracle.softmax(x), 1e-4, 1e-9, "softmax config3")
+    assert_close(hip.layer_norm(tx, hip.tensor(gam), hip.tensor(bet)).numpy(),
+                 oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, "layer_norm config3")
+
+
+def test_closed_forms_on_device(hip):
+    c = hip.softmax(hip.tensor(np.full((4, 4096), -2.5, np.float32))).numpy()
+    assert np.all(c == np.float32(1 / 4096))
+    beta = np.linspace(-1, 1, 512, dtype=np.float32)
+    ln = hip.layer_norm(hip.tensor(np.full((3, 512), 4.0, np.float32)),
+                        hip.tensor(np.ones(512, np.float32)), hip.tensor(beta)).numpy()
+    assert np.array_equal(ln, np.broadcast_to(beta, ln.shape))
+
+
+def test_layer_norm_short_gamma_rejected(hip):
+    x = hip.tensor(np.ones((2, 8), np.float32))
+    with pytest.raises(hip.CloveError):
+        hip.layer_norm(x, hip.tensor(np.ones(4, np.float32)), hip.tensor(np.ones(8, np.float32)))

@@ -1,0 +1,359 @@
+"""Pins of the CPU oracle (CPU only).
+
+The oracle restates Clove's Rayon kernels; these tests pin it against
+(1) Clove's own known-answer tests (tests/golden/clove_kats.json),
+(2) independent float64 library implementations (numpy, torch, scipy),
+(3) closed forms and invariants chosen so that a plausible mistake -- a
+wrong broadcast index, a transposed operand, an unbiased variance, eps
+outside the square root, a fused multiply-add, a pairwise instead of a
+sequential sum, a wrong block-table index -- fails at least one of them.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close, rng
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "clove_kats.json")
+
+
+@pytest.fixture(scope="module")
+def kats():
+    with open(GOLDEN) as f:
+        return json.load(f)
+
+
+# ---------------------------------------------------------------------------
+# Clove's own known answers
+# ---------------------------------------------------------------------------
+
+def test_kat_sub_mul(kats):
+    for name, fn in (("sub", oracle.sub), ("mul", oracle.mul)):
+        k = kats[name]
+        out = fn(np.array(k["a"], np.float32), np.array(k["b"], np.float32))
+        assert np.array_equal(out, np.array(k["out"], np.float32)), name
+
+
+def test_kat_trig(kats):
+    for name, fn in (("sin", oracle.sin), ("cos", oracle.cos)):
+        k = kats[name]
+        out = fn(np.array(k["x"], np.float32))
+        assert np.all(np.abs(out - np.array(k["out"])) < k["tol"]), name
+
+
+def test_kat_linear_relu(kats):
+    k = kats["linear_relu"]
+    x, w, b = (np.array(k[n], np.float32) for n in ("x", "w", "b"))
+    out = oracle.relu(oracle.add(oracle.matmul(x, w), b))
+    assert np.all(np.abs(out - np.array(k["out"])) < k["tol"])
+
+
+# ---------------------------------------------------------------------------
+# elementwise
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("nb", [1, 3, 4, 7, 12, 64])
+def test_binary_broadcast_matches_numpy(nb):
+    g = rng(10 + nb)
+    a = g.standard_normal((8, 96), dtype=np.float32)
+    b = g.standard_normal(nb, dtype=np.float32)
+    bb = np.resize(b, a.size).reshape(a.shape)  # b[i % nb], built independently
+    assert np.array_equal(oracle.add(a, b), a + bb)
+    assert np.array_equal(oracle.sub(a, b), a - bb)
+    assert np.array_equal(oracle.mul(a, b), a * bb)
+
+
+def test_mul_scalar_and_relu_exact():
+    g = rng(11)
+    a = g.standard_normal(1000, dtype=np.float32)
+    a[:4] = [0.0, -0.0, np.inf, -np.inf]
+    assert np.array_equal(oracle.mul_scalar(a, 0.37), a * np.float32(0.37))
+    r = oracle.relu(a)
+    assert np.array_equal(r, np.where(a > 0, a, np.float32(0)))
+    assert not np.signbit(r[1])  # relu(-0.0) is +0.0 (the `else { 0.0 }` arm)
+    assert np.isnan(oracle.relu(np.array([np.nan], np.float32)))[0] == False  # NaN > 0 is false
+
+
+def test_gelu_against_torch_float64():
+    torch = pytest.importorskip("torch")
+    g = rng(12)
+    x = np.concatenate([g.standard_normal(20000, dtype=np.float32) * 3,
+                        np.linspace(-10, 10, 2001, dtype=np.float32)])
+    want = torch.nn.functional.gelu(torch.from_numpy(x.astype(np.float64)),
+                                    approximate="tanh").numpy()
+    assert_close(oracle.gelu(x), want, rtol=2e-6, atol=2e-7, what="gelu")
+    assert oracle.gelu(np.zeros(1, np.float32))[0] == 0.0
+
+
+def test_gelu_uses_f32_sqrt_2_over_pi():
+    # (2/pi).sqrt() in f32 is 0x3F4C4229; the WGSL literal 0.7978845608 is one
+    # ulp higher.  Evaluate both step by step in numpy f32 (IEEE, no FMA) and
+    # check the oracle matches the f32 constant on inputs where they differ.
+    x = np.linspace(0.5, 3.0, 4001, dtype=np.float32)
+    f = np.float32
+    def step(k):
+        x3 = (x * x) * x
+        inner = k * (x + f(0.044715) * x3)
+        return f(0.5) * x * (f(1) + np.tanh(inner.astype(np.float64)).astype(np.float32))
+    k_cpu = np.sqrt(f(2) / f(np.pi))
+    assert k_cpu.view(np.uint32) == 0x3F4C4229
+    ref = step(k_cpu)
+    alt = step(f(0.7978845608))
+    differ = ref != alt
+    assert differ.sum() > 10
+    got = oracle.gelu(x)
+    # tanhf in glibc and numpy's f64->f32 tanh may differ by an ulp; the
+    # constant choice shows up in the majority vote on the differing inputs.
+    assert (got[differ] == ref[differ]).mean() > (got[differ] == alt[differ]).mean()
+
+
+def test_sigmoid_tanh_trig_against_float64():
+    g = rng(13)
+    x = g.standard_normal(50000, dtype=np.float32) * 4
+    xd = x.astype(np.float64)
+    assert_close(oracle.sigmoid(x), 1 / (1 + np.exp(-xd)), rtol=3e-7, atol=1e-30, what="sigmoid")
+    assert_close(oracle.tanh(x), np.tanh(xd), rtol=3e-7, atol=1e-30, what="tanh")
+    assert_close(oracle.sin(x), np.sin(xd), rtol=0, atol=2e-7, what="sin")
+    assert_close(oracle.cos(x), np.cos(xd), rtol=0, atol=2e-7, what="cos")
+
+
+# ---------------------------------------------------------------------------
+# softmax / layer norm
+# ---------------------------------------------------------------------------
+
+def test_softmax_against_torch_float64():
+    torch = pytest.importorskip("torch")
+    g = rng(14)
+    x = g.normal(0, 2, (64, 513)).astype(np.float32)
+    want = torch.softmax(torch.from_numpy(x.astype(np.float64)), dim=-1).numpy()
+    assert_close(oracle.softmax(x), want, rtol=1e-5, atol=1e-12, what="softmax")
+
+
+def test_softmax_closed_forms():
+    c = oracle.softmax(np.full((2, 4096), 3.25, np.float32))
+    assert np.all(c == np.float32(1 / 4096))          # constant row: exactly 1/n
+    oh = oracle.softmax(np.array([[0.0, 0.0, 120.0, 0.0]], np.float32))
+    # one-hot on a large gap: exp(-120) underflows to 0 in f32
+    assert oh[0, 2] == 1.0 and np.all(oh[0, [0, 1, 3]] == 0.0)
+    g = rng(15)
+    x = g.normal(0, 2, (16, 1000)).astype(np.float32)
+    s = oracle.softmax(x).astype(np.float64).sum(-1)
+    assert np.all(np.abs(s - 1) < 1000 * 6e-8)         # rows sum to 1 within n*u
+
+
+def test_layer_norm_against_torch_float64():
+    torch = pytest.importorskip("torch")
+    g = rng(16)
+    for cols, scale in ((8, 1.0), (4096, 2.0), (33, 1e-3)):
+        x = (g.standard_normal((32, cols)) * scale).astype(np.float32)
+        gamma = g.uniform(0.5, 1.5, cols).astype(np.float32)
+        beta = g.uniform(-0.1, 0.1, cols).astype(np.float32)
+        want = torch.nn.functional.layer_norm(
+            torch.from_numpy(x.astype(np.float64)), (cols,),
+            torch.from_numpy(gamma.astype(np.float64)), torch.from_numpy(beta.astype(np.float64)),
+            eps=1e-5).numpy()
+        # cols=8 separates biased from unbiased variance (a 6% difference);
+        # scale=1e-3 makes var ~ eps, which separates eps inside / outside sqrt.
+        assert_close(oracle.layer_norm(x, gamma, beta), want, rtol=1e-4, atol=1e-5,
+                     what=f"layer_norm cols={cols}")
+
+
+def test_layer_norm_constant_row_is_beta():
+    beta = np.linspace(-1, 1, 64, dtype=np.float32)
+    out = oracle.layer_norm(np.full((3, 64), 7.5, np.float32), np.full(64, 2.0, np.float32), beta)
+    assert np.array_equal(out, np.broadcast_to(beta, out.shape))
+
+
+# ---------------------------------------------------------------------------
+# matmul
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,k,n", [(1, 1, 1), (3, 5, 7), (17, 64, 9), (64, 784, 128)])
+def test_matmul_against_numpy_float64(m, k, n):
+    g = rng(17 + m)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    b = g.standard_normal((k, n)).astype(np.float32)
+    want = a.astype(np.float64) @ b.astype(np.float64)
+    scale = np.abs(a).astype(np.float64) @ np.abs(b).astype(np.float64)
+    err = np.abs(oracle.matmul(a, b) - want)
+    assert np.all(err <= k * 6e-8 * scale + 1e-30)
+
+
+def test_matmul_identity_permutation_rank1():
+    g = rng(18)
+    a = g.standard_normal((6, 9)).astype(np.float32)
+    assert np.array_equal(oracle.matmul(a, np.eye(9, dtype=np.float32)), a)
+    p = np.eye(9, dtype=np.float32)[g.permutation(9)]
+    assert np.array_equal(oracle.matmul(a, p), a @ p)  # column permutation, exact
+    u = g.standard_normal((5, 1)).astype(np.float32)
+    v = g.standard_normal((1, 4)).astype(np.float32)
+    assert np.array_equal(oracle.matmul(u, v), u * v)  # rank 1, k = 1: exact products
+
+
+def test_matmul_leading_dims():
+    g = rng(19)
+    a = g.standard_normal((2, 3, 5)).astype(np.float32)
+    b = g.standard_normal((5, 4)).astype(np.float32)
+    out = oracle.matmul(a, b)
+    assert out.shape == (2, 3, 4)
+    assert np.array_equal(out.reshape(6, 4), oracle.matmul(a.reshape(6, 5), b))
+
+
+def test_matmul_is_a_sequential_f32_fold_without_fma():
+    # Sequential f32: (1e8 + 1) rounds to 1e8, then - 1e8 gives 0; a pairwise
+    # or f64 sum gives 1.
+    a = np.array([[1e8, 1.0, -1e8]], np.float32)
+    b = np.ones((3, 1), np.float32)
+    assert oracle.matmul(a, b)[0, 0] == 0.0
+    # Separate roundings: a*b rounds before the add.  Emulate one dot product
+    # step by step with numpy f32 scalars (IEEE, never contracted).
+    g = rng(20)
+    x = g.standard_normal((1, 257)).astype(np.float32)
+    y = g.standard_normal((257, 1)).astype(np.float32)
+    s = np.float32(0)
+    for p in range(257):
+        s = np.float32(s + np.float32(x[0, p] * y[p, 0]))
+    assert oracle.matmul(x, y)[0, 0] == s
+
+
+# ---------------------------------------------------------------------------
+# paged attention
+# ---------------------------------------------------------------------------
+
+def make_paged(seed, B=3, H=2, D=64, bs=16, nb=40, max_blocks=6, ctx=None):
+    g = rng(seed)
+    kv = g.standard_normal((2, nb, bs, H, D)).astype(np.float32)
+    q = g.standard_normal((B, H, D)).astype(np.float32)
+    kn = g.standard_normal((B, H, D)).astype(np.float32)
+    vn = g.standard_normal((B, H, D)).astype(np.float32)
+    bt = g.permutation(nb)[: B * max_blocks].reshape(B, max_blocks).astype(np.int32)
+    if ctx is None:
+        ctx = g.integers(1, max_blocks * bs + 1, B)
+    cl = np.asarray(ctx, np.int32)
+    return q, kn, vn, kv, bt, cl
+
+
+def gather_reference(q, kn, vn, kv, bt, cl, scale):
+    """Contiguous K/V by explicit slot arithmetic, then torch SDPA in f64."""
+    torch = pytest.importorskip("torch")
+    _, nb, bs, H, D = kv.shape
+    out = np.zeros(q.shape, np.float64)
+    for b in range(cl.size):
+        ctx = int(cl[b])
+        if ctx == 0:
+            continue
+        slots = [int(bt[b, t // bs]) * bs + t % bs for t in range(ctx)]
+        K = kv[0].reshape(nb * bs, H, D)[slots].astype(np.float64)
+        V = kv[1].reshape(nb * bs, H, D)[slots].astype(np.float64)
+        if kn is not None:
+            K[-1], V[-1] = kn[b], vn[b]
+        qq = torch.from_numpy(q[b].astype(np.float64))[:, None, :]          # [H, 1, D]
+        KK = torch.from_numpy(np.ascontiguousarray(K.transpose(1, 0, 2)))   # [H, ctx, D]
+        VV = torch.from_numpy(np.ascontiguousarray(V.transpose(1, 0, 2)))
+        o = torch.nn.functional.scaled_dot_product_attention(qq, KK, VV, scale=float(scale))
+        out[b] = o[:, 0, :].numpy()
+    return out
+
+
+@pytest.mark.parametrize("with_new", [False, True])
+def test_paged_against_torch_sdpa(with_new):
+    q, kn, vn, kv, bt, cl = make_paged(21, ctx=[1, 37, 96])
+    if not with_new:
+        kn = vn = None
+    scale = 1 / np.sqrt(np.float32(64))
+    want = gather_reference(q, kn, vn, kv, bt, cl, scale)
+    assert_close(oracle.paged_attention(q, kn, vn, kv, bt, cl), want, 1e-5, 1e-6, "f32 oracle")
+    assert_close(oracle.paged_attention(q, kn, vn, kv, bt, cl, f64=True), want, 1e-12, 1e-14,
+                 "f64 oracle")
+
+
+def test_paged_invariants():
+    q, kn, vn, kv, bt, cl = make_paged(22, ctx=[1, 50, 80])
+    B, H, D = q.shape
+    # ctx = 1: the output is V of the single token.
+    out = oracle.paged_attention(q, None, None, kv, bt, cl)
+    slot0 = int(bt[0, 0]) * 16
+    assert np.array_equal(out[0], kv[1].reshape(-1, H, D)[slot0])
+    # q = 0: uniform weights, the output is the mean of V over the context.
+    out0 = oracle.paged_attention(np.zeros_like(q), None, None, kv, bt, cl, f64=True)
+    slots = [int(bt[1, t // 16]) * 16 + t % 16 for t in range(50)]
+    assert_close(out0[1], kv[1].reshape(-1, H, D)[slots].astype(np.float64).mean(0), 1e-12, 1e-14)
+    # V constant per head: the output is that constant, whatever the scores.
+    kv2 = kv.copy()
+    kv2[1] = np.arange(H, dtype=np.float32)[None, None, :, None] + 0.5
+    o2 = oracle.paged_attention(q, None, None, kv2, bt, cl)
+    assert_close(o2, np.broadcast_to((np.arange(H) + 0.5)[None, :, None], o2.shape), 1e-6, 0)
+
+
+def test_paged_new_token_equals_cache_write():
+    q, kn, vn, kv, bt, cl = make_paged(23, ctx=[5, 16, 17])
+    with_new = oracle.paged_attention(q, kn, vn, kv, bt, cl)
+    kv2 = kv.copy()
+    for b in range(3):
+        t = int(cl[b]) - 1
+        kv2[0, bt[b, t // 16], t % 16] = kn[b]
+        kv2[1, bt[b, t // 16], t % 16] = vn[b]
+    assert np.array_equal(with_new, oracle.paged_attention(q, None, None, kv2, bt, cl))
+
+
+def test_paged_permuted_pool_equals_contiguous():
+    # The same logical cache stored contiguously (identity table) and
+    # scattered through a permuted table gives bit-identical outputs.
+    q, kn, vn, kv, bt, cl = make_paged(24, ctx=[70, 3, 96])
+    out = oracle.paged_attention(q, None, None, kv, bt, cl)
+    B, mb = bt.shape
+    contig = np.zeros((2, B * mb) + kv.shape[2:], np.float32)
+    for b in range(B):
+        for j in range(mb):
+            contig[:, b * mb + j] = kv[:, bt[b, j]]
+    ident = np.arange(B * mb, dtype=np.int32).reshape(B, mb)
+    assert np.array_equal(out, oracle.paged_attention(q, None, None, contig, ident, cl))
+
+
+def test_paged_slots_brute_force():
+    g = rng(25)
+    bt = g.permutation(100)[:40].reshape(5, 8).astype(np.int32)
+    cl = np.array([0, 1, 16, 17, 128], np.int32)
+    got = oracle.paged_slots(bt, cl, 16, 130)
+    for b in range(5):
+        for t in range(130):
+            want = bt[b, t // 16] * 16 + t % 16 if t < cl[b] else -1
+            assert got[b, t] == want
+
+
+def test_paged_empty_context_is_zero():
+    q, kn, vn, kv, bt, cl = make_paged(26, ctx=[0, 5, 0])
+    out = oracle.paged_attention(q, None, None, kv, bt, cl)
+    assert np.all(out[0] == 0) and np.all(out[2] == 0) and np.any(out[1] != 0)
+
+
+# ---------------------------------------------------------------------------
+# compositions
+# ---------------------------------------------------------------------------
+
+def test_chain_against_float64_composition():
+    torch = pytest.importorskip("torch")
+    g = rng(27)
+    a, b, c, d = (g.standard_normal(4096).astype(np.float32) for _ in range(4))
+    ops = [("mul", -1, -2), ("add", 0, -3), ("gelu", 1), ("mul", 2, -4)]
+    (out,) = oracle.chain(ops, [a, b, c, d])
+    x = torch.from_numpy(a.astype(np.float64) * b + c)
+    want = torch.nn.functional.gelu(x, approximate="tanh").numpy() * d
+    assert_close(out, want, 1e-5, 1e-6, "gelu(a*b+c)*d")
+
+
+def test_mlp_forward_against_float64():
+    g = rng(28)
+    x = g.random((8, 20)).astype(np.float32)
+    w1 = g.uniform(-0.5, 0.5, (20, 16)).astype(np.float32)
+    b1 = g.uniform(-1, 1, (1, 16)).astype(np.float32)
+    w2 = g.uniform(-0.5, 0.5, (16, 10)).astype(np.float32)
+    b2 = g.uniform(-1, 1, (1, 10)).astype(np.float32)
+    h = np.maximum(x.astype(np.float64) @ w1 + b1, 0)
+    z = h @ w2 + b2
+    want = np.exp(z - z.max(1, keepdims=True))
+    want /= want.sum(1, keepdims=True)
+    assert_close(oracle.mlp_forward(x, w1, b1, w2, b2), want, 1e-5, 1e-9, "mlp")
