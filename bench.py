@@ -43,22 +43,26 @@ def log(*a):
 
 
 def timed(ca, launch, steps, warmup):
-    """Runs `launch` warmup + steps times.  Returns (wall ms per step,
-    per-launch kernel ms from events recorded between launches)."""
+    """Runs `launch` warmup + steps times.  Returns (wall ms per step over
+    the timed region, bracketed by device synchronisation, and the per-launch
+    ms from a HIP event pair recorded on the library's stream around every
+    launch).  Each step's output is released right away, so the caching
+    allocator hands the same block back and no hipMalloc happens in the
+    timed region."""
     for _ in range(warmup):
         launch()
     ca.synchronize()
     ca.event_reset()
+    pairs = []
     t0 = time.perf_counter()
-    evs = [ca.event_record()]
-    keep = []
     for _ in range(steps):
-        keep.append(launch())
-        evs.append(ca.event_record())
+        e0 = ca.event_record()
+        r = launch()
+        pairs.append((e0, ca.event_record()))
+        del r
     ca.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    per = np.array([ca.event_elapsed(evs[i], evs[i + 1]) for i in range(steps)])
-    del keep
+    per = np.array([ca.event_elapsed(a, b) for a, b in pairs])
     return wall, per
 
 
@@ -89,7 +93,7 @@ def bench_chain(ca, args, broadcast=False):
     if broadcast:
         ins[2] = ca.empty((4096,)).fill_normal(3)
     nbytes = 4 * n * 5 if not broadcast else 4 * n * 4 + 4 * 4096
-    wall, per = timed(ca, lambda: ca.fused_chain(CHAIN, ins), args.steps, args.warmup)
+    wall, per = timed(ca, ca.FusedChain(CHAIN, ins), args.steps, args.warmup)
     return ins, nbytes, wall, per
 
 
@@ -227,10 +231,12 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--parts", default="all",
-                    help="comma list of chain,bcast,rows,matmul,paged,mlp or 'all' / 'none'")
+                    help="comma list of copy,bcast,rows,matmul,paged,mlp or 'all' / 'none' "
+                         "(the config 2 chain always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--traffic", default=None,
-                    help="JSON file with measured HBM bytes per chain launch (rocprof counters)")
+    ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "hbm_traffic.json"),
+                    help="JSON summary of the rocprof FETCH_SIZE/WRITE_SIZE passes "
+                         "(bytes per launch of the chain kernel)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -241,7 +247,7 @@ def main():
     import clove_amd as ca
 
     ca.init(0)
-    parts = {"chain", "bcast", "rows", "matmul", "paged", "mlp"} if args.parts == "all" else \
+    parts = {"copy", "bcast", "rows", "matmul", "paged", "mlp"} if args.parts == "all" else \
         set() if args.parts == "none" else set(args.parts.split(","))
     oracle = None
     if not args.no_cpu:
@@ -279,6 +285,20 @@ def main():
     del ins
 
     out = {}
+    if "copy" in parts:
+        # A plain copy through the same chain kernel (one Flatten op): the
+        # practical streaming ceiling of this box, and the known-size kernel
+        # that calibrates the HBM byte counters.
+        src = ca.empty((4096, 4096)).fill_normal(9)
+        cwall, cper = timed(ca, ca.FusedChain([("flatten", -1)], [src]), args.steps,
+                            args.warmup)
+        cbytes = 2 * 4 * 4096 * 4096
+        gbs = cbytes / (cper.mean() * 1e-3) / 1e9
+        out["copy_reference"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(cper.mean(), 4),
+                                 "bytes": cbytes,
+                                 "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        log(f"copy reference: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+        del src
     if "bcast" in parts:
         bins, bbytes, bwall, bper = bench_chain(ca, args, broadcast=True)
         gbs = bbytes / (bper.mean() * 1e-3) / 1e9

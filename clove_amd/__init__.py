@@ -364,23 +364,36 @@ def paged_gather_indices(block_tables: Tensor, context_lens: Tensor, block_size:
                                                         block_size, max_ctx))
 
 
-def fused_chain(ops: Sequence[tuple], inputs: Sequence[Tensor]) -> list:
-    """Runs one fused elementwise chain (Step::Fused, lazy.rs:1694-1838).
+class FusedChain:
+    """A fused elementwise chain bound to its inputs (Step::Fused,
+    lazy.rs:1694-1838).  ``ops`` holds tuples ``(opname, src0, src1, store,
+    param)``; operand ``>= 0`` names an earlier op, ``< 0`` names input
+    ``-(src+1)``.  Calling it runs the chain and returns the stored values
+    (the last op always) in op order.  The argument arrays are built once,
+    so repeated calls cost one C call each."""
 
-    ``ops`` holds tuples ``(opname, src0, src1, store, param)``; operand
-    ``>= 0`` names an earlier op, ``< 0`` names input ``-(src+1)``.  Returns
-    the stored values (the last op always) in op order.
-    """
-    arr = (ChainOp * len(ops))()
-    for i, op in enumerate(ops):
-        name, s0, s1, store, param = (tuple(op) + (0, 0, 0, 0.0))[:5]
-        arr[i] = ChainOp(OP[name.upper()], s0, s1, 1 if store else 0, float(param))
-    ins = (C.c_void_p * len(inputs))(*[t.handle.value for t in inputs])
-    outs = (C.c_void_p * len(ops))()
-    n = lib().clove_hip_fused_chain(arr, len(ops), ins, len(inputs), outs)
-    if n < 0:
-        raise CloveError(-n, last_error())
-    return [Tensor(outs[i]) for i in range(n)]
+    def __init__(self, ops: Sequence[tuple], inputs: Sequence[Tensor]):
+        self._n_ops = len(ops)
+        self._ops = (ChainOp * len(ops))()
+        for i, op in enumerate(ops):
+            name, s0, s1, store, param = (tuple(op) + (0, 0, 0, 0.0))[:5]
+            self._ops[i] = ChainOp(OP[name.upper()], s0, s1, 1 if store else 0, float(param))
+        self._inputs = list(inputs)  # keeps the handles alive
+        self._n_in = len(inputs)
+        self._ins = (C.c_void_p * len(inputs))(*[t.handle.value for t in inputs])
+        self._outs = (C.c_void_p * len(ops))()
+        self._fn = lib().clove_hip_fused_chain
+
+    def __call__(self) -> list:
+        n = self._fn(self._ops, self._n_ops, self._ins, self._n_in, self._outs)
+        if n < 0:
+            raise CloveError(-n, last_error())
+        return [Tensor(self._outs[i]) for i in range(n)]
+
+
+def fused_chain(ops: Sequence[tuple], inputs: Sequence[Tensor]) -> list:
+    """Runs one fused elementwise chain once; see :class:`FusedChain`."""
+    return FusedChain(ops, inputs)()
 
 
 # ---------------------------------------------------------------------------

@@ -19,6 +19,7 @@
 //     per element with 32-bit indices and a `%` per operand per element.
 #include <hip/hiprtc.h>
 
+#include <cstdlib>
 #include <cstring>
 #include <sstream>
 #include <unordered_map>
@@ -47,6 +48,18 @@ struct Compiled {
 };
 
 std::unordered_map<std::string, Compiled> g_cache;
+
+// Launch-geometry knobs for tuning sweeps: CLOVE_CHAIN_UNROLL (vectors per
+// thread per iteration, default 4) and CLOVE_CHAIN_BLOCKS_PER_CU (grid cap,
+// default 32).  They change scheduling only, never the result.
+int env_int(const char *name, int dflt, int lo, int hi) {
+    const char *v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    const int x = std::atoi(v);
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+int chain_unroll() { return env_int("CLOVE_CHAIN_UNROLL", 4, 1, 16); }
+int chain_blocks_per_cu() { return env_int("CLOVE_CHAIN_BLOCKS_PER_CU", 32, 1, 1024); }
 
 const char *op_fn(int opcode) {
     switch (opcode) {
@@ -82,15 +95,34 @@ void division_magic(uint64_t d, unsigned int *magic, unsigned int *shift) {
     *shift = l - 1;
 }
 
+// Kernel symbol naming the chain, e.g. clove_chain_mul_add_gelu_mul_b0000
+// (the suffix lists each input's broadcast class).
+std::string kernel_name(const std::vector<ChainOp> &ops, const std::vector<int> &modes) {
+    static const char *names[] = {"input", "matmul", "add", "sub", "mul", "scale", "flatten",
+                                  "relu", "gelu", "sin", "cos", "softmax", "layernorm",
+                                  "dropout", "relugrad", "gelugrad", "cast", "sigmoid", "tanh"};
+    std::string n = "clove_chain";
+    for (size_t i = 0; i < ops.size() && i < 12; ++i) {
+        const int op = ops[i].opcode;
+        n += "_";
+        n += (op >= 0 && op < (int)(sizeof(names) / sizeof(names[0]))) ? names[op] : "op";
+    }
+    if (ops.size() > 12) n += "_more";
+    n += "_b";
+    for (int m : modes) n += char('0' + m);
+    return n;
+}
+
 std::string operand_expr(int src) {
     return src < 0 ? "x[" + std::to_string(-src - 1) + "]" : "n" + std::to_string(src);
 }
 
 std::string generate(const std::vector<ChainOp> &ops, const std::vector<int> &modes, bool wide,
-                     int nout) {
+                     int nout, const std::string &name, int unroll) {
     std::ostringstream s;
     const int nin = (int)modes.size();
     s << "#define CL_NIN " << nin << "\n#define CL_NOUT " << nout << "\n";
+    s << "#define CL_KERNEL_NAME " << name << "\n#define CL_UNROLL " << unroll << "\n";
     s << "#include \"ew_device.h\"\n";
     s << "__device__ __forceinline__ void cl_load_all(const cl_chain_args &a, unsigned long long v, cl_f4 *x) {\n";
     for (int k = 0; k < nin; ++k)
@@ -138,10 +170,11 @@ std::string signature(const std::vector<ChainOp> &ops, const std::vector<int> &m
     s << "|m";
     for (int m : modes) s << m;
     s << (wide ? "|w" : "|n");
+    s << "|u" << chain_unroll();
     return s.str();
 }
 
-Compiled compile(const std::string &src) {
+Compiled compile(const std::string &src, const std::string &name) {
     hiprtcProgram prog;
     const char *headers[] = {kAbiSrc, kDeviceSrc, kKernelSrc};
     const char *names[] = {"ew_abi.h", "ew_device.h", "ew_chain_kernel.h"};
@@ -149,7 +182,7 @@ Compiled compile(const std::string &src) {
         HIPRTC_SUCCESS)
         fail(CLOVE_HIP_ERR_JIT, "hiprtcCreateProgram failed");
     const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++17",
-                          // packed f32 arithmetic stays off (see the build notes in Makefile)
+                          // no packed-f32 instructions in any device code of this library
                           "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
     hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
     if (r != HIPRTC_SUCCESS) {
@@ -167,7 +200,7 @@ Compiled compile(const std::string &src) {
     hiprtcDestroyProgram(&prog);
     Compiled c;
     CLOVE_HIP_CHECK(hipModuleLoadData(&c.module, code.data()));
-    CLOVE_HIP_CHECK(hipModuleGetFunction(&c.fn, c.module, "cl_chain"));
+    CLOVE_HIP_CHECK(hipModuleGetFunction(&c.fn, c.module, name.c_str()));
     return c;
 }
 
@@ -269,17 +302,18 @@ void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *
     const std::string sig = signature(ops, modes, wide);
     auto it = g_cache.find(sig);
     if (it == g_cache.end()) {
-        Compiled comp = compile(generate(ops, modes, wide, nstore));
+        const std::string name = kernel_name(ops, modes);
+        Compiled comp = compile(generate(ops, modes, wide, nstore, name, chain_unroll()), name);
         it = g_cache.emplace(sig, comp).first;
     }
 
-    // Grid: enough 256-thread blocks to cover the vectors once with an
-    // unroll of 4, capped at 32 blocks per CU (a grid-stride loop covers the
-    // rest).
-    const uint64_t per_block = 256ull * 4;
+    // Grid: enough 256-thread blocks to cover the vectors once at the
+    // chain's unroll, capped at a number of blocks per CU (a grid-stride loop
+    // covers the rest).
+    const uint64_t per_block = 256ull * chain_unroll();
     uint64_t blocks = (args.nvec + per_block - 1) / per_block;
     if (blocks == 0) blocks = (numel + 255) / 256;
-    const uint64_t cap = (uint64_t)c.num_cus * 32;
+    const uint64_t cap = (uint64_t)c.num_cus * chain_blocks_per_cu();
     if (blocks > cap) blocks = cap;
     if (blocks == 0) blocks = 1;
     void *params[] = {&args};

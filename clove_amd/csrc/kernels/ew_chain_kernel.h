@@ -4,6 +4,8 @@
 //   CL_NIN, CL_NOUT          number of inputs and of stored values
 //   cl_load_all<T>(a, i, x)  loads every input at vector/element i into x[]
 //   cl_body<T>(x, prm, y)    the chain itself, T = float or cl_f4
+//   CL_KERNEL_NAME           the kernel's symbol (it names the chain's ops,
+//                            so profiles show which chain ran)
 // Each thread streams CL_UNROLL 16-byte vectors per input per iteration
 // (all loads issued before any arithmetic), walking the index space with a
 // grid stride; a scalar loop finishes the elements past the last full vector.
@@ -14,7 +16,7 @@
 #endif
 #define CL_BLOCK 256
 
-extern "C" __global__ void __launch_bounds__(CL_BLOCK) cl_chain(cl_chain_args a) {
+extern "C" __global__ void __launch_bounds__(CL_BLOCK) CL_KERNEL_NAME(cl_chain_args a) {
     const unsigned long long nvec = a.nvec;
     const unsigned long long tile = (unsigned long long)CL_BLOCK * CL_UNROLL;
     const unsigned long long stride = (unsigned long long)gridDim.x * tile;

@@ -37,6 +37,14 @@ namespace {
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 
+struct GemmArgs {
+    const float *A, *B;
+    float *C;
+    float *ws;        // split-K partial tiles [splits][tiles][BM*BN]
+    int32_t *tickets; // [tiles], zero before and after each launch
+    int M, N, K, tiles_n, k_per_split, splits;
+};
+
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmCfg {
     static constexpr int kThreads = 256;
@@ -121,16 +129,20 @@ __device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, c
 }
 
 template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC>
-__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float *__restrict__ A,
-                                                            const float *__restrict__ B,
-                                                            float *__restrict__ C, int M, int N,
-                                                            int K, int tiles_n) {
+__global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
     __shared__ __attribute__((aligned(16))) float smem[2 * (Cfg::kSizeA + Cfg::kSizeB)];
+    __shared__ int s_last;
+    const float *__restrict__ A = g.A;
+    const float *__restrict__ B = g.B;
+    const int M = g.M, N = g.N, K = g.K;
 
     const int tile = blockIdx.x;
-    const int m0 = (tile / tiles_n) * BM;
-    const int n0 = (tile % tiles_n) * BN;
+    const int split = blockIdx.y;
+    const int m0 = (tile / g.tiles_n) * BM;
+    const int n0 = (tile % g.tiles_n) * BN;
+    const int k_begin = split * g.k_per_split;
+    const int k_len = min(g.k_per_split, K - k_begin);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -148,9 +160,9 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float *__restr
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
     f4 ra[Cfg::kLoadsA], rb[Cfg::kLoadsB];
-    const int slabs = (K + BK - 1) / BK;
+    const int slabs = (k_len + BK - 1) / BK;
 
-    load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, 0, ra, rb);
+    load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, k_begin, ra, rb);
     store_slab<Cfg, BK, BN>(smem, smem + Cfg::kSizeA, ra, rb);
     __syncthreads();
 
@@ -158,21 +170,22 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float *__restr
         float *sA = smem + (s & 1) * (Cfg::kSizeA + Cfg::kSizeB);
         float *sB = sA + Cfg::kSizeA;
         const bool more = s + 1 < slabs;
-        if (more) load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, (s + 1) * BK, ra, rb);
+        if (more)
+            load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, k_begin + (s + 1) * BK, ra, rb);
 
 #pragma unroll
-        for (int g = 0; g < BK / 8; ++g) {
+        for (int gk = 0; gk < BK / 8; ++gk) {
             f4 a[Cfg::kBlocksM];
             float b[Cfg::kBlocksN][4];
 #pragma unroll
             for (int i = 0; i < Cfg::kBlocksM; ++i)
                 a[i] = *reinterpret_cast<const f4 *>(sA + (wm0 + 32 * i + l32) * Cfg::kPitchA +
-                                                     8 * g + 4 * h);
+                                                     8 * gk + 4 * h);
 #pragma unroll
             for (int j = 0; j < Cfg::kBlocksN; ++j)
 #pragma unroll
                 for (int t = 0; t < 4; ++t)
-                    b[j][t] = sB[(8 * g + 4 * h + t) * Cfg::kPitchB + wn0 + 32 * j + l32];
+                    b[j][t] = sB[(8 * gk + 4 * h + t) * Cfg::kPitchB + wn0 + 32 * j + l32];
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -190,47 +203,129 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(const float *__restr
         __syncthreads();
     }
 
-    // Epilogue: accumulator element e of block (i, j) is C[row][col] with
-    // row = 8*(e/4) + 4*h + e%4 and col = l%32 inside the 32x32 block.
+    // Accumulator element e of block (i, j) is tile element (r, c) with
+    // r = wm0 + 32*i + 8*(e/4) + 4*h + e%4 and c = wn0 + 32*j + l%32.
+    if (g.splits == 1) {
+#pragma unroll
+        for (int i = 0; i < Cfg::kBlocksM; ++i)
+#pragma unroll
+            for (int j = 0; j < Cfg::kBlocksN; ++j)
+#pragma unroll
+                for (int e = 0; e < 16; ++e) {
+                    const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
+                    const int col = n0 + wn0 + 32 * j + l32;
+                    if (!EDGE || (row < M && col < N)) g.C[(size_t)row * N + col] = acc[i][j][e];
+                }
+        return;
+    }
+
+    // Split-K: park this split's tile, then the last split of the tile to
+    // finish sums all splits in split order (deterministic) and writes C.
+    const int tiles = gridDim.x;
+    float *part = g.ws + ((size_t)split * tiles + tile) * (BM * BN);
 #pragma unroll
     for (int i = 0; i < Cfg::kBlocksM; ++i)
 #pragma unroll
         for (int j = 0; j < Cfg::kBlocksN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
-                const int col = n0 + wn0 + 32 * j + l32;
-                if (!EDGE || (row < M && col < N)) C[(size_t)row * N + col] = acc[i][j][e];
+                const int r = wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
+                const int c = wn0 + 32 * j + l32;
+                part[r * BN + c] = acc[i][j][e];
             }
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) s_last = atomicAdd(g.tickets + tile, 1) == g.splits - 1;
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    for (int idx = threadIdx.x; idx < BM * BN / 4; idx += Cfg::kThreads) {
+        const int r = (4 * idx) / BN, c = (4 * idx) % BN;
+        f4 sum = *reinterpret_cast<const f4 *>(g.ws + (size_t)tile * (BM * BN) + 4 * idx);
+        for (int sp = 1; sp < g.splits; ++sp)
+            sum += *reinterpret_cast<const f4 *>(g.ws + ((size_t)sp * tiles + tile) * (BM * BN) + 4 * idx);
+        const int row = m0 + r, col = n0 + c;
+        if (row < M) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                if (col + q < N) g.C[(size_t)row * N + col + q] = sum[q];
+        }
+    }
+    if (threadIdx.x == 0) g.tickets[tile] = 0;
 }
 
+// Tile configurations: (BM, BN, BK, WM, WN).
+enum { CFG_32x128 = 0, CFG_64x64 = 1, CFG_128x128 = 2, CFG_128x128_K32 = 3, CFG_256x128 = 4,
+       CFG_128x256 = 5, CFG_COUNT = 6 };
+const int kCfgBM[CFG_COUNT] = {32, 64, 128, 128, 256, 128};
+const int kCfgBN[CFG_COUNT] = {128, 64, 128, 128, 128, 256};
+const int kCfgBK[CFG_COUNT] = {32, 16, 16, 32, 16, 16};
+
 template <int BM, int BN, int BK, int WM, int WN>
-void launch_cfg(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s) {
-    const int tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
-    const bool vec = (K % 4 == 0) && (N % 4 == 0) &&
-                     ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) == 0;
-    const bool interior = vec && (M % BM == 0) && (N % BN == 0) && (K % BK == 0);
-    const dim3 grid((unsigned)(tm * tn));
-    if (interior)
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
-    else if (vec)
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
+void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
+    const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
+    if (p.interior)
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true><<<grid, 256, 0, s>>>(g);
+    else if (p.vec)
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true><<<grid, 256, 0, s>>>(g);
     else
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false><<<grid, 256, 0, s>>>(A, B, C, M, N, K, tn);
+        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false><<<grid, 256, 0, s>>>(g);
 }
 
 }  // namespace
 
-void gemm_f32(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s) {
-    if (M <= 0 || N <= 0) return;
-    if (K <= 0) {
-        (void)hipMemsetAsync(C, 0, (size_t)M * N * sizeof(float), s);
+GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg) {
+    GemmPlan p{};
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
+    if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
+    p.cfg = cfg;
+    const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
+    p.tiles_n = (N + BN - 1) / BN;
+    p.tiles = ((M + BM - 1) / BM) * p.tiles_n;
+    // Split K when the tiles alone cannot fill the chip: aim for about two
+    // workgroups per CU, each split covering at least four K slabs.
+    const int slabs = (K + BK - 1) / BK;
+    int splits = 1;
+    if (p.tiles < num_cus) {
+        splits = (2 * num_cus + p.tiles - 1) / p.tiles;
+        const int max_splits = slabs / 4 > 1 ? slabs / 4 : 1;
+        if (splits > max_splits) splits = max_splits;
+        if (splits > 64) splits = 64;
+    }
+    int slabs_per = (slabs + splits - 1) / splits;
+    p.k_per_split = slabs_per * BK;
+    p.splits = (K + p.k_per_split - 1) / p.k_per_split;
+    p.ws_floats = p.splits > 1 ? (size_t)p.splits * p.tiles * BM * BN : 0;
+    p.vec = (K % 4 == 0) && (N % 4 == 0);
+    p.interior = p.vec && (M % BM == 0) && (N % BN == 0) && (K % BK == 0) &&
+                 (p.k_per_split % BK == 0);
+    return p;
+}
+
+void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
+              int32_t *tickets, hipStream_t s) {
+    if (p.M <= 0 || p.N <= 0) return;
+    if (p.K <= 0) {
+        (void)hipMemsetAsync(C, 0, (size_t)p.M * p.N * sizeof(float), s);
         return;
     }
-    if (M <= 64)
-        launch_cfg<64, 64, 16, 32, 32>(A, B, C, M, N, K, s);
-    else
-        launch_cfg<128, 128, 16, 64, 64>(A, B, C, M, N, K, s);
+    GemmPlan q = p;
+    if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) {
+        q.vec = false;
+        q.interior = false;
+    }
+    GemmArgs g{A, B, C, ws, tickets, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits};
+    switch (q.cfg) {
+    case CFG_32x128: launch_cfg<32, 128, 32, 32, 32>(q, g, s); break;
+    case CFG_64x64: launch_cfg<64, 64, 16, 32, 32>(q, g, s); break;
+    case CFG_128x128: launch_cfg<128, 128, 16, 64, 64>(q, g, s); break;
+    case CFG_128x128_K32: launch_cfg<128, 128, 32, 64, 64>(q, g, s); break;
+    case CFG_256x128: launch_cfg<256, 128, 16, 128, 64>(q, g, s); break;
+    default: launch_cfg<128, 256, 16, 64, 128>(q, g, s); break;
+    }
 }
 
 }  // namespace k

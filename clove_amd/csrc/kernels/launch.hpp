@@ -21,7 +21,20 @@ void layer_norm_rows(const float *x, const float *gamma, const float *beta, floa
                      size_t rows, size_t cols, float eps, hipStream_t s);
 
 // gemm_f32.hip -- C[M,N] = A[M,K] . B[K,N], row-major f32, MFMA f32 accumulate.
-void gemm_f32(const float *A, const float *B, float *C, int M, int N, int K, hipStream_t s);
+struct GemmPlan {
+    int M, N, K;
+    int cfg;           // tile configuration
+    int tiles, tiles_n;
+    int splits;        // K splits (1: no workspace)
+    int k_per_split;   // multiple of the configuration's K slab
+    size_t ws_floats;  // split-K workspace
+    bool vec, interior;
+};
+// Picks the tile configuration and K split for a shape (force_cfg >= 0
+// overrides the configuration, for tuning).
+GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg);
+void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
+              int32_t *tickets, hipStream_t s);
 
 // paged_attention.hip
 struct PagedArgs {
@@ -35,6 +48,7 @@ struct PagedArgs {
     float *out;            // [B, H, D]
     float *partials;       // workspace: [B, H, max_parts, D + 2]
     int32_t *err_flag;     // set to 1 when a table entry used lies outside the pool
+    int32_t *counters;     // [B, H] partition tickets; zero before and after each launch
     int64_t num_blocks;    // blocks in the pool (bounds for table entries)
     int num_seqs, num_heads, head_dim, block_size, max_blocks, max_parts;
     int part_tokens;       // tokens per partition (multiple of block_size)

@@ -10,17 +10,29 @@
 // pool and, when a new token's k/v are passed, token ctx_b - 1 is read from
 // them.
 //
-// Work split (flash-decoding): the context of each (b, h) is cut into
+// Work split (flash-decoding).  The context of each (b, h) is cut into
 // partitions of `part_tokens` tokens (a whole number of KV blocks).  One
-// workgroup of four waves handles one (partition, h, b); the waves take the
-// partition's KV blocks round-robin.  Within a wave a token's head vector
-// (D floats) is spread over D/4 lanes as 16-byte loads, so one wave load
-// instruction reads 64/(D/4) whole token rows (two 512-byte rows for
-// D = 128) and every byte fetched is used.  q.k is reduced across those
-// lanes with butterflies; the online softmax keeps (max, sum, acc) per wave,
-// the waves are merged through LDS, and a partition's (max, sum, acc) goes
-// to a workspace that a second kernel merges with the log-sum-exp rule.
-// A sequence that fits one partition is written directly.
+// workgroup of four waves handles one (partition, h, b); its waves take the
+// partition's KV blocks round-robin.
+//
+// Lane layout.  A token's head row (D floats, contiguous) belongs to one
+// 16-lane DPP row of the wave: lane c of the row holds the 16-byte pieces
+// at floats 4c, 64+4c, ... (D/64 pieces).  One wave load therefore reads
+// four whole token rows in 256-byte contiguous runs, every byte fetched is
+// used, and q.k is reduced inside the DPP row with four full-rate
+// v_add_f32_dpp (quad_perm 1032, quad_perm 2301, row_ror 4, row_ror 8) --
+// no LDS traffic.  A KV block (16 tokens) is 4 such loads for K and 4 for
+// V per piece; all of them are issued before any arithmetic so a wave keeps
+// 16 KiB in flight.  Only the block that holds token ctx-1 can be partial
+// or carry the new token; it alone takes the per-token checked path.
+//
+// Softmax.  Each wave keeps a running (max, sum, acc) (online softmax); the
+// four waves are merged through LDS; a partition's (max, sum, acc) goes to a
+// workspace, and the LAST workgroup of the (b, h) to finish (an atomic
+// ticket per (b, h)) merges the partitions with the log-sum-exp rule and
+// writes the output.  The ticket counters reset themselves, so they are zero
+// at the start of every launch.  exp is the hardware 2^x of x*log2(e)
+// (relative error ~1e-6, far below the 2e-3 parity bound).
 //
 // Safety: context lengths are clamped to the table's capacity and table
 // entries outside [0, num_blocks) are skipped; both set a device error flag
@@ -54,168 +66,215 @@ __device__ __forceinline__ int clamp_ctx(const PagedArgs &a, int b, bool report)
     return ctx;
 }
 
+__device__ __forceinline__ float fast_exp(float x) {
+    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(
+        float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a DPP row; every lane of the row gets the sum.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp<0x124>(v);  // row_ror 4
+    v += dpp<0x128>(v);  // row_ror 8
+    return v;
+}
+
+__device__ __forceinline__ float dot4(cl_f4 a, cl_f4 b) {
+    return (a.x * b.x + a.y * b.y) + (a.z * b.z + a.w * b.w);
+}
+
+struct WaveState {
+    float m, l;
+};
+
+// Folds one KV block into the wave's running softmax state.  `kb`/`vb`
+// point at this lane's first piece of the block's row `row`; rows advance
+// by 4 per step.  CHECKED handles a partial block and the new-token row.
+template <int D, int BS, bool CHECKED>
+__device__ __forceinline__ void fold_block(const PagedArgs &a, const float *kb, const float *vb,
+                                           size_t row_stride, int t0, int t_end, int ctx,
+                                           int row, size_t new_off, const cl_f4 (&q)[D / 64],
+                                           WaveState &st, cl_f4 (&o)[D / 64]) {
+    constexpr int NV = D / 64;
+    constexpr int STEPS = BS / 4;
+    cl_f4 kk[STEPS][NV], vv[STEPS][NV];
+    bool in[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const int t = t0 + 4 * s + row;
+        in[s] = !CHECKED || t < t_end;
+        const bool fresh = CHECKED && a.k_new != nullptr && t == ctx - 1;
+        const float *kp = fresh ? a.k_new + new_off : kb + (size_t)(4 * s) * row_stride;
+        const float *vp = fresh ? a.v_new + new_off : vb + (size_t)(4 * s) * row_stride;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) {
+            if (in[s]) {
+                kk[s][j] = *reinterpret_cast<const cl_f4 *>(kp + 64 * j);
+                vv[s][j] = *reinterpret_cast<const cl_f4 *>(vp + 64 * j);
+            } else {
+                kk[s][j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
+                vv[s][j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
+            }
+        }
+    }
+    float sc[STEPS];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        float d = dot4(q[0], kk[s][0]);
+#pragma unroll
+        for (int j = 1; j < NV; ++j) d += dot4(q[j], kk[s][j]);
+        d = row16_sum(d);
+        sc[s] = in[s] ? d * a.scale : -INFINITY;
+        bm = fmaxf(bm, sc[s]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float m_new = fmaxf(st.m, bm);
+    const float alpha = (st.m == -INFINITY) ? 0.0f : fast_exp(st.m - m_new);
+    st.l *= alpha;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) o[j] *= alpha;
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) {
+        const float p = in[s] ? fast_exp(sc[s] - m_new) : 0.0f;
+        st.l += p;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) o[j] += p * vv[s][j];
+    }
+    st.m = m_new;
+}
+
 template <int D, int BS>
 __global__ void __launch_bounds__(256) paged_partition_kernel(PagedArgs a) {
-    constexpr int LPT = D / 4;      // lanes per token row
-    constexpr int TPL = 64 / LPT;   // token rows per wave load
-    constexpr int STEPS = BS / TPL; // wave loads per KV block
-    static_assert(BS % TPL == 0, "block size must be a multiple of the rows per load");
+    constexpr int NV = D / 64;
+    static_assert(BS % 4 == 0 && D % 64 == 0, "4 rows per wave load, 64 floats per piece row");
     __shared__ float s_o[4][D];
     __shared__ float s_m[4], s_l[4];
+    __shared__ int s_last;
 
     const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row = lane >> 4, c16 = lane & 15;
+    const int H = a.num_heads;
+    const size_t head_off = ((size_t)b * H + h) * D;
     const int ctx = clamp_ctx(a, b, part == 0 && h == 0 && threadIdx.x == 0);
     const int t_begin = part * a.part_tokens;
-    if (t_begin >= ctx) return;
+    if (t_begin >= ctx) {
+        if (ctx == 0 && part == 0 && (int)threadIdx.x < D) a.out[head_off + threadIdx.x] = 0.0f;
+        return;
+    }
     const int t_end = min(t_begin + a.part_tokens, ctx);
-    const int H = a.num_heads;
-    const int sub = lane / LPT;     // which token row of a load group
-    const int dl = lane % LPT;      // 16-byte column within the row
+    const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
 
-    const size_t head_off = ((size_t)b * H + h) * D;
-    const cl_f4 q = *reinterpret_cast<const cl_f4 *>(a.q + head_off + 4 * dl);
+    cl_f4 q[NV], o[NV];
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        q[j] = *reinterpret_cast<const cl_f4 *>(a.q + head_off + 64 * j + 4 * c16);
+        o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
+    }
     const int32_t *bt = a.block_tables + (size_t)b * a.max_blocks;
-    const bool has_new = a.k_new != nullptr;
     const size_t row_stride = (size_t)H * D;  // floats between consecutive slots
-
-    float m = -INFINITY, l = 0.0f;
-    cl_f4 o = {0.f, 0.f, 0.f, 0.f};
+    const size_t lane_off = (size_t)h * D + 4 * c16 + (size_t)row * row_stride;
+    const size_t new_off = head_off + 4 * c16;
+    WaveState st{-INFINITY, 0.0f};
 
     const int lb_first = t_begin / BS, lb_last = (t_end - 1) / BS;
+    const bool tail_checked = t_end == ctx && (ctx % BS != 0 || a.k_new != nullptr);
     for (int lb = lb_first + wave; lb <= lb_last; lb += 4) {
         const int64_t blk = bt[lb];
         if (blk < 0 || blk >= a.num_blocks) {
             if (lane == 0) atomicOr(a.err_flag, 1);
             continue;
         }
-        const size_t blk_off = (size_t)blk * BS * row_stride + (size_t)h * D + 4 * dl;
-        const float *kbase = a.k_cache + blk_off;
-        const float *vbase = a.v_cache + blk_off;
-        // All K rows of the block are loaded before any is used.
-        cl_f4 kv[STEPS];
-        bool in[STEPS];
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-            const int r = st * TPL + sub;
-            const int t = lb * BS + r;
-            in[st] = t >= t_begin && t < t_end;
-            kv[st] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-            if (in[st]) {
-                const float *kp = (has_new && t == ctx - 1) ? a.k_new + head_off + 4 * dl
-                                                            : kbase + (size_t)r * row_stride;
-                kv[st] = *reinterpret_cast<const cl_f4 *>(kp);
-            }
-        }
-        float sc[STEPS];
-        float bm = -INFINITY;
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-            float d = (q.x * kv[st].x + q.y * kv[st].y) + (q.z * kv[st].z + q.w * kv[st].w);
-#pragma unroll
-            for (int off = LPT / 2; off > 0; off >>= 1) d += __shfl_xor(d, off, 64);
-            sc[st] = in[st] ? d * a.scale : -INFINITY;
-            bm = fmaxf(bm, sc[st]);
-        }
-#pragma unroll
-        for (int off = LPT; off < 64; off <<= 1) bm = fmaxf(bm, __shfl_xor(bm, off, 64));
-        const float m_new = fmaxf(m, bm);
-        const float alpha = (m == -INFINITY) ? 0.0f : expf(m - m_new);
-        l *= alpha;
-        o *= alpha;
-        cl_f4 vv[STEPS];
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-            const int r = st * TPL + sub;
-            const int t = lb * BS + r;
-            vv[st] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-            if (in[st]) {
-                const float *vp = (has_new && t == ctx - 1) ? a.v_new + head_off + 4 * dl
-                                                            : vbase + (size_t)r * row_stride;
-                vv[st] = *reinterpret_cast<const cl_f4 *>(vp);
-            }
-        }
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) {
-            if (in[st]) {
-                const float p = expf(sc[st] - m_new);
-                l += p;
-                o += p * vv[st];
-            }
-        }
-        m = m_new;
+        const size_t off = (size_t)blk * BS * row_stride + lane_off;
+        if (tail_checked && lb == lb_last)
+            fold_block<D, BS, true>(a, a.k_cache + off, a.v_cache + off, row_stride, lb * BS,
+                                    t_end, ctx, row, new_off, q, st, o);
+        else
+            fold_block<D, BS, false>(a, a.k_cache + off, a.v_cache + off, row_stride, lb * BS,
+                                     t_end, ctx, row, new_off, q, st, o);
     }
 
-    // Merge the token-row groups of the wave (same running max in all lanes).
+    // Merge the four token rows of the wave (same running max everywhere).
+    st.l += __shfl_xor(st.l, 16, 64);
+    st.l += __shfl_xor(st.l, 32, 64);
 #pragma unroll
-    for (int off = LPT; off < 64; off <<= 1) {
-        l += __shfl_xor(l, off, 64);
-        o.x += __shfl_xor(o.x, off, 64);
-        o.y += __shfl_xor(o.y, off, 64);
-        o.z += __shfl_xor(o.z, off, 64);
-        o.w += __shfl_xor(o.w, off, 64);
+    for (int j = 0; j < NV; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            float v = o[j][c];
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            o[j][c] = v;
+        }
     }
-    if (sub == 0) *reinterpret_cast<cl_f4 *>(&s_o[wave][4 * dl]) = o;
+    if (row == 0) {
+#pragma unroll
+        for (int j = 0; j < NV; ++j) *reinterpret_cast<cl_f4 *>(&s_o[wave][64 * j + 4 * c16]) = o[j];
+    }
     if (lane == 0) {
-        s_m[wave] = m;
-        s_l[wave] = l;
+        s_m[wave] = st.m;
+        s_l[wave] = st.l;
     }
     __syncthreads();
 
     // Merge the four waves: thread d < D owns output element d.
     const int d = threadIdx.x;
+    float M = -INFINITY, L = 0.0f, O = 0.0f;
     if (d < D) {
-        float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w]);
-        float L = 0.0f, O = 0.0f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
             if (s_m[w] == -INFINITY) continue;
-            const float e = expf(s_m[w] - M);
+            const float e = fast_exp(s_m[w] - M);
             L += s_l[w] * e;
             O += s_o[w][d] * e;
         }
-        if (ctx <= a.part_tokens) {
-            a.out[head_off + d] = O / L;
-        } else {
-            float *p = a.partials + (((size_t)b * H + h) * a.max_parts + part) * (D + 2);
-            p[d] = O;
-            if (d == 0) {
-                p[D] = M;
-                p[D + 1] = L;
-            }
-        }
     }
-}
-
-// Merges the partitions of each (b, h): out = sum_p O_p e^(M_p - M) /
-// sum_p L_p e^(M_p - M).  Also writes zeros for empty contexts.
-__global__ void __launch_bounds__(256) paged_merge_kernel(PagedArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int D = a.head_dim;
-    const int d = threadIdx.x;
-    if (d >= D) return;
-    const int ctx = clamp_ctx(a, b, false);
-    const size_t head_off = ((size_t)b * a.num_heads + h) * D;
-    if (ctx <= 0) {
-        a.out[head_off + d] = 0.0f;
+    if (n_parts == 1) {
+        if (d < D) a.out[head_off + d] = O / L;
         return;
     }
-    const int parts = (ctx + a.part_tokens - 1) / a.part_tokens;
-    if (parts <= 1) return;
-    const float *p = a.partials + ((size_t)b * a.num_heads + h) * a.max_parts * (D + 2);
-    float M = -INFINITY;
-    for (int i = 0; i < parts; ++i) M = fmaxf(M, p[i * (D + 2) + D]);
-    float L = 0.0f, O = 0.0f;
-    for (int i = 0; i < parts; ++i) {
-        const float mi = p[i * (D + 2) + D];
-        if (mi == -INFINITY) continue;
-        const float e = expf(mi - M);
-        L += p[i * (D + 2) + D + 1] * e;
-        O += p[i * (D + 2) + d] * e;
+    float *ws = a.partials + ((size_t)b * H + h) * a.max_parts * (D + 2);
+    if (d < D) {
+        ws[part * (D + 2) + d] = O;
+        if (d == 0) {
+            ws[part * (D + 2) + D] = M;
+            ws[part * (D + 2) + D + 1] = L;
+        }
     }
-    a.out[head_off + d] = O / L;
+    // Last workgroup of this (b, h) merges every partition.
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int ticket = atomicAdd(a.counters + (size_t)b * H + h, 1);
+        s_last = ticket == n_parts - 1;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (d < D) {
+        float gm = -INFINITY;
+        for (int p = 0; p < n_parts; ++p) gm = fmaxf(gm, ws[p * (D + 2) + D]);
+        float gl = 0.0f, go = 0.0f;
+        for (int p = 0; p < n_parts; ++p) {
+            const float mp = ws[p * (D + 2) + D];
+            if (mp == -INFINITY) continue;
+            const float e = fast_exp(mp - gm);
+            gl += ws[p * (D + 2) + D + 1] * e;
+            go += ws[p * (D + 2) + d] * e;
+        }
+        a.out[head_off + d] = go / gl;
+    }
+    if (threadIdx.x == 0) a.counters[(size_t)b * H + h] = 0;
 }
 
 __global__ void __launch_bounds__(256) paged_slots_kernel(const int32_t *__restrict__ bt,
@@ -267,7 +326,6 @@ void paged_attention(const PagedArgs &a, hipStream_t s) {
     CLOVE_PAGED_CASE(256, 8) CLOVE_PAGED_CASE(256, 16) CLOVE_PAGED_CASE(256, 32)
     { return; }
 #undef CLOVE_PAGED_CASE
-    paged_merge_kernel<<<dim3((unsigned)a.num_heads, (unsigned)a.num_seqs), 256, 0, s>>>(a);
 }
 
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,

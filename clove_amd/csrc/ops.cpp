@@ -8,6 +8,7 @@
 // lazy planner emits for longer chains, so eager and fused results are
 // produced by identical device code.
 #include <cmath>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "kernels/launch.hpp"
@@ -141,12 +142,27 @@ static void matmul_dims(const Tensor &a, const Tensor &b, size_t *m, size_t *k, 
                   CLOVE_HIP_ERR_SHAPE, "matmul dimensions exceed 2^31");
 }
 
+// CLOVE_GEMM_CFG selects a tile configuration by index (tuning sweeps only;
+// every configuration computes the same product).
+static int gemm_cfg_override() {
+    const char *v = std::getenv("CLOVE_GEMM_CFG");
+    return (v && *v) ? std::atoi(v) : -1;
+}
+
 void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out) {
     need_f32(a, "a");
     need_f32(b, "b");
     size_t m, kk, n;
     matmul_dims(a, b, &m, &kk, &n);
-    k::gemm_f32(a.f32(), b.f32(), out.f32(), (int)m, (int)n, (int)kk, ctx().stream);
+    Context &c = ctx();
+    const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override());
+    TensorNode ws;
+    int32_t *tickets = nullptr;
+    if (p.ws_floats) {
+        ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
+        tickets = zeroed_counters((size_t)p.tiles);
+    }
+    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, tickets, c.stream);
 }
 
 // backend.rs:1282-1306: m = prod(a.shape[..last]), k = a.shape[last],
@@ -210,6 +226,7 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
     a.context_lens = cl.i32();
     a.out = out.f32();
     a.err_flag = device_error_flag();
+    a.counters = zeroed_counters(B * H);
     a.num_blocks = (int64_t)nb;
     a.num_seqs = (int)B;
     a.num_heads = (int)H;
