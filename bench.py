@@ -7,10 +7,11 @@ the headline metric is quoted on), with every input already resident in HBM.
 Rank 0 prints ONE JSON line on stdout:
 
   value        whole-job algorithmic HBM GB/s of the step (5 x 64 MiB per step)
-  roofline     the chain kernel: algorithmic bytes / mean kernel duration
-               (HIP events around every launch of the timed region) vs the
-               8 TB/s HBM3E peak; `traffic` is the measured HBM bytes per
-               launch when a rocprof counter summary is supplied (--traffic)
+  roofline     the chain kernel: algorithmic bytes / mean launch duration
+               (two HIP events on the library's stream bracketing the K
+               back-to-back launches of the timed region) vs the 8 TB/s HBM3E
+               peak; `traffic` is the measured HBM bytes per launch from the
+               rocprof FETCH_SIZE / WRITE_SIZE summary in profiles/
   cpu_baseline the CPU restatement of Clove's Rayon kernels (oracle/), four
                unfused passes as Clove's eager CPU path runs them, timed on
                this host's cores
@@ -42,28 +43,36 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+class Timing:
+    """wall: host ms per step over the timed region (device synchronised on
+    both sides); kernel: device ms per launch from the two HIP events that
+    bracket the launches on the library's stream."""
+
+    def __init__(self, wall, kernel):
+        self.wall, self.kernel = wall, kernel
+
+    def mean(self):
+        return self.kernel
+
+
 def timed(ca, launch, steps, warmup):
-    """Runs `launch` warmup + steps times.  Returns (wall ms per step over
-    the timed region, bracketed by device synchronisation, and the per-launch
-    ms from a HIP event pair recorded on the library's stream around every
-    launch).  Each step's output is released right away, so the caching
-    allocator hands the same block back and no hipMalloc happens in the
-    timed region."""
+    """Runs `launch` warmup + steps times back to back.  Each step's output
+    is released right away, so the caching allocator hands the same block
+    back and no hipMalloc happens in the timed region; no event sits between
+    two launches."""
     for _ in range(warmup):
         launch()
     ca.synchronize()
     ca.event_reset()
-    pairs = []
     t0 = time.perf_counter()
+    e0 = ca.event_record()
     for _ in range(steps):
-        e0 = ca.event_record()
         r = launch()
-        pairs.append((e0, ca.event_record()))
         del r
+    e1 = ca.event_record()
     ca.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    per = np.array([ca.event_elapsed(a, b) for a, b in pairs])
-    return wall, per
+    return wall, Timing(wall, ca.event_elapsed(e0, e1) / steps)
 
 
 def cpu_time(fn, reps=3):

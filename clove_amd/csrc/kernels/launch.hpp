@@ -34,7 +34,7 @@ struct GemmPlan {
 // overrides the configuration, for tuning).
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
-              int32_t *tickets, hipStream_t s);
+              hipStream_t s);
 
 // paged_attention.hip
 struct PagedArgs {
@@ -48,7 +48,6 @@ struct PagedArgs {
     float *out;            // [B, H, D]
     float *partials;       // workspace: [B, H, max_parts, D + 2]
     int32_t *err_flag;     // set to 1 when a table entry used lies outside the pool
-    int32_t *counters;     // [B, H] partition tickets; zero before and after each launch
     int64_t num_blocks;    // blocks in the pool (bounds for table entries)
     int num_seqs, num_heads, head_dim, block_size, max_blocks, max_parts;
     int part_tokens;       // tokens per partition (multiple of block_size)
@@ -57,7 +56,7 @@ struct PagedArgs {
 // Workspace floats needed for a given shape (0 when one partition suffices).
 size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max_ctx,
                               int part_tokens);
-int paged_part_tokens(int head_dim, int block_size);
+int paged_part_tokens(int num_seqs, int num_heads, int capacity, int block_size, int num_cus);
 // Head dims 64/128/256 and block sizes 8/16/32 have kernels.
 bool paged_supported(int head_dim, int block_size);
 void paged_attention(const PagedArgs &a, hipStream_t s);

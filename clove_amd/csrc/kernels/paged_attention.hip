@@ -12,8 +12,13 @@
 //
 // Work split (flash-decoding).  The context of each (b, h) is cut into
 // partitions of `part_tokens` tokens (a whole number of KV blocks).  One
-// workgroup of four waves handles one (partition, h, b); its waves take the
-// partition's KV blocks round-robin.
+// workgroup handles one partition of one sequence for four adjacent heads,
+// one wave per head.  Measured on MI355X at the benchmark shape
+// (B=32, H=32, D=128, ctx 512..4096): head-major waves with 2048-token
+// partitions stream at ~6 TB/s, against ~5.1 TB/s when the four waves split
+// one head's KV blocks (each workgroup then reads 512-byte rows at a 16 KiB
+// stride while the neighbouring heads of the same tokens are read at
+// unrelated times).
 //
 // Lane layout.  A token's head row (D floats, contiguous) belongs to one
 // 16-lane DPP row of the wave: lane c of the row holds the 16-byte pieces
@@ -26,13 +31,13 @@
 // 16 KiB in flight.  Only the block that holds token ctx-1 can be partial
 // or carry the new token; it alone takes the per-token checked path.
 //
-// Softmax.  Each wave keeps a running (max, sum, acc) (online softmax); the
-// four waves are merged through LDS; a partition's (max, sum, acc) goes to a
-// workspace, and the LAST workgroup of the (b, h) to finish (an atomic
-// ticket per (b, h)) merges the partitions with the log-sum-exp rule and
-// writes the output.  The ticket counters reset themselves, so they are zero
-// at the start of every launch.  exp is the hardware 2^x of x*log2(e)
-// (relative error ~1e-6, far below the 2e-3 parity bound).
+// Softmax.  Each wave keeps a running (max, sum, acc) (online softmax); a
+// partition's (max, sum, acc) goes to a workspace that a one-wave-per-(b, h)
+// kernel merges with the log-sum-exp rule (a device-wide fence plus ticket
+// inside the partition kernel would write back the per-XCD L2s and costs
+// far more than the second launch).
+// exp is the hardware 2^x of x*log2(e) (relative error ~1e-6, far below the
+// 2e-3 parity bound).
 //
 // Safety: context lengths are clamped to the table's capacity and table
 // entries outside [0, num_blocks) are skipped; both set a device error flag
@@ -42,6 +47,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 
 #include "launch.hpp"
 #include "wave.h"
@@ -151,23 +157,79 @@ __device__ __forceinline__ void fold_block(const PagedArgs &a, const float *kb, 
     st.m = m_new;
 }
 
-template <int D, int BS>
-__global__ void __launch_bounds__(256) paged_partition_kernel(PagedArgs a) {
+// Folds NB whole KV blocks (every row in range, no new-token row) into the
+// running state in one step: the K and V rows of all NB blocks are issued
+// before any arithmetic, so a wave keeps NB * 16 KiB in flight.  `off[n]`
+// is this lane's offset of block n's row `row` in a plane.
+template <int D, int BS, int NB>
+__device__ __forceinline__ void fold_full(const PagedArgs &a, const size_t (&off)[NB],
+                                          size_t row_stride, const cl_f4 (&q)[D / 64],
+                                          WaveState &st, cl_f4 (&o)[D / 64]) {
     constexpr int NV = D / 64;
-    static_assert(BS % 4 == 0 && D % 64 == 0, "4 rows per wave load, 64 floats per piece row");
-    __shared__ float s_o[4][D];
-    __shared__ float s_m[4], s_l[4];
-    __shared__ int s_last;
+    constexpr int STEPS = BS / 4;
+    constexpr int T = NB * STEPS;
+    cl_f4 kk[T][NV], vv[T][NV];
+#pragma unroll
+    for (int n = 0; n < NB; ++n)
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) {
+            const float *kp = a.k_cache + off[n] + (size_t)(4 * s) * row_stride;
+            const float *vp = a.v_cache + off[n] + (size_t)(4 * s) * row_stride;
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                kk[n * STEPS + s][j] = *reinterpret_cast<const cl_f4 *>(kp + 64 * j);
+                vv[n * STEPS + s][j] = *reinterpret_cast<const cl_f4 *>(vp + 64 * j);
+            }
+        }
+    float sc[T];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < T; ++s) {
+        float d = dot4(q[0], kk[s][0]);
+#pragma unroll
+        for (int j = 1; j < NV; ++j) d += dot4(q[j], kk[s][j]);
+        sc[s] = row16_sum(d) * a.scale;
+        bm = fmaxf(bm, sc[s]);
+    }
+    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
+    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
+    const float m_new = fmaxf(st.m, bm);
+    const float alpha = (st.m == -INFINITY) ? 0.0f : fast_exp(st.m - m_new);
+    st.l *= alpha;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) o[j] *= alpha;
+#pragma unroll
+    for (int s = 0; s < T; ++s) {
+        const float p = fast_exp(sc[s] - m_new);
+        st.l += p;
+#pragma unroll
+        for (int j = 0; j < NV; ++j) o[j] += p * vv[s][j];
+    }
+    st.m = m_new;
+}
 
-    const int part = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+// One workgroup = HPW adjacent heads of one (partition, sequence); wave w
+// owns head HPW*blockIdx.x + w for the whole partition.  The waves walk the
+// same KV blocks together, so a token's HPW head rows (HPW * D * 4 bytes,
+// contiguous in the pool) are read at the same time, and the grid's fastest
+// dimension is the head group, so neighbouring workgroups read the other
+// heads of the same tokens: the pool is streamed in long contiguous runs.
+template <int D, int BS, int HPW, int NB>
+__global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
+    constexpr int NV = D / 64;
+    const int part = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row = lane >> 4, c16 = lane & 15;
+    const int h = blockIdx.x * HPW + wave;
     const int H = a.num_heads;
+    if (h >= H) return;
+    const int row = lane >> 4, c16 = lane & 15;
     const size_t head_off = ((size_t)b * H + h) * D;
-    const int ctx = clamp_ctx(a, b, part == 0 && h == 0 && threadIdx.x == 0);
+    const int ctx = clamp_ctx(a, b, part == 0 && h == 0 && lane == 0);
     const int t_begin = part * a.part_tokens;
     if (t_begin >= ctx) {
-        if (ctx == 0 && part == 0 && (int)threadIdx.x < D) a.out[head_off + threadIdx.x] = 0.0f;
+        if (ctx == 0 && part == 0) {
+            for (int d = lane; d < D; d += 64) a.out[head_off + d] = 0.0f;
+        }
         return;
     }
     const int t_end = min(t_begin + a.part_tokens, ctx);
@@ -180,29 +242,58 @@ __global__ void __launch_bounds__(256) paged_partition_kernel(PagedArgs a) {
         o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
     }
     const int32_t *bt = a.block_tables + (size_t)b * a.max_blocks;
-    const size_t row_stride = (size_t)H * D;  // floats between consecutive slots
+    const size_t row_stride = (size_t)H * D;
     const size_t lane_off = (size_t)h * D + 4 * c16 + (size_t)row * row_stride;
     const size_t new_off = head_off + 4 * c16;
     WaveState st{-INFINITY, 0.0f};
 
     const int lb_first = t_begin / BS, lb_last = (t_end - 1) / BS;
     const bool tail_checked = t_end == ctx && (ctx % BS != 0 || a.k_new != nullptr);
-    for (int lb = lb_first + wave; lb <= lb_last; lb += 4) {
+    const int64_t nb = a.num_blocks;
+    const int full_end = tail_checked ? lb_last : lb_last + 1;  // whole blocks: [lb_first, full_end)
+    int lb = lb_first;
+    for (; lb + NB <= full_end; lb += NB) {
+        size_t off[NB];
+        bool ok = true;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int64_t blk = bt[lb + n];
+            ok = ok && blk >= 0 && blk < nb;
+            off[n] = (size_t)(ok ? blk : 0) * BS * row_stride + lane_off;
+        }
+        if (ok) {
+            fold_full<D, BS, NB>(a, off, row_stride, q, st, o);
+            continue;
+        }
+        for (int n = 0; n < NB; ++n) {  // some entry is bad: take the good ones one by one
+            const int64_t blk = bt[lb + n];
+            if (blk < 0 || blk >= nb) {
+                if (lane == 0) atomicOr(a.err_flag, 1);
+                continue;
+            }
+            const size_t one[1] = {(size_t)blk * BS * row_stride + lane_off};
+            fold_full<D, BS, 1>(a, one, row_stride, q, st, o);
+        }
+    }
+    for (; lb < full_end; ++lb) {
         const int64_t blk = bt[lb];
-        if (blk < 0 || blk >= a.num_blocks) {
+        if (blk < 0 || blk >= nb) {
             if (lane == 0) atomicOr(a.err_flag, 1);
             continue;
         }
-        const size_t off = (size_t)blk * BS * row_stride + lane_off;
-        if (tail_checked && lb == lb_last)
-            fold_block<D, BS, true>(a, a.k_cache + off, a.v_cache + off, row_stride, lb * BS,
-                                    t_end, ctx, row, new_off, q, st, o);
-        else
-            fold_block<D, BS, false>(a, a.k_cache + off, a.v_cache + off, row_stride, lb * BS,
-                                     t_end, ctx, row, new_off, q, st, o);
+        const size_t one[1] = {(size_t)blk * BS * row_stride + lane_off};
+        fold_full<D, BS, 1>(a, one, row_stride, q, st, o);
     }
-
-    // Merge the four token rows of the wave (same running max everywhere).
+    if (tail_checked) {
+        const int64_t blk = bt[lb_last];
+        if (blk < 0 || blk >= nb) {
+            if (lane == 0) atomicOr(a.err_flag, 1);
+        } else {
+            const size_t off = (size_t)blk * BS * row_stride + lane_off;
+            fold_block<D, BS, true>(a, a.k_cache + off, a.v_cache + off, row_stride, lb_last * BS,
+                                    t_end, ctx, row, new_off, q, st, o);
+        }
+    }
     st.l += __shfl_xor(st.l, 16, 64);
     st.l += __shfl_xor(st.l, 32, 64);
 #pragma unroll
@@ -215,66 +306,57 @@ __global__ void __launch_bounds__(256) paged_partition_kernel(PagedArgs a) {
             o[j][c] = v;
         }
     }
-    if (row == 0) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) *reinterpret_cast<cl_f4 *>(&s_o[wave][64 * j + 4 * c16]) = o[j];
-    }
-    if (lane == 0) {
-        s_m[wave] = st.m;
-        s_l[wave] = st.l;
-    }
-    __syncthreads();
-
-    // Merge the four waves: thread d < D owns output element d.
-    const int d = threadIdx.x;
-    float M = -INFINITY, L = 0.0f, O = 0.0f;
-    if (d < D) {
-#pragma unroll
-        for (int w = 0; w < 4; ++w) M = fmaxf(M, s_m[w]);
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-            if (s_m[w] == -INFINITY) continue;
-            const float e = fast_exp(s_m[w] - M);
-            L += s_l[w] * e;
-            O += s_o[w][d] * e;
-        }
-    }
+    if (row != 0) return;
     if (n_parts == 1) {
-        if (d < D) a.out[head_off + d] = O / L;
+        const float inv = 1.0f / st.l;
+#pragma unroll
+        for (int j = 0; j < NV; ++j)
+            *reinterpret_cast<cl_f4 *>(a.out + head_off + 64 * j + 4 * c16) = o[j] * inv;
         return;
     }
-    float *ws = a.partials + ((size_t)b * H + h) * a.max_parts * (D + 2);
-    if (d < D) {
-        ws[part * (D + 2) + d] = O;
-        if (d == 0) {
-            ws[part * (D + 2) + D] = M;
-            ws[part * (D + 2) + D + 1] = L;
-        }
+    float *ws = a.partials + (((size_t)b * H + h) * a.max_parts + part) * (D + 2);
+#pragma unroll
+    for (int j = 0; j < NV; ++j)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ws[64 * j + 4 * c16 + c] = o[j][c];
+    if (c16 == 0) {
+        ws[D] = st.m;
+        ws[D + 1] = st.l;
     }
-    // Last workgroup of this (b, h) merges every partition.
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const int ticket = atomicAdd(a.counters + (size_t)b * H + h, 1);
-        s_last = ticket == n_parts - 1;
+}
+
+// Merges the partitions of each (b, h) with the log-sum-exp rule:
+// out = sum_p O_p e^(M_p - M) / sum_p L_p e^(M_p - M).  One wave per (b, h);
+// sequences that fit one partition were written by the partition kernel.
+__global__ void __launch_bounds__(256) paged_merge_kernel(PagedArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pair >= a.num_seqs * a.num_heads) return;
+    const int b = pair / a.num_heads;
+    const int D = a.head_dim;
+    const int ctx = clamp_ctx(a, b, false);
+    const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
+    if (n_parts <= 1) return;
+    const float *ws = a.partials + (size_t)pair * a.max_parts * (D + 2);
+    float M = -INFINITY;
+#pragma unroll 8
+    for (int p = 0; p < n_parts; ++p) M = fmaxf(M, ws[p * (D + 2) + D]);
+    float L = 0.0f;
+#pragma unroll 8
+    for (int p = 0; p < n_parts; ++p) {
+        const float mp = ws[p * (D + 2) + D];
+        L += mp == -INFINITY ? 0.0f : ws[p * (D + 2) + D + 1] * fast_exp(mp - M);
     }
-    __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    if (d < D) {
-        float gm = -INFINITY;
-        for (int p = 0; p < n_parts; ++p) gm = fmaxf(gm, ws[p * (D + 2) + D]);
-        float gl = 0.0f, go = 0.0f;
+    const float invL = 1.0f / L;
+    for (int d = lane; d < D; d += 64) {
+        float O = 0.0f;
+#pragma unroll 8
         for (int p = 0; p < n_parts; ++p) {
             const float mp = ws[p * (D + 2) + D];
-            if (mp == -INFINITY) continue;
-            const float e = fast_exp(mp - gm);
-            gl += ws[p * (D + 2) + D + 1] * e;
-            go += ws[p * (D + 2) + d] * e;
+            O += mp == -INFINITY ? 0.0f : ws[p * (D + 2) + d] * fast_exp(mp - M);
         }
-        a.out[head_off + d] = go / gl;
+        a.out[(size_t)pair * D + d] = O * invL;
     }
-    if (threadIdx.x == 0) a.counters[(size_t)b * H + h] = 0;
 }
 
 __global__ void __launch_bounds__(256) paged_slots_kernel(const int32_t *__restrict__ bt,
@@ -300,9 +382,24 @@ bool paged_supported(int head_dim, int block_size) {
            (block_size == 8 || block_size == 16 || block_size == 32);
 }
 
-int paged_part_tokens(int head_dim, int block_size) {
-    (void)head_dim;
-    int blocks = 512 / block_size;
+// Partition length: long partitions stream best, but the grid should still
+// hold about two workgroups per CU when every context is full; the result
+// is a power of two between 256 and 2048 tokens, rounded to whole KV
+// blocks.  CLOVE_PAGED_PART overrides it (tuning only; the output does not
+// depend on it beyond summation order).
+int paged_part_tokens(int num_seqs, int num_heads, int capacity, int block_size, int num_cus) {
+    int tokens;
+    const char *v = std::getenv("CLOVE_PAGED_PART");
+    if (v && *v) {
+        tokens = std::atoi(v);
+    } else {
+        const int64_t groups = (int64_t)num_seqs * ((num_heads + 3) / 4);
+        const int64_t want = 2LL * num_cus;
+        tokens = 256;
+        while (tokens < 2048 && groups * ((capacity + 2 * tokens - 1) / (2 * tokens)) >= want)
+            tokens *= 2;
+    }
+    int blocks = tokens / block_size;
     if (blocks < 1) blocks = 1;
     return blocks * block_size;
 }
@@ -316,16 +413,20 @@ size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max
 
 void paged_attention(const PagedArgs &a, hipStream_t s) {
     if (a.num_seqs <= 0 || a.num_heads <= 0) return;
-    const dim3 grid((unsigned)a.max_parts, (unsigned)a.num_heads, (unsigned)a.num_seqs);
-#define CLOVE_PAGED_CASE(D, BS)                                              \
-    if (a.head_dim == D && a.block_size == BS) {                             \
-        paged_partition_kernel<D, BS><<<grid, 256, 0, s>>>(a);               \
+    const dim3 grid((unsigned)((a.num_heads + 3) / 4), (unsigned)a.max_parts,
+                    (unsigned)a.num_seqs);
+#define CLOVE_PAGED_CASE(D, BS)                                                     \
+    if (a.head_dim == D && a.block_size == BS) {                                    \
+        paged_heads_kernel<D, BS, 4, 1><<<grid, 256, 0, s>>>(a);                    \
     } else
     CLOVE_PAGED_CASE(64, 8) CLOVE_PAGED_CASE(64, 16) CLOVE_PAGED_CASE(64, 32)
     CLOVE_PAGED_CASE(128, 8) CLOVE_PAGED_CASE(128, 16) CLOVE_PAGED_CASE(128, 32)
     CLOVE_PAGED_CASE(256, 8) CLOVE_PAGED_CASE(256, 16) CLOVE_PAGED_CASE(256, 32)
     { return; }
 #undef CLOVE_PAGED_CASE
+    const int pairs = a.num_seqs * a.num_heads;
+    if (a.max_parts > 1)
+        paged_merge_kernel<<<(unsigned)((pairs + 3) / 4), 256, 0, s>>>(a);
 }
 
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,

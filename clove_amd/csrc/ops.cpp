@@ -157,12 +157,8 @@ void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out) {
     Context &c = ctx();
     const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override());
     TensorNode ws;
-    int32_t *tickets = nullptr;
-    if (p.ws_floats) {
-        ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
-        tickets = zeroed_counters((size_t)p.tiles);
-    }
-    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, tickets, c.stream);
+    if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
+    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, c.stream);
 }
 
 // backend.rs:1282-1306: m = prod(a.shape[..last]), k = a.shape[last],
@@ -226,15 +222,14 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
     a.context_lens = cl.i32();
     a.out = out.f32();
     a.err_flag = device_error_flag();
-    a.counters = zeroed_counters(B * H);
     a.num_blocks = (int64_t)nb;
     a.num_seqs = (int)B;
     a.num_heads = (int)H;
     a.head_dim = (int)D;
     a.block_size = (int)bs;
     a.max_blocks = (int)max_blocks;
-    a.part_tokens = k::paged_part_tokens((int)D, (int)bs);
     const int cap = (int)(max_blocks * bs);
+    a.part_tokens = k::paged_part_tokens((int)B, (int)H, cap, (int)bs, c.num_cus);
     a.max_parts = std::max(1, (cap + a.part_tokens - 1) / a.part_tokens);
     a.scale = scale;
     const size_t ws = k::paged_workspace_floats((int)B, (int)H, (int)D, cap, a.part_tokens);

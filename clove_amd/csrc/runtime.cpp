@@ -27,8 +27,6 @@ size_t g_reserved = 0;
 std::vector<hipEvent_t> g_events;
 
 int32_t *g_err_flag = nullptr;  // device word set by kernels that saw bad indices
-int32_t *g_counters = nullptr;  // self-resetting ticket counters
-size_t g_counters_len = 0;
 }  // namespace
 
 void set_last_error(const std::string &msg) { g_last_error = msg; }
@@ -184,11 +182,6 @@ void shutdown() {
         g_reserved -= 512;
         g_err_flag = nullptr;
     }
-    if (g_counters) {
-        (void)hipFree(g_counters);
-        g_counters = nullptr;
-        g_counters_len = 0;
-    }
     (void)hipStreamDestroy(g_ctx.own_stream);
     g_ctx = Context{};
     g_ready = false;
@@ -199,21 +192,6 @@ int32_t *device_error_flag() {
     return g_err_flag;
 }
 
-int32_t *zeroed_counters(size_t n) {
-    Context &c = ctx();
-    if (n > g_counters_len) {
-        size_t len = 4096;
-        while (len < n) len <<= 1;
-        CLOVE_HIP_CHECK(hipStreamSynchronize(c.stream));
-        if (g_counters) CLOVE_HIP_CHECK(hipFree(g_counters));
-        g_counters = nullptr;
-        g_counters_len = 0;
-        CLOVE_HIP_CHECK(hipMalloc(&g_counters, len * sizeof(int32_t)));
-        CLOVE_HIP_CHECK(hipMemsetAsync(g_counters, 0, len * sizeof(int32_t), c.stream));
-        g_counters_len = len;
-    }
-    return g_counters;
-}
 
 void synchronize() {
     Context &c = ctx();

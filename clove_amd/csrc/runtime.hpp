@@ -16,9 +16,6 @@ void shutdown();
 void synchronize();
 void set_stream(void *s);
 int32_t *device_error_flag();
-// A device array of at least n int32 zeros that kernels return to zero
-// before they finish (ticket counters); grows on demand.
-int32_t *zeroed_counters(size_t n);
 
 void upload(Tensor &t, const void *src, size_t offset, size_t count);
 void download(const Tensor &t, void *dst, size_t offset, size_t count);
