@@ -106,6 +106,7 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_paged_attention": (vp, [vp, vp, vp, vp, vp, vp]),
         "clove_hip_paged_attention_scaled": (vp, [vp, vp, vp, vp, vp, vp, f]),
         "clove_hip_paged_gather_indices": (vp, [vp, vp, C.c_int, C.c_int]),
+        "clove_hip_paged_kv_append": (C.c_int, [vp, vp, vp, vp, vp]),
         "clove_hip_fused_chain": (C.c_int, [C.POINTER(ChainOp), C.c_int, C.POINTER(vp), C.c_int,
                                             C.POINTER(vp)]),
         "clove_hip_graph_create": (vp, []),
@@ -356,6 +357,13 @@ def paged_attention(q: Tensor, k: Optional[Tensor], v: Optional[Tensor], kv_cach
         p = lib().clove_hip_paged_attention_scaled(q.handle, kh, vh, kv_cache.handle,
                                                    block_tables.handle, context_lens.handle, scale)
     return _handle(p)
+
+
+def paged_kv_append(kv_cache: Tensor, k: Tensor, v: Tensor, block_tables: Tensor,
+                    context_lens: Tensor) -> None:
+    """Writes each sequence's new-token k/v into its cache slot ctx-1."""
+    _check(lib().clove_hip_paged_kv_append(kv_cache.handle, k.handle, v.handle,
+                                           block_tables.handle, context_lens.handle))
 
 
 def paged_gather_indices(block_tables: Tensor, context_lens: Tensor, block_size: int,

@@ -300,6 +300,15 @@ CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_ca
     });
 }
 
+int clove_hip_paged_kv_append(CTensor kv_cache, CTensor k, CTensor v, CTensor block_tables,
+                              CTensor context_lens) {
+    return guarded([&] {
+        HipBackend::paged_kv_append(deref(kv_cache, "kv_cache"), deref(k, "k"), deref(v, "v"),
+                                    deref(block_tables, "block_tables"),
+                                    deref(context_lens, "context_lens"));
+    });
+}
+
 CTensor clove_hip_paged_gather_indices(CTensor block_tables, CTensor context_lens, int block_size,
                                        int max_ctx) {
     return guarded_tensor([&] {

@@ -14,7 +14,12 @@
 //      same element count form one fused chain; MatMul, Softmax, LayerNorm
 //      and PagedAttention are barriers that flush the chain.  Every chain
 //      value consumed outside its chain or requested as an output is stored
-//      (the reference stores only the chain's last value, lazy.rs:1823);
+//      (the reference stores only the chain's last value, lazy.rs:1823).
+//      A MatMul whose only consumer is Add(matmul, bias), optionally followed
+//      by a ReLU or GELU that is the Add's only consumer, becomes one GEMM
+//      step with the bias and activation applied in its store (the
+//      Linear::forward pattern, nn.rs:115-118); the reference runs these as
+//      separate passes;
 //   4. liveness (lazy.rs:2500-2535): step outputs share virtual buffers
 //      whose last reader has already run; buffers live in the model and grow
 //      on demand (the reference reallocates at 2x, lazy.rs:2585-2607).
@@ -326,8 +331,9 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
         steps.push_back(st);
         group.clear();
     };
+    std::set<int> absorbed;  // nodes folded into a GEMM epilogue
     for (const Node &n : nodes) {
-        if (!alive[n.id] || n.op == CLOVE_OP_INPUT) continue;
+        if (!alive[n.id] || n.op == CLOVE_OP_INPUT || absorbed.count(n.id)) continue;
         if (ew_arity(n.op) > 0) {
             if (!group.empty() &&
                 (shape_key(nodes[group.back()].shape) != shape_key(n.shape) ||
@@ -346,6 +352,32 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
         }
         st.in = n.deps;
         st.out = {n.id};
+        if (n.op == CLOVE_OP_MATMUL) {
+            // Epilogue fusion.  `sole` is the only consumer of `id`, or -1.
+            auto sole = [&](int id) {
+                return (!out_set.count(id) && users[id].size() == 1) ? users[id][0] : -1;
+            };
+            int tail = n.id;
+            const int add = sole(n.id);
+            if (add >= 0 && nodes[add].op == CLOVE_OP_ADD && nodes[add].deps[0] == n.id &&
+                nodes[add].deps[1] != n.id) {
+                const int bias = nodes[add].deps[1];
+                // the bias must already exist when this step runs
+                if (nodes[bias].op == CLOVE_OP_INPUT || bias < n.id) {
+                    st.in.push_back(bias);
+                    absorbed.insert(add);
+                    tail = add;
+                }
+            }
+            const int act = sole(tail);
+            if (act >= 0 && nodes[act].deps[0] == tail &&
+                (nodes[act].op == CLOVE_OP_RELU || nodes[act].op == CLOVE_OP_GELU)) {
+                st.act = nodes[act].op == CLOVE_OP_RELU ? 1 : 2;
+                absorbed.insert(act);
+                tail = act;
+            }
+            st.out = {tail};
+        }
         steps.push_back(st);
     }
     flush();
@@ -383,7 +415,10 @@ std::string Model::describe() const {
             s << "]";
             break;
         }
-        case Step::MATMUL: s << "MatMul"; break;
+        case Step::MATMUL:
+            s << "MatMul" << (st.in.size() > 2 ? "+Add" : "")
+              << (st.act == 1 ? "+ReLU" : st.act == 2 ? "+GELU" : "");
+            break;
         case Step::SOFTMAX: s << "Softmax"; break;
         case Step::LAYER_NORM: s << "LayerNorm"; break;
         default: s << "PagedAttention"; break;
@@ -465,7 +500,8 @@ std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const 
             break;
         }
         case Step::MATMUL:
-            HipBackend::matmul_into(*arg(st.in[0]), *arg(st.in[1]), *view_of(st.out[0]));
+            HipBackend::matmul_into(*arg(st.in[0]), *arg(st.in[1]), *view_of(st.out[0]),
+                                    st.in.size() > 2 ? arg(st.in[2]) : nullptr, st.act);
             break;
         case Step::SOFTMAX:
             HipBackend::softmax_into(*arg(st.in[0]), *view_of(st.out[0]));

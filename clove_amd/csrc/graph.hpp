@@ -53,6 +53,8 @@ struct Step {
     std::vector<int> out;   // node ids written
     std::vector<ChainOp> chain;  // FUSED only
     SymPtr numel;                // FUSED only: index space
+    int act = 0;                 // MATMUL only: fused activation (0 none, 1 ReLU, 2 GELU);
+                                 // a third input, when present, is the fused bias
 };
 
 // CompiledModel (lazy.rs:2545-2555).

@@ -42,7 +42,26 @@ struct GemmArgs {
     float *C;
     float *ws;        // split-K partial tiles [splits][tiles][BM*BN]
     int M, N, K, tiles_n, k_per_split, splits;
+    GemmEpilogue epi;
 };
+
+// Epilogue: C = act(acc + bias[(row*N + col) % bias_n]), each step rounded
+// in f32 exactly as Clove's separate Add (backend.rs:1489) and ReLU
+// (:1823) / GELU (:1924) passes round it.
+__device__ __forceinline__ float epilogue(const GemmEpilogue &e, float v, int row, int col, int N) {
+#pragma clang fp contract(off)
+    if (e.bias_mode == GEMM_BIAS_COL) v = v + e.bias[col];
+    else if (e.bias_mode == GEMM_BIAS_SCALAR) v = v + e.bias[0];
+    else if (e.bias_mode == GEMM_BIAS_MOD) v = v + e.bias[((uint64_t)row * N + col) % e.bias_n];
+    if (e.act == GEMM_ACT_RELU) {
+        v = v > 0.0f ? v : 0.0f;
+    } else if (e.act == GEMM_ACT_GELU) {
+        const float k = 0x1.988452p-1f;  // (2/pi).sqrt() in f32, backend.rs:1924
+        const float x3 = (v * v) * v;
+        v = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * x3)));
+    }
+    return v;
+}
 
 template <int BM, int BN, int BK, int WM, int WN>
 struct GemmCfg {
@@ -212,7 +231,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
                 for (int e = 0; e < 16; ++e) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
-                    if (!EDGE || (row < M && col < N)) g.C[(size_t)row * N + col] = acc[i][j][e];
+                    if (!EDGE || (row < M && col < N))
+                        g.C[(size_t)row * N + col] = epilogue(g.epi, acc[i][j][e], row, col, N);
                 }
         return;
     }
@@ -236,7 +256,7 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float *__restrict__ ws,
                                                           float *__restrict__ C, int M, int N,
                                                           int BM, int BN, int tiles_n, int tiles,
-                                                          int splits) {
+                                                          int splits, GemmEpilogue epi) {
     const int quads_per_row = BN / 4;
     const int64_t total = (int64_t)tiles * BM * quads_per_row;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
@@ -253,7 +273,7 @@ __global__ void __launch_bounds__(256) gemm_splitk_reduce(const float *__restric
             sum += *reinterpret_cast<const f4 *>(ws + (size_t)sp * tiles * BM * BN + off);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
-            if (col + q < N) C[(size_t)row * N + col + q] = sum[q];
+            if (col + q < N) C[(size_t)row * N + col + q] = epilogue(epi, sum[q], row, col + q, N);
     }
 }
 
@@ -312,7 +332,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg) {
 }
 
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
-              hipStream_t s) {
+              const GemmEpilogue &epi, hipStream_t s) {
     if (p.M <= 0 || p.N <= 0) return;
     if (p.K <= 0) {
         (void)hipMemsetAsync(C, 0, (size_t)p.M * p.N * sizeof(float), s);
@@ -323,7 +343,7 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
         q.vec = false;
         q.interior = false;
     }
-    GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits};
+    GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits, epi};
     switch (q.cfg) {
     case CFG_32x128: launch_cfg<32, 128, 32, 32, 32>(q, g, s); break;
     case CFG_64x64: launch_cfg<64, 64, 16, 32, 32>(q, g, s); break;
@@ -338,7 +358,7 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
         int64_t blocks = (work + 255) / 256;
         if (blocks > 8192) blocks = 8192;
         gemm_splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(ws, C, p.M, p.N, BM, BN, p.tiles_n,
-                                                            p.tiles, p.splits);
+                                                            p.tiles, p.splits, epi);
     }
 }
 

@@ -30,11 +30,21 @@ struct GemmPlan {
     size_t ws_floats;  // split-K workspace
     bool vec, interior;
 };
+// Optional epilogue fused into the GEMM store: bias add with Clove's
+// broadcast rule (bias read at flat index % bias_n) and an activation.
+enum { GEMM_BIAS_NONE = 0, GEMM_BIAS_COL = 1, GEMM_BIAS_SCALAR = 2, GEMM_BIAS_MOD = 3 };
+enum { GEMM_ACT_NONE = 0, GEMM_ACT_RELU = 1, GEMM_ACT_GELU = 2 };
+struct GemmEpilogue {
+    const float *bias = nullptr;
+    uint64_t bias_n = 0;
+    int bias_mode = GEMM_BIAS_NONE;
+    int act = GEMM_ACT_NONE;
+};
 // Picks the tile configuration and K split for a shape (force_cfg >= 0
 // overrides the configuration, for tuning).
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
-              hipStream_t s);
+              const GemmEpilogue &epi, hipStream_t s);
 
 // paged_attention.hip
 struct PagedArgs {
@@ -60,6 +70,11 @@ int paged_part_tokens(int num_seqs, int num_heads, int capacity, int block_size,
 // Head dims 64/128/256 and block sizes 8/16/32 have kernels.
 bool paged_supported(int head_dim, int block_size);
 void paged_attention(const PagedArgs &a, hipStream_t s);
+// row_floats = H * D (a multiple of 4); k_new/v_new are [B, row_floats].
+void paged_append(float *k_cache, float *v_cache, const float *k_new, const float *v_new,
+                  const int32_t *block_tables, const int32_t *context_lens, int num_seqs,
+                  int max_blocks, int block_size, int64_t num_blocks, int row_floats,
+                  int32_t *err_flag, hipStream_t s);
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,
                  int num_seqs, int max_blocks, int block_size, int max_ctx, hipStream_t s);
 

@@ -359,6 +359,36 @@ __global__ void __launch_bounds__(256) paged_merge_kernel(PagedArgs a) {
     }
 }
 
+// Writes the new token's K and V rows of every sequence into its cache slot.
+// One workgroup per sequence copies H*D floats per plane as 16-byte vectors.
+__global__ void __launch_bounds__(256) paged_append_kernel(float *__restrict__ k_cache,
+                                                           float *__restrict__ v_cache,
+                                                           const float *__restrict__ k_new,
+                                                           const float *__restrict__ v_new,
+                                                           const int32_t *__restrict__ bt,
+                                                           const int32_t *__restrict__ cl,
+                                                           int max_blocks, int bs, int64_t num_blocks,
+                                                           int row_floats, int32_t *err_flag) {
+    const int b = blockIdx.x;
+    const int ctx = cl[b];
+    if (ctx <= 0) return;
+    if (ctx > max_blocks * bs) {
+        if (threadIdx.x == 0) atomicOr(err_flag, 1);
+        return;
+    }
+    const int64_t blk = bt[(size_t)b * max_blocks + (ctx - 1) / bs];
+    if (blk < 0 || blk >= num_blocks) {
+        if (threadIdx.x == 0) atomicOr(err_flag, 1);
+        return;
+    }
+    const size_t dst = ((size_t)blk * bs + (ctx - 1) % bs) * row_floats;
+    const size_t src = (size_t)b * row_floats;
+    for (int i = threadIdx.x; i < row_floats / 4; i += 256) {
+        reinterpret_cast<cl_f4 *>(k_cache + dst)[i] = reinterpret_cast<const cl_f4 *>(k_new + src)[i];
+        reinterpret_cast<cl_f4 *>(v_cache + dst)[i] = reinterpret_cast<const cl_f4 *>(v_new + src)[i];
+    }
+}
+
 __global__ void __launch_bounds__(256) paged_slots_kernel(const int32_t *__restrict__ bt,
                                                           const int32_t *__restrict__ cl,
                                                           int32_t *__restrict__ slots,
@@ -427,6 +457,17 @@ void paged_attention(const PagedArgs &a, hipStream_t s) {
     const int pairs = a.num_seqs * a.num_heads;
     if (a.max_parts > 1)
         paged_merge_kernel<<<(unsigned)((pairs + 3) / 4), 256, 0, s>>>(a);
+}
+
+void paged_append(float *k_cache, float *v_cache, const float *k_new, const float *v_new,
+                  const int32_t *block_tables, const int32_t *context_lens, int num_seqs,
+                  int max_blocks, int block_size, int64_t num_blocks, int row_floats,
+                  int32_t *err_flag, hipStream_t s) {
+    if (num_seqs <= 0) return;
+    paged_append_kernel<<<(unsigned)num_seqs, 256, 0, s>>>(k_cache, v_cache, k_new, v_new,
+                                                          block_tables, context_lens, max_blocks,
+                                                          block_size, num_blocks, row_floats,
+                                                          err_flag);
 }
 
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,

@@ -75,28 +75,41 @@ __global__ void __launch_bounds__(256) softmax_wave_kernel(const float *__restri
     }
 }
 
+// gamma and beta are staged in LDS once per workgroup (2 * cols floats):
+// every row of the workgroup reads them, and fetching them from L2 per row
+// costs as much traffic as the rows themselves (at 4096 columns the pair is
+// 32 KiB, the size of the vector L1).  The row's own loads are issued first
+// so the staging overlaps them.
 template <int VPT>
 __global__ void __launch_bounds__(256) layer_norm_wave_kernel(const float *__restrict__ x,
                                                               const float *__restrict__ gamma,
                                                               const float *__restrict__ beta,
                                                               float *__restrict__ y, int rows,
                                                               int cols, float eps) {
+    extern __shared__ cl_f4 s_gb[];  // [nvec] gamma, then [nvec] beta
     const int lane = threadIdx.x & 63;
     const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    const bool live = row < rows;
     const int nvec = cols >> 2;
-    const cl_f4 *xr = reinterpret_cast<const cl_f4 *>(x + row * (long)cols);
-    cl_f4 *yr = reinterpret_cast<cl_f4 *>(y + row * (long)cols);
-    const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(gamma);
-    const cl_f4 *b4 = reinterpret_cast<const cl_f4 *>(beta);
+    const cl_f4 *xr = reinterpret_cast<const cl_f4 *>(x + (live ? row : 0) * (long)cols);
     cl_f4 v[VPT];
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int c = lane + 64 * i;
-        v[i] = c < nvec ? __builtin_nontemporal_load(xr + c) : (cl_f4){0.f, 0.f, 0.f, 0.f};
-        s += hsum4(v[i]);
+        v[i] = (live && c < nvec) ? __builtin_nontemporal_load(xr + c) : (cl_f4){0.f, 0.f, 0.f, 0.f};
     }
+    const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(gamma);
+    const cl_f4 *b4 = reinterpret_cast<const cl_f4 *>(beta);
+    for (int c = threadIdx.x; c < nvec; c += 256) {
+        s_gb[c] = g4[c];
+        s_gb[nvec + c] = b4[c];
+    }
+    __syncthreads();
+    if (!live) return;
+    cl_f4 *yr = reinterpret_cast<cl_f4 *>(y + row * (long)cols);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) s += hsum4(v[i]);
     const float n = (float)cols;
     const float mean = wave_sum(s) / n;
     float q = 0.0f;
@@ -113,7 +126,7 @@ __global__ void __launch_bounds__(256) layer_norm_wave_kernel(const float *__res
     for (int i = 0; i < VPT; ++i) {
         const int c = lane + 64 * i;
         if (c < nvec) {
-            const cl_f4 o = ((v[i] - mean) * rsd) * g4[c] + b4[c];
+            const cl_f4 o = ((v[i] - mean) * rsd) * s_gb[c] + s_gb[nvec + c];
             __builtin_nontemporal_store(o, yr + c);
         }
     }
@@ -200,13 +213,14 @@ void layer_norm_rows(const float *x, const float *gamma, const float *beta, floa
     const int r = (int)rows, c = (int)cols;
     const bool al = aligned16(x) && aligned16(y) && aligned16(gamma) && aligned16(beta);
     const int vpt = al ? pick_vpt(c) : 0;
+    const size_t lds = 2 * (size_t)c * sizeof(float);
     switch (vpt) {
-    case 1: layer_norm_wave_kernel<1><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
-    case 2: layer_norm_wave_kernel<2><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
-    case 4: layer_norm_wave_kernel<4><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
-    case 8: layer_norm_wave_kernel<8><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
-    case 16: layer_norm_wave_kernel<16><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
-    case 32: layer_norm_wave_kernel<32><<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 1: layer_norm_wave_kernel<1><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 2: layer_norm_wave_kernel<2><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 4: layer_norm_wave_kernel<4><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 8: layer_norm_wave_kernel<8><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 16: layer_norm_wave_kernel<16><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
+    case 32: layer_norm_wave_kernel<32><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
     default: layer_norm_loop_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
     }
 }

@@ -149,16 +149,30 @@ static int gemm_cfg_override() {
     return (v && *v) ? std::atoi(v) : -1;
 }
 
-void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out) {
+void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, const Tensor *bias,
+                             int act) {
     need_f32(a, "a");
     need_f32(b, "b");
     size_t m, kk, n;
     matmul_dims(a, b, &m, &kk, &n);
     Context &c = ctx();
+    k::GemmEpilogue epi;
+    if (bias) {
+        need_f32(*bias, "bias");
+        CLOVE_REQUIRE(bias->numel > 0, CLOVE_HIP_ERR_SHAPE, "bias is empty");
+        epi.bias = bias->f32();
+        epi.bias_n = bias->numel;
+        epi.bias_mode = bias->numel == 1 ? k::GEMM_BIAS_SCALAR
+                        : bias->numel == n ? k::GEMM_BIAS_COL
+                                           : k::GEMM_BIAS_MOD;
+    }
+    CLOVE_REQUIRE(act >= k::GEMM_ACT_NONE && act <= k::GEMM_ACT_GELU, CLOVE_HIP_ERR_INVALID,
+                  "unknown GEMM epilogue activation");
+    epi.act = act;
     const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override());
     TensorNode ws;
     if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
-    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, c.stream);
+    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, epi, c.stream);
 }
 
 // backend.rs:1282-1306: m = prod(a.shape[..last]), k = a.shape[last],
@@ -280,6 +294,39 @@ void fill_normal(Tensor &t, uint64_t seed, float mean, float stddev) {
 void fill_uniform(Tensor &t, uint64_t seed, float lo, float hi) {
     need_f32(t, "tensor");
     k::fill_uniform(t.f32(), t.numel, seed, lo, hi, ctx().stream);
+}
+
+}  // namespace clove
+
+namespace clove {
+
+// KV-cache append (the cache write before decode; no counterpart in Clove).
+void HipBackend::paged_kv_append(const Tensor &kv, const Tensor &k, const Tensor &v,
+                                 const Tensor &bt, const Tensor &cl) {
+    need_f32(kv, "kv_cache");
+    need_f32(k, "k");
+    need_f32(v, "v");
+    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
+                  "block_tables and context_lens must be int32 tensors");
+    CLOVE_REQUIRE(kv.shape.size() == 5 && kv.shape[0] == 2, CLOVE_HIP_ERR_SHAPE,
+                  "kv_cache must be [2, num_blocks, block_size, heads, head_dim], got " +
+                      shape_str(kv.shape));
+    const size_t nb = kv.shape[1], bs = kv.shape[2], H = kv.shape[3], D = kv.shape[4];
+    const size_t B = cl.numel, row = H * D;
+    CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == B, CLOVE_HIP_ERR_SHAPE,
+                  "block_tables must be [num_seqs, max_blocks] with num_seqs = numel(context_lens)");
+    CLOVE_REQUIRE(k.numel == B * row && v.numel == B * row, CLOVE_HIP_ERR_SHAPE,
+                  "k and v must hold num_seqs*heads*head_dim elements");
+    CLOVE_REQUIRE(row % 4 == 0 && ((reinterpret_cast<uintptr_t>(k.data) |
+                                    reinterpret_cast<uintptr_t>(v.data) |
+                                    reinterpret_cast<uintptr_t>(kv.data)) & 15) == 0,
+                  CLOVE_HIP_ERR_INVALID, "kv append needs 16-byte aligned rows");
+    CLOVE_REQUIRE(bt.shape[1] * bs < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "context capacity exceeds 2^31 tokens");
+    if (B == 0) return;
+    k::paged_append(kv.f32(), kv.f32() + nb * bs * row, k.f32(), v.f32(), bt.i32(), cl.i32(),
+                    (int)B, (int)bt.shape[1], (int)bs, (int64_t)nb, (int)row, device_error_flag(),
+                    ctx().stream);
 }
 
 }  // namespace clove

@@ -74,6 +74,8 @@ struct HipBackend {
                                       const TensorNode &v, const TensorNode &kv_cache,
                                       const TensorNode &block_tables,
                                       const TensorNode &context_lens, float scale);
+    static void paged_kv_append(const Tensor &kv_cache, const Tensor &k, const Tensor &v,
+                                const Tensor &block_tables, const Tensor &context_lens);
     static TensorNode paged_gather_indices(const TensorNode &block_tables,
                                            const TensorNode &context_lens, int block_size,
                                            int max_ctx);
@@ -83,7 +85,10 @@ struct HipBackend {
     static void softmax_into(const Tensor &a, Tensor &out);
     static void layer_norm_into(const Tensor &a, const Tensor &gamma, const Tensor &beta,
                                 Tensor &out);
-    static void matmul_into(const Tensor &a, const Tensor &b, Tensor &out);
+    // Optional fused epilogue: out = act(a.b + bias[i % numel(bias)]) with
+    // act 0 none, 1 ReLU, 2 GELU (CLOVE_OP_* elementwise semantics).
+    static void matmul_into(const Tensor &a, const Tensor &b, Tensor &out,
+                            const Tensor *bias = nullptr, int act = 0);
     static void paged_attention_into(const Tensor &q, const Tensor *k, const Tensor *v,
                                      const Tensor &kv_cache, const Tensor &block_tables,
                                      const Tensor &context_lens, float scale, Tensor &out);

@@ -169,6 +169,16 @@ CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_ca
 CTensor clove_hip_paged_attention_scaled(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
                                          CTensor block_tables, CTensor context_lens,
                                          float scale);
+/* KV-cache append: writes each sequence's new-token k[b] and v[b] (f32
+ * [B, H*D]) into planes 0 and 1 of kv_cache at the slot of token ctx_b - 1,
+ * bt[b][(ctx_b-1)/bs]*bs + (ctx_b-1)%bs.  Sequences with ctx_b <= 0 are
+ * skipped.  Afterwards paged_attention(q, NULL, NULL, ...) equals
+ * paged_attention(q, k, v, ...) bit for bit.  Clove has no counterpart: this is
+ * the cache write that must precede decode (the k/v projections of
+ * nn.rs:540-542 never reach kv_cache in the reference).  Table entries outside
+ * the pool are skipped and reported by the next synchronising call. */
+int clove_hip_paged_kv_append(CTensor kv_cache, CTensor k, CTensor v, CTensor block_tables,
+                              CTensor context_lens);
 /* Gather-index debug entry: int32 [B, max_ctx] of physical token slots
  * bt[b][t/bs]*bs + t%bs (lazy.rs:5262-5270), -1 where t >= ctx_b.  Computed
  * on the device by the same index code the attention kernel uses. */

@@ -218,6 +218,26 @@ def paged_attention(q, k_new, v_new, kv_cache, block_tables, context_lens, scale
     return out
 
 
+def paged_kv_append(kv_cache, k_new, v_new, block_tables, context_lens):
+    """Copy of kv_cache with each sequence's new-token k/v written at the slot
+    of token ctx-1 (the cache write that precedes decode; Clove has none).
+    Sequences with ctx <= 0 are left alone."""
+    kv = np.array(kv_cache, dtype=np.float32, copy=True)
+    _, nb, bs, H, D = kv.shape
+    bt = np.asarray(block_tables, dtype=np.int64)
+    cl = np.asarray(context_lens, dtype=np.int64)
+    kn = np.asarray(k_new, dtype=np.float32).reshape(cl.size, H, D)
+    vn = np.asarray(v_new, dtype=np.float32).reshape(cl.size, H, D)
+    for b in range(cl.size):
+        t = int(cl[b]) - 1
+        if t < 0:
+            continue
+        blk = int(bt[b, t // bs])
+        kv[0, blk, t % bs] = kn[b]
+        kv[1, blk, t % bs] = vn[b]
+    return kv
+
+
 def paged_slots(block_tables, context_lens, block_size: int, max_ctx: int):
     """Physical slot of each logical token (lazy.rs:5262-5270), -1 past ctx."""
     bt = np.ascontiguousarray(block_tables, dtype=np.int32)

@@ -95,12 +95,32 @@ def mlp_graph():
 
 
 def test_plan_mlp():
+    # Linear::forward (matmul then bias add, nn.rs:115-118) and the ReLU fold
+    # into the GEMM's epilogue; the softmax stays a row step.
     g, y = mlp_graph()
     m = g.compile([y])
-    assert steps(m) == ["MatMul", "Fused[Add,ReLU]", "MatMul", "Fused[Add]", "Softmax"]
-    assert m.num_steps == 5
-    # liveness: the first matmul's buffer is free once the chain has read it
-    assert "vbufs=2" in m.describe() or "vbufs=3" in m.describe()
+    assert steps(m) == ["MatMul+Add+ReLU", "MatMul+Add", "Softmax"]
+    assert m.num_steps == 3
+    # liveness: the hidden layer's buffer is reused once the second GEMM has
+    # read it
+    assert "vbufs=2" in m.describe()
+
+
+def test_plan_epilogue_fusion_only_for_sole_consumers():
+    g = ca.Graph()
+    x, w, b = g.input("4,8"), g.input("8,6"), g.input("6")
+    mm = g.op("matmul", x, w)
+    add = g.op("add", mm, b)
+    act = g.op("gelu", add)
+    both = g.op("mul", act, add)     # add has a second consumer: GELU stays unfused
+    m = g.compile([both])
+    assert steps(m) == ["MatMul+Add", "Fused[GELU,Mul]"]
+    g2 = ca.Graph()
+    x, w, b = g2.input("4,8"), g2.input("8,6"), g2.input("6")
+    mm = g2.op("matmul", x, w)
+    y = g2.op("add", b, mm)          # bias first: shape follows b, no fusion
+    m2 = g2.compile([y, mm])
+    assert steps(m2) == ["MatMul", "Fused[Add]"]
 
 
 def test_plan_dce_and_constant_folding():

@@ -83,3 +83,56 @@ def test_paged_attention_in_graph(hip):
     (out,) = m.execute([hip.tensor(v) for v in (q, kn, vn, kv, bt, cl)])
     want = oracle.mul_scalar(oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D), 3.0)
     assert_close(out.numpy(), want, 2e-3, 1e-5, "paged in graph")
+
+
+@pytest.mark.parametrize("m,k,n,bias_n,act", [(64, 784, 128, 128, "relu"), (300, 256, 192, 1, "gelu"),
+                                               (130, 96, 10, 3, None), (512, 512, 512, 512, "gelu"),
+                                               (16, 1000, 30, 30, "relu")])
+def test_gemm_epilogue_fusion(hip, m, k, n, bias_n, act):
+    """MatMul -> Add(bias) [-> ReLU/GELU] planned as one GEMM with a fused
+    epilogue equals the eager composition: the matmul tolerance on the
+    pre-activation, then the elementwise ops applied to the same values."""
+    gg = rng(m + n)
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, bias_n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},{k}"), g.input(f"{k},{n}"), g.input(f"{bias_n}")
+    y = g.op("add", g.op("matmul", x, wi), bi)
+    if act:
+        y = g.op(act, y)
+    model = g.compile([y])
+    assert model.num_steps == 1, model.describe()
+    (out,) = model.execute([hip.tensor(v) for v in (a, w, b)])
+    pre = oracle.add(oracle.matmul(a, w), b)
+    want = getattr(oracle, act)(pre) if act else pre
+    atol = 1e-4 * float(np.abs(want).max())
+    assert_close(out.numpy(), want, 2e-3, atol, f"fused epilogue {m}x{k}x{n} bias={bias_n} {act}")
+
+
+def test_concurrent_callers(hip):
+    """The C ABI serialises host-side calls under one lock; callers on several
+    threads get the same results as one caller."""
+    import threading
+
+    gg = rng(12)
+    xs = [gg.normal(0, 2, (64, 1024)).astype(np.float32) for _ in range(8)]
+    want = [oracle.softmax(x) for x in xs]
+    got = [None] * 8
+    errors = []
+
+    def work(i):
+        try:
+            for _ in range(5):
+                got[i] = hip.softmax(hip.tensor(xs[i])).numpy()
+        except Exception as e:  # reported below
+            errors.append(e)
+
+    ts = [threading.Thread(target=work, args=(i,)) for i in range(8)]
+    for t_ in ts:
+        t_.start()
+    for t_ in ts:
+        t_.join()
+    assert not errors, errors
+    for g_, w in zip(got, want):
+        assert_close(g_, w, 1e-4, 1e-9, "threaded softmax")

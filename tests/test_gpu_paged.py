@@ -121,3 +121,29 @@ def test_config5_full(hip):
     pool, sbt, scl = workloads.compact_pool(read_block, bt, ctx, seqs, bs)
     want = oracle.paged_attention(q[seqs], None, None, pool, sbt, scl).reshape(len(seqs), H * D)
     assert_close(out[seqs], want, RTOL, ATOL, "config5 sampled sequences")
+
+
+def test_kv_append_then_cached_decode_equals_new_token_decode(hip):
+    """The append writes k/v at slot ctx-1; decoding from the cache afterwards
+    gives exactly the new-token decode (same rows, same order)."""
+    q, kn, vn, kv, bt, cl = make(10, 4, 4, 128, 16, 200, 32, [1, 16, 17, 300])
+    t = hip.tensor
+    tkv, tbt, tcl = t(kv), t(bt), t(cl)
+    fresh = hip.paged_attention(t(q), t(kn), t(vn), tkv, tbt, tcl).numpy()
+    hip.paged_kv_append(tkv, t(kn), t(vn), tbt, tcl)
+    assert np.array_equal(tkv.numpy(), oracle.paged_kv_append(kv, kn, vn, bt, cl))
+    cached = hip.paged_attention(t(q), None, None, tkv, tbt, tcl).numpy()
+    assert np.array_equal(cached, fresh)
+
+
+def test_kv_append_skips_empty_and_reports_bad_entries(hip):
+    q, kn, vn, kv, bt, cl = make(11, 3, 2, 64, 16, 20, 4, [0, 5, 20])
+    t = hip.tensor
+    tkv = t(kv)
+    hip.paged_kv_append(tkv, t(kn), t(vn), t(bt), t(cl))
+    assert np.array_equal(tkv.numpy(), oracle.paged_kv_append(kv, kn, vn, bt, cl))
+    bt[2, 1] = -7
+    hip.paged_kv_append(tkv, t(kn), t(vn), t(bt), t(cl))
+    with pytest.raises(hip.CloveError) as e:
+        hip.synchronize()
+    assert e.value.code == hip.ERR_RANGE

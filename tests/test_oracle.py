@@ -357,3 +357,15 @@ def test_mlp_forward_against_float64():
     want = np.exp(z - z.max(1, keepdims=True))
     want /= want.sum(1, keepdims=True)
     assert_close(oracle.mlp_forward(x, w1, b1, w2, b2), want, 1e-5, 1e-9, "mlp")
+
+
+def test_paged_kv_append_is_the_cache_write():
+    q, kn, vn, kv, bt, cl = make_paged(29, ctx=[0, 16, 33])
+    kv2 = oracle.paged_kv_append(kv, kn, vn, bt, cl)
+    # only slot ctx-1 of sequences 1 and 2 changed, in both planes
+    changed = np.argwhere(np.any(kv2 != kv, axis=(3, 4)))
+    want = sorted([(p, int(bt[b, (cl[b] - 1) // 16]), int((cl[b] - 1) % 16))
+                   for p in (0, 1) for b in (1, 2)])
+    assert sorted(map(tuple, changed.tolist())) == want
+    assert np.array_equal(oracle.paged_attention(q, None, None, kv2, bt, cl)[1:],
+                          oracle.paged_attention(q, kn, vn, kv, bt, cl)[1:])
