@@ -146,7 +146,7 @@ __device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, c
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC>
+template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC, bool EPI>
 __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
     __shared__ __attribute__((aligned(16))) float smem[2 * (Cfg::kSizeA + Cfg::kSizeB)];
@@ -232,7 +232,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
                     if (!EDGE || (row < M && col < N))
-                        g.C[(size_t)row * N + col] = epilogue(g.epi, acc[i][j][e], row, col, N);
+                        g.C[(size_t)row * N + col] =
+                            EPI ? epilogue(g.epi, acc[i][j][e], row, col, N) : acc[i][j][e];
                 }
         return;
     }
@@ -287,12 +288,25 @@ const int kCfgBK[CFG_COUNT] = {32, 16, 16, 32, 16, 16};
 template <int BM, int BN, int BK, int WM, int WN>
 void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
-    if (p.interior)
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true><<<grid, 256, 0, s>>>(g);
-    else if (p.vec)
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true><<<grid, 256, 0, s>>>(g);
-    else
-        gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false><<<grid, 256, 0, s>>>(g);
+    // The fused epilogue (bias modulo, GELU) costs registers; kernels without
+    // one (and split-K kernels, whose reduce applies it) are built without it.
+    const bool epi = p.splits == 1 &&
+                     (g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE);
+    if (epi) {
+        if (p.interior)
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, true><<<grid, 256, 0, s>>>(g);
+        else if (p.vec)
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, true><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, true><<<grid, 256, 0, s>>>(g);
+    } else {
+        if (p.interior)
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, false, true, false><<<grid, 256, 0, s>>>(g);
+        else if (p.vec)
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, true, false><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_mfma_kernel<BM, BN, BK, WM, WN, true, false, false><<<grid, 256, 0, s>>>(g);
+    }
 }
 
 }  // namespace
