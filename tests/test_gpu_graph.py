@@ -110,6 +110,31 @@ def test_gemm_epilogue_fusion(hip, m, k, n, bias_n, act):
     assert_close(out.numpy(), want, 2e-3, atol, f"fused epilogue {m}x{k}x{n} bias={bias_n} {act}")
 
 
+@pytest.mark.parametrize("m,k,n,bias_n,act", [(64, 784, 128, 128, "relu"), (32, 4096, 512, 512, "gelu"),
+                                               (300, 256, 192, 7, None), (1024, 512, 1024, 1, "gelu")])
+def test_gemm_epilogue_matches_eager_bits(hip, m, k, n, bias_n, act):
+    """The fused epilogue rounds in the unfused order: the planned
+    GEMM+bias(+act) equals eager matmul, then add, then the activation, bit
+    for bit (split-K shapes included: 32x4096 splits K)."""
+    gg = rng(7 * m + n)
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, bias_n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},{k}"), g.input(f"{k},{n}"), g.input(f"{bias_n}")
+    y = g.op("add", g.op("matmul", x, wi), bi)
+    if act:
+        y = g.op(act, y)
+    model = g.compile([y])
+    assert model.num_steps == 1, model.describe()
+    ta, tw, tb = hip.tensor(a), hip.tensor(w), hip.tensor(b)
+    (fused,) = model.execute([ta, tw, tb])
+    eager = hip.add(hip.matmul(ta, tw), tb)
+    if act:
+        eager = getattr(hip, act)(eager)
+    assert np.array_equal(fused.numpy(), eager.numpy())
+
+
 def test_concurrent_callers(hip):
     """The C ABI serialises host-side calls under one lock; callers on several
     threads get the same results as one caller."""
