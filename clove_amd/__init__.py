@@ -276,6 +276,14 @@ def tensor(data, dtype=None) -> Tensor:
     return _handle(p)
 
 
+def wrap(device_ptr: int, shape, dtype=np.float32) -> Tensor:
+    """Borrows device memory the caller owns (clove_hip_tensor_wrap); the
+    memory must outlive the handle, and freeing the handle leaves it alone."""
+    code = 1 if dtype == np.int32 else 0
+    return _handle(lib().clove_hip_tensor_wrap(C.c_void_p(device_ptr), _shape_arr(shape),
+                                               len(shape), code))
+
+
 def tensor2d(data) -> Tensor:
     """clove_hip_tensor_create(data, rows, cols), the 2-d form of ffi.rs:72."""
     a = np.ascontiguousarray(data, dtype=np.float32)

@@ -253,29 +253,225 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 }
 
 // C[row][col] = sum over splits, in split order, of the parked tiles
-// (deterministic).  One thread per four consecutive columns of a tile row.
-__global__ void __launch_bounds__(256) gemm_splitk_reduce(const float *__restrict__ ws,
-                                                          float *__restrict__ C, int M, int N,
-                                                          int BM, int BN, int tiles_n, int tiles,
-                                                          int splits, GemmEpilogue epi) {
+// (deterministic).  One thread per four consecutive columns of a tile row;
+// the loads of four splits are issued before they are added (the additions
+// stay in split order), and one-wave workgroups spread the few thousand
+// threads over all CUs.
+__global__ void __launch_bounds__(64) gemm_splitk_reduce(const float *__restrict__ ws,
+                                                         float *__restrict__ C, int M, int N,
+                                                         int BM, int BN, int tiles_n, int tiles,
+                                                         int splits, GemmEpilogue epi) {
     const int quads_per_row = BN / 4;
     const int64_t total = (int64_t)tiles * BM * quads_per_row;
-    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
-         i += (int64_t)gridDim.x * 256) {
+    const size_t split_stride = (size_t)tiles * BM * BN;
+    for (int64_t i = (int64_t)blockIdx.x * 64 + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * 64) {
         const int tile = (int)(i / ((int64_t)BM * quads_per_row));
         const int rem = (int)(i % ((int64_t)BM * quads_per_row));
         const int r = rem / quads_per_row, c = 4 * (rem % quads_per_row);
         const int row = (tile / tiles_n) * BM + r;
         const int col = (tile % tiles_n) * BN + c;
         if (row >= M || col >= N) continue;
-        const size_t off = (size_t)tile * BM * BN + (size_t)r * BN + c;
-        f4 sum = *reinterpret_cast<const f4 *>(ws + off);
-        for (int sp = 1; sp < splits; ++sp)
-            sum += *reinterpret_cast<const f4 *>(ws + (size_t)sp * tiles * BM * BN + off);
+        const float *src = ws + (size_t)tile * BM * BN + (size_t)r * BN + c;
+        f4 sum = *reinterpret_cast<const f4 *>(src);
+        int sp = 1;
+        for (; sp + 4 <= splits; sp += 4) {
+            const f4 v0 = *reinterpret_cast<const f4 *>(src + (size_t)sp * split_stride);
+            const f4 v1 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 1) * split_stride);
+            const f4 v2 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 2) * split_stride);
+            const f4 v3 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 3) * split_stride);
+            sum += v0;
+            sum += v1;
+            sum += v2;
+            sum += v3;
+        }
+        for (; sp < splits; ++sp) sum += *reinterpret_cast<const f4 *>(src + (size_t)sp * split_stride);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (col + q < N) C[(size_t)row * N + col + q] = epilogue(epi, sum[q], row, col + q, N);
     }
+}
+
+// Skinny GEMM, M <= 32*MB (the 32-row decode-style product, the MLP layers).
+//
+// With M this small, B (K x N) is almost all of the HBM traffic and every B
+// element feeds at most MB MFMA steps, so the kernel is a stream over B that
+// must keep the matrix cores busy at the same time: at M=32, N=K=4096 the
+// MFMA floor (6.8 us) and the HBM floor (8.4 us) are close.
+//  * A workgroup owns 32*NB columns of C (all M rows) and W waves; wave w
+//    covers its own range of k_per_wave values of K (a K split inside the
+//    workgroup); the grid's y dimension splits K further across workgroups.
+//  * Column interleave: lane l (l%32 = c) loads the NB consecutive floats
+//    B[k][n0 + NB*c .. NB*c + NB-1] in one load and hands float q to MFMA
+//    block q, so block q computes the columns n0 + NB*c + q.  One 16-byte
+//    load per lane (NB = 4) feeds four MFMA blocks, and the A values a wave
+//    reads (one 16-byte load per 32-row block and 8-group of k) are shared
+//    by all NB blocks: A traffic into the CU is 1/NB of B's.
+//  * Each wave loads straight into the MFMA operand registers, D groups of
+//    8 k ahead of the MFMAs that use them (lane half h = l/32 supplies
+//    k = 8g + 4h + t, t = 0..3, as in the tiled kernel), so the loads of D
+//    groups are in flight while one group is multiplied.
+//  * Loads go through buffer resources: a lane's byte offset is fixed for
+//    the whole wave and the per-group row step is a uniform scalar offset,
+//    so there is no per-load address arithmetic.  A lane whose k lies outside
+//    the wave's range (or whose row >= M / column >= N) gets an offset past
+//    the end of the buffer, which the hardware answers with zeros.
+//  * The W partial blocks meet in LDS and are summed in wave order
+//    (deterministic), then stored through the epilogue (one split) or parked
+//    for gemm_splitk_reduce, which sums the splits in order.
+// Needs K % 4 == 0, N % NB == 0, a 16-byte aligned A, and A, B under 2 GiB
+// each (the plan checks all four).
+
+// Raw buffer resource over [base, base + bytes): stride 0, word 3 = 32-bit
+// data format (DATA_FORMAT = 4 in bits 15..18), the gfx9-family setting.
+// Reads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+template <int NB>
+__device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
+                                       float *dst) {
+    if constexpr (NB == 1) {
+        dst[0] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)voff,
+                                                                                (int)soff, 0));
+    } else if constexpr (NB == 2) {
+        typedef unsigned u2 __attribute__((ext_vector_type(2)));
+        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)voff, (int)soff, 0);
+        dst[0] = __uint_as_float(v.x);
+        dst[1] = __uint_as_float(v.y);
+    } else {
+        const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff,
+                                                                                  (int)soff, 0));
+        dst[0] = v.x;
+        dst[1] = v.y;
+        dst[2] = v.z;
+        dst[3] = v.w;
+    }
+}
+
+template <int MB, int NB, int W, int CH>
+__global__ void __launch_bounds__(64 * W) gemm_skinny_kernel(GemmArgs g) {
+    constexpr int D = NB == 4 ? 4 : 8;           // 8-groups in flight per wave
+    constexpr int k_per_wave = 8 * D * CH;       // CH chunks of D groups
+    constexpr int kRows = 32 * MB, kCols = 32 * NB;
+    constexpr int kBlock = kRows * kCols;        // floats of one wave's partial tile
+    __shared__ __attribute__((aligned(16))) float red[W * kBlock];
+    const int M = g.M, N = g.N, K = g.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l32 = lane & 31, h = lane >> 5;
+    const int n0 = blockIdx.x * kCols;
+    const int k_begin = (blockIdx.y * W + wave) * k_per_wave;
+    const int k_end = min(k_begin + k_per_wave, K);
+
+    // The plan keeps both matrices under 2 GiB, so kOutside is past the end.
+    constexpr uint32_t kOutside = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, (uint32_t)((size_t)K * N * 4));
+    const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, (uint32_t)((size_t)M * K * 4));
+    const int col = n0 + NB * l32;  // first of this lane's NB columns
+    const int k_lane = k_begin + 4 * h;
+    const int k_lim = k_end - k_lane;  // group gi is in range iff 8*gi < k_lim
+    const uint32_t boff = col < N ? ((uint32_t)k_lane * (uint32_t)N + (uint32_t)col) * 4u : kOutside;
+    uint32_t aoff[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i) {
+        const int r = 32 * i + l32;
+        aoff[i] = r < M ? ((uint32_t)r * (uint32_t)K + (uint32_t)k_lane) * 4u : kOutside;
+    }
+    const uint32_t row_bytes = (uint32_t)N * 4u;
+
+    f16v acc[MB][NB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    float bq[D][4][NB];
+    f4 aq[D][MB];
+    auto load = [&](int gi, int d) {
+        const bool ok = 8 * gi < k_lim;  // k_end % 4 == 0, so t = 0..3 share it
+        const uint32_t bv = ok ? boff : kOutside;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) load_b<NB>(rsrc_b, bv, (uint32_t)(8 * gi + t) * row_bytes, bq[d][t]);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+            aq[d][i] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, (int)(ok ? aoff[i] : kOutside),
+                                                          32 * gi, 0));
+    };
+    auto mma = [&](int d) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+#pragma unroll
+                for (int j = 0; j < NB; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(aq[d][i][t], bq[d][t][j],
+                                                                     acc[i][j], 0, 0, 0);
+    };
+
+    // Rolling pipeline: consume slot d, refill it with the group D ahead.
+    // The scheduling barriers keep that order (left alone, the scheduler
+    // gathers each chunk's loads at its end and waits for all of them at the
+    // start of the next, exposing the full load latency once per chunk).
+    // The chunk loop is unrolled completely: across a loop back-edge the
+    // compiler's wait counts turn conservative and drain the pipeline.
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, d);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int c = 0; c + 1 < CH; ++c) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            mma(d);
+            load((c + 1) * D + d, d);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        mma(d);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // Accumulator element e of block (i, j) is row 32*i + 8*(e/4) + 4*h + e%4
+    // and column NB*(l%32) + j of the workgroup's kCols columns.
+    float *mine = red + wave * kBlock;
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            float *dst = mine + (32 * i + 8 * (e / 4) + 4 * h + (e % 4)) * kCols + NB * l32;
+#pragma unroll
+            for (int j = 0; j < NB; ++j) dst[j] = acc[i][j][e];
+        }
+    __syncthreads();
+
+    constexpr int kPer = kBlock / (64 * W);  // consecutive outputs per thread
+    static_assert(kPer >= 1 && kCols % kPer == 0, "outputs per thread split a row evenly");
+    const int idx = threadIdx.x * kPer;
+    float sum[kPer];
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) sum[j] = red[idx + j];
+    for (int w = 1; w < W; ++w)
+#pragma unroll
+        for (int j = 0; j < kPer; ++j) sum[j] += red[w * kBlock + idx + j];
+    const int r = idx / kCols, c0 = idx % kCols;
+    if (g.splits == 1) {
+        if (r < M)
+#pragma unroll
+            for (int j = 0; j < kPer; ++j) {
+                const int cc = n0 + c0 + j;
+                if (cc < N) g.C[(size_t)r * N + cc] = epilogue(g.epi, sum[j], r, cc, N);
+            }
+        return;
+    }
+    float *part = g.ws + ((size_t)blockIdx.y * gridDim.x + blockIdx.x) * kBlock;
+#pragma unroll
+    for (int j = 0; j < kPer; ++j) part[idx + j] = sum[j];
 }
 
 // Tile configurations: (BM, BN, BK, WM, WN).
@@ -309,13 +505,80 @@ void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     }
 }
 
+template <int MB, int NB, int W>
+void launch_skinny_w(const GemmPlan &p, const GemmArgs &g, dim3 grid, hipStream_t s) {
+    constexpr int chunk = 8 * (NB == 4 ? 4 : 8);  // k per chunk of pipeline groups
+    switch (p.k_per_wave / chunk) {
+    case 1: gemm_skinny_kernel<MB, NB, W, 1><<<grid, 64 * W, 0, s>>>(g); break;
+    case 2: gemm_skinny_kernel<MB, NB, W, 2><<<grid, 64 * W, 0, s>>>(g); break;
+    case 4: gemm_skinny_kernel<MB, NB, W, 4><<<grid, 64 * W, 0, s>>>(g); break;
+    default: gemm_skinny_kernel<MB, NB, W, 8><<<grid, 64 * W, 0, s>>>(g); break;
+    }
+}
+
+// (mb, nb, waves) variants: LDS holds waves * 32mb x 32nb floats (<= 64 KiB).
+void launch_skinny(const GemmPlan &p, const GemmArgs &g, dim3 grid, hipStream_t s) {
+    if (p.mb == 1 && p.nb == 4) launch_skinny_w<1, 4, 4>(p, g, grid, s);
+    else if (p.mb == 1 && p.nb == 2) launch_skinny_w<1, 2, 8>(p, g, grid, s);
+    else if (p.mb == 1) launch_skinny_w<1, 1, 8>(p, g, grid, s);
+    else if (p.nb == 2) launch_skinny_w<2, 2, 4>(p, g, grid, s);
+    else launch_skinny_w<2, 1, 8>(p, g, grid, s);
+}
+
 }  // namespace
 
-GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg) {
+GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned,
+                   bool force_skinny, int force_skinny_nb, int force_skinny_splits) {
     GemmPlan p{};
     p.M = M;
     p.N = N;
     p.K = K;
+    // Skinny path: M <= 64 (one or two 32-row blocks per wave), K % 4 == 0,
+    // a 16-byte aligned A and B under 2 GiB.  NB column blocks per wave: 4
+    // for M <= 32, 2 for M <= 64, fewer when N is not a multiple.  It is
+    // chosen for a B of 4 MiB and more: there it measured ahead of the tiled
+    // kernel (M=32, N=K=4096: 19.0 against 19.4 us, reduce included); on
+    // small B the tiled split-K kernel finishes first (more parallelism per
+    // MFMA chain), so the skinny path runs there only when forced.
+    const uint64_t b_bytes = (uint64_t)K * (uint64_t)N * 4u;
+    const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned &&
+                          b_bytes < (1ull << 31) && force_cfg < 0;
+    if (eligible && (force_skinny || b_bytes >= (4ull << 20))) {
+        p.skinny = true;
+        p.mb = M <= 32 ? 1 : 2;
+        int nb = p.mb == 1 ? 4 : 2;
+        if (force_skinny_nb == 1 || force_skinny_nb == 2 || (force_skinny_nb == 4 && p.mb == 1))
+            nb = force_skinny_nb;
+        while (nb > 1 && N % nb != 0) nb /= 2;
+        p.nb = nb;
+        p.waves = (nb == 1 || (nb == 2 && p.mb == 1)) ? 8 : 4;
+        const int W = p.waves;
+        const int chunk = 8 * (nb == 4 ? 4 : 8);
+        p.tiles_n = (N + 32 * nb - 1) / (32 * nb);
+        p.tiles = p.tiles_n;
+        // Splits: enough workgroups for every CU and one wave per SIMD
+        // (measured at M=32, N=K=4096: 8 splits of 4-wave groups beat 16;
+        // more waves per SIMD did not help).
+        int splits = (4 * num_cus + p.tiles * W - 1) / (p.tiles * W);
+        const int for_cus = (num_cus + p.tiles - 1) / p.tiles;
+        if (splits < for_cus) splits = for_cus;
+        const int max_splits = K / (chunk * W) > 1 ? K / (chunk * W) : 1;
+        if (splits > max_splits) splits = max_splits;
+        if (force_skinny_splits > 0) splits = force_skinny_splits;
+        if (splits > 64) splits = 64;
+        if (splits < 1) splits = 1;
+        // k_per_wave is chunk * CH for CH in {1, 2, 4, 8} (kernel variants);
+        // a longer range takes more splits instead.
+        const int kw_raw = (K + splits * W - 1) / (splits * W);
+        int ch = 1;
+        while (ch < 8 && chunk * ch < kw_raw) ch *= 2;
+        p.k_per_wave = chunk * ch;
+        p.k_per_split = p.k_per_wave * W;
+        p.splits = (K + p.k_per_split - 1) / p.k_per_split;
+        p.ws_floats = p.splits > 1 ? (size_t)p.splits * p.tiles * (32 * p.mb) * (32 * nb) : 0;
+        p.vec = true;
+        return p;
+    }
     // 128x256 tiles measured ~3% faster than 128x128 at 4096^3; they are used
     // whenever they alone still give every CU a tile.
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
@@ -358,6 +621,19 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
         q.interior = false;
     }
     GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits, epi};
+    if (p.skinny) {
+        const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
+        launch_skinny(p, g, grid, s);
+        if (p.splits > 1) {
+            const int BM = 32 * p.mb, BN = 32 * p.nb;
+            const int64_t work = (int64_t)p.tiles * BM * (BN / 4);
+            int64_t blocks = (work + 63) / 64;
+            if (blocks > 32768) blocks = 32768;
+            gemm_splitk_reduce<<<(unsigned)blocks, 64, 0, s>>>(ws, C, p.M, p.N, BM, BN, p.tiles_n,
+                                                               p.tiles, p.splits, epi);
+        }
+        return;
+    }
     switch (q.cfg) {
     case CFG_32x128: launch_cfg<32, 128, 32, 32, 32>(q, g, s); break;
     case CFG_64x64: launch_cfg<64, 64, 16, 32, 32>(q, g, s); break;
@@ -369,10 +645,10 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
     if (p.splits > 1) {
         const int BM = kCfgBM[q.cfg], BN = kCfgBN[q.cfg];
         const int64_t work = (int64_t)p.tiles * BM * (BN / 4);
-        int64_t blocks = (work + 255) / 256;
-        if (blocks > 8192) blocks = 8192;
-        gemm_splitk_reduce<<<(unsigned)blocks, 256, 0, s>>>(ws, C, p.M, p.N, BM, BN, p.tiles_n,
-                                                            p.tiles, p.splits, epi);
+        int64_t blocks = (work + 63) / 64;
+        if (blocks > 32768) blocks = 32768;
+        gemm_splitk_reduce<<<(unsigned)blocks, 64, 0, s>>>(ws, C, p.M, p.N, BM, BN, p.tiles_n,
+                                                           p.tiles, p.splits, epi);
     }
 }
 

@@ -25,10 +25,17 @@ struct GemmPlan {
     int M, N, K;
     int cfg;           // tile configuration
     int tiles, tiles_n;
-    int splits;        // K splits (1: no workspace)
+    int splits;        // K splits across workgroups (1: no workspace)
     int k_per_split;   // multiple of the configuration's K slab
     size_t ws_floats;  // split-K workspace
     bool vec, interior;
+    // Skinny path (M <= 64): one workgroup of `waves` waves per 32*nb
+    // columns and K split; each wave streams its own k_per_wave range of B.
+    bool skinny;
+    int mb;            // 32-row blocks per wave (1 or 2)
+    int nb;            // 32-column blocks per wave (1, 2 or 4)
+    int waves;         // waves per workgroup (K split inside the workgroup)
+    int k_per_wave;    // a whole number of pipeline chunks
 };
 // Optional epilogue fused into the GEMM store: bias add with Clove's
 // broadcast rule (bias read at flat index % bias_n) and an activation.
@@ -40,9 +47,15 @@ struct GemmEpilogue {
     int bias_mode = GEMM_BIAS_NONE;
     int act = GEMM_ACT_NONE;
 };
-// Picks the tile configuration and K split for a shape (force_cfg >= 0
-// overrides the configuration, for tuning).
-GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg);
+// Picks the tile configuration and K split for a shape.  a_aligned: A is
+// 16-byte aligned (the skinny path needs it).  force_cfg >= 0 overrides the
+// configuration and turns the skinny path off; force_skinny takes the skinny
+// path wherever it is legal, with force_skinny_nb (1, 2, 4) /
+// force_skinny_splits > 0 overriding its plan (tuning and tests).  Every
+// plan computes the same product.
+GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned = true,
+                   bool force_skinny = false, int force_skinny_nb = 0,
+                   int force_skinny_splits = 0);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
 

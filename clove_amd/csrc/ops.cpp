@@ -8,6 +8,8 @@
 // lazy planner emits for longer chains, so eager and fused results are
 // produced by identical device code.
 #include <cmath>
+#include <cstdint>
+#include <cstdio>
 #include <cstdlib>
 
 #include "common.hpp"
@@ -142,11 +144,22 @@ static void matmul_dims(const Tensor &a, const Tensor &b, size_t *m, size_t *k, 
                   CLOVE_HIP_ERR_SHAPE, "matmul dimensions exceed 2^31");
 }
 
-// CLOVE_GEMM_CFG selects a tile configuration by index (tuning sweeps only;
-// every configuration computes the same product).
+// CLOVE_GEMM_CFG selects a tile configuration by index and turns the
+// skinny path off; CLOVE_GEMM_SKINNY="nb,splits" forces the skinny path where
+// it is legal (M <= 64, K % 4 == 0) and sets its column blocks per wave and
+// K splits (0 keeps the default).  Both are for tuning sweeps only: every plan computes the same
+// product.
 static int gemm_cfg_override() {
     const char *v = std::getenv("CLOVE_GEMM_CFG");
     return (v && *v) ? std::atoi(v) : -1;
+}
+static bool gemm_skinny_override(int *nb, int *splits) {
+    *nb = 0;
+    *splits = 0;
+    const char *v = std::getenv("CLOVE_GEMM_SKINNY");
+    if (!v || !*v) return false;
+    if (std::sscanf(v, "%d,%d", nb, splits) < 1) *nb = 0;
+    return true;
 }
 
 void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, const Tensor *bias,
@@ -169,7 +182,11 @@ void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, cons
     CLOVE_REQUIRE(act >= k::GEMM_ACT_NONE && act <= k::GEMM_ACT_GELU, CLOVE_HIP_ERR_INVALID,
                   "unknown GEMM epilogue activation");
     epi.act = act;
-    const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override());
+    int sk_nb, sk_splits;
+    const bool sk_force = gemm_skinny_override(&sk_nb, &sk_splits);
+    const bool a_aligned = (reinterpret_cast<uintptr_t>(a.data) & 15) == 0;
+    const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override(),
+                                       a_aligned, sk_force, sk_nb, sk_splits);
     TensorNode ws;
     if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
     k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, epi, c.stream);

@@ -161,3 +161,25 @@ def test_concurrent_callers(hip):
     assert not errors, errors
     for g_, w in zip(got, want):
         assert_close(g_, w, 1e-4, 1e-9, "threaded softmax")
+
+
+@pytest.mark.parametrize("plan", ["0,1", "0,3", "1,2"])
+@pytest.mark.parametrize("m,k,n,bias_n,act", [(64, 784, 128, 128, "relu"), (32, 4096, 512, 3, "gelu")])
+def test_skinny_epilogue(hip, monkeypatch, plan, m, k, n, bias_n, act):
+    """The fused epilogue on the skinny path: applied in the kernel (one
+    split) or by the split-K reduce, equal to the eager composition's bits."""
+    monkeypatch.setenv("CLOVE_GEMM_SKINNY", plan)
+    gg = rng(5 * m + n)
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, bias_n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},{k}"), g.input(f"{k},{n}"), g.input(f"{bias_n}")
+    y = g.op(act, g.op("add", g.op("matmul", x, wi), bi))
+    model = g.compile([y])
+    ta, tw, tb = hip.tensor(a), hip.tensor(w), hip.tensor(b)
+    (fused,) = model.execute([ta, tw, tb])
+    eager = getattr(hip, act)(hip.add(hip.matmul(ta, tw), tb))
+    assert np.array_equal(fused.numpy(), eager.numpy())
+    want = getattr(oracle, act)(oracle.add(oracle.matmul(a, w), b))
+    assert_close(fused.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "skinny epilogue")

@@ -68,3 +68,54 @@ def test_config4_full(hip):
     assert np.max(np.abs(got[sub] - ref64)) < 1e-5
     a32 = a[:32].copy()
     check(hip.matmul(hip.tensor(a32), tb).numpy(), oracle.matmul(a32, b), "skinny 32x4096x4096")
+
+
+# The skinny path (M <= 64, K % 4 == 0, 16-byte aligned A): 32*nb columns
+# per workgroup, a K split over the workgroup's waves and across workgroups.
+# The plan picks it for B >= 4 MiB; CLOVE_GEMM_SKINNY forces it on the small
+# edge shapes here.
+@pytest.mark.parametrize("m,k,n", [(1, 4, 1), (5, 12, 33), (31, 20, 100), (32, 4096, 96),
+                                   (33, 784, 128), (63, 1028, 200), (64, 4100, 64),
+                                   (17, 8, 31), (64, 784, 10), (48, 2052, 40), (32, 36, 4096),
+                                   (30, 4096, 1000), (64, 2048, 1536)])
+def test_skinny_shapes(hip, monkeypatch, m, k, n):
+    monkeypatch.setenv("CLOVE_GEMM_SKINNY", "0")
+    g = rng(m * 11 + k * 5 + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    check(hip.matmul(hip.tensor(a), hip.tensor(b)).numpy(), oracle.matmul(a, b),
+          f"skinny {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m", [24, 40])
+@pytest.mark.parametrize("plan", ["4,1", "2,1", "1,2", "4,5", "2,7", "1,64", "4,64"])
+def test_skinny_plan_variants(hip, monkeypatch, m, plan):
+    """Every (column blocks per wave, K splits) choice of the skinny plan,
+    and the tiled path (CLOVE_GEMM_CFG), computes the same product within
+    the matmul bound; each plan is deterministic."""
+    g = rng(21 + m)
+    k, n = 3076, 72
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    want = oracle.matmul(a, b)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    monkeypatch.setenv("CLOVE_GEMM_SKINNY", plan)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, want, f"skinny plan {plan}")
+    assert np.array_equal(got, hip.matmul(ta, tb).numpy())
+    monkeypatch.delenv("CLOVE_GEMM_SKINNY")
+    monkeypatch.setenv("CLOVE_GEMM_CFG", "1")
+    check(hip.matmul(ta, tb).numpy(), want, "tiled path")
+
+
+def test_skinny_misaligned_a_falls_back(hip):
+    """A borrowed A that is not 16-byte aligned takes the tiled path (the
+    skinny kernel reads A in 16-byte vectors)."""
+    g = rng(22)
+    m, k, n = 16, 64, 48
+    a = g.normal(0, 1, (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    buf = hip.tensor(np.concatenate([[0.0], a.ravel()]).astype(np.float32))
+    av = hip.wrap(buf.device_ptr + 4, (m, k))
+    check(hip.matmul(av, hip.tensor(b)).numpy(), oracle.matmul(a, b), "misaligned A")
+    del av
