@@ -17,9 +17,10 @@ Rank 0 prints ONE JSON line on stdout:
                this host's cores
   parts        the other configurations measured in the same run: the
                broadcast chain, softmax and layer norm (GB/s), 4096^3 and
-               skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s) and
-               the MLP plan (us per forward), each with its roofline fraction
-               and a sampled CPU baseline.
+               skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
+               MLP plan (us per forward) and the backward passes and losses
+               (GB/s; the matmul backward in TFLOP/s), each with its roofline
+               fraction and a sampled CPU baseline.
 Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
 exits with a message.
 """
@@ -232,6 +233,85 @@ def bench_mlp(ca, oracle, args, out):
     log(f"mlp plan: {wall * 1e3:.1f} us/forward wall, {per.mean() * 1e3:.1f} us GPU")
 
 
+def bench_backward(ca, oracle, args, out):
+    """The backward row: each op at a config-sized shape, HBM roofline (the
+    matmul backward: FP32 MFMA), CPU baseline on a bounded sample."""
+    g = np.random.Generator(np.random.PCG64(7))
+    R, Cc, N = 8192, 4096, 4096 * 4096
+    x = ca.empty((R, Cc)).fill_normal(2, 0.0, 2.0)
+    y = ca.softmax(x)
+    dy = ca.empty((R, Cc)).fill_normal(21)
+    targets = ca.tensor(g.integers(0, Cc, R).astype(np.float32))
+    one = ca.tensor(np.ones(1, np.float32))
+    a = ca.empty((4096, 4096)).fill_normal(5)
+    b = ca.empty((4096, 4096)).fill_normal(6)
+    cases = [
+        ("softmax_backward", lambda: ca.softmax_backward(y, dy), 3 * 4 * R * Cc),
+        ("gelu_backward", lambda: ca.gelu_backward(a, b), 3 * 4 * N),
+        ("broadcast_grad", lambda: ca.broadcast_grad(a, 4096), 4 * N + 4 * 4096),
+        ("cross_entropy", lambda: ca.cross_entropy(x, targets), 4 * R * Cc + 4 * R),
+        ("cross_entropy_backward", lambda: ca.cross_entropy_backward(x, targets, one),
+         2 * 4 * R * Cc + 4 * R),
+        ("mse", lambda: ca.mse(a, b), 2 * 4 * N),
+        ("mse_backward", lambda: ca.mse_backward(a, b, one), 3 * 4 * N),
+    ]
+    for name, launch, nbytes in cases:
+        wall, per = timed(ca, launch, args.steps, args.warmup)
+        gbs = nbytes / (per.mean() * 1e-3) / 1e9
+        part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
+                "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+        if oracle is not None:
+            part["cpu_baseline"] = cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes)
+        out[name] = part
+        log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
+            f"{per.mean() * 1e3:.1f} us")
+    # matmul backward at 4096^3: grad_a and grad_b, two GEMMs and two transposes
+    dc = ca.empty((4096, 4096)).fill_normal(8)
+    steps = max(5, args.steps // 10)
+    wall, per = timed(ca, lambda: ca.matmul_backward(a, b, dc), steps, max(2, args.warmup // 5))
+    flops = 4.0 * 4096 ** 3
+    tf = flops / (per.mean() * 1e-3) / 1e12
+    part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
+            "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
+    if oracle is not None:
+        rows = 16
+        ah, bh, dch = a.numpy(), b.numpy(), dc.numpy()
+        t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch, da_rows=(0, rows),
+                                                    db_rows=(0, rows)), reps=1)
+        t *= 4096 / rows
+        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                "cores": oracle.threads(), "kind": "port",
+                                "sample": f"{rows} of 4096 rows of grad_a and of grad_b, scaled"}
+    out["matmul_backward_4096"] = part
+    log(f"matmul backward 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA "
+        f"peak), {per.mean():.3f} ms")
+
+
+def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
+    rows = 1024  # row-sampled cases: 1/8 of the 8192 rows, scaled
+    if name in ("softmax_backward", "cross_entropy", "cross_entropy_backward"):
+        th = targets.numpy()[:rows]
+        if name == "softmax_backward":
+            ys, dys = y.read(0, rows * 4096).reshape(rows, 4096), dy.read(0, rows * 4096).reshape(rows, 4096)
+            fn = lambda: oracle.softmax_backward(ys, dys)
+        else:
+            xs = x.read(0, rows * 4096).reshape(rows, 4096)
+            fn = (lambda: oracle.cross_entropy(xs, th)) if name == "cross_entropy" else \
+                (lambda: oracle.cross_entropy_backward(xs, th, 1.0))
+        t = cpu_time(fn) * (8192 / rows)
+        sample = f"{rows} of 8192 rows, scaled"
+    else:
+        ah, bh = a.numpy(), b.numpy()
+        fn = {"gelu_backward": lambda: oracle.gelu_backward(ah, bh),
+              "broadcast_grad": lambda: oracle.bias_grad(ah, 4096),
+              "mse": lambda: oracle.mse(ah, bh),
+              "mse_backward": lambda: oracle.mse_backward(ah, bh, 1.0)}[name]
+        t = cpu_time(fn)
+        sample = "full workload"
+    return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "cores": oracle.threads(),
+            "kind": "port", "sample": sample}
+
+
 # ---------------------------------------------------------------------------
 
 def main():
@@ -240,7 +320,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--parts", default="all",
-                    help="comma list of copy,bcast,rows,matmul,paged,mlp or 'all' / 'none' "
+                    help="comma list of copy,bcast,rows,matmul,paged,mlp,backward or 'all' / "
+                         "'none' "
                          "(the config 2 chain always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "hbm_traffic.json"),
@@ -256,7 +337,8 @@ def main():
     import clove_amd as ca
 
     ca.init(0)
-    parts = {"copy", "bcast", "rows", "matmul", "paged", "mlp"} if args.parts == "all" else \
+    parts = {"copy", "bcast", "rows", "matmul", "paged", "mlp", "backward"} \
+        if args.parts == "all" else \
         set() if args.parts == "none" else set(args.parts.split(","))
     oracle = None
     if not args.no_cpu:
@@ -324,6 +406,8 @@ def main():
         bench_paged(ca, oracle, args, out)
     if "mlp" in parts:
         bench_mlp(ca, oracle, args, out)
+    if "backward" in parts:
+        bench_backward(ca, oracle, args, out)
     if out:
         result["parts"] = out
     ca.synchronize()

@@ -107,6 +107,15 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_paged_attention_scaled": (vp, [vp, vp, vp, vp, vp, vp, f]),
         "clove_hip_paged_gather_indices": (vp, [vp, vp, C.c_int, C.c_int]),
         "clove_hip_paged_kv_append": (C.c_int, [vp, vp, vp, vp, vp]),
+        "clove_hip_relu_backward": (vp, [vp, vp]),
+        "clove_hip_gelu_backward": (vp, [vp, vp]),
+        "clove_hip_softmax_backward": (vp, [vp, vp]),
+        "clove_hip_matmul_backward": (C.c_int, [vp, vp, vp, C.POINTER(vp), C.POINTER(vp)]),
+        "clove_hip_broadcast_grad": (vp, [vp, sz, C.c_int]),
+        "clove_hip_cross_entropy": (vp, [vp, vp]),
+        "clove_hip_cross_entropy_backward": (vp, [vp, vp, vp]),
+        "clove_hip_mse": (vp, [vp, vp]),
+        "clove_hip_mse_backward": (vp, [vp, vp, vp]),
         "clove_hip_fused_chain": (C.c_int, [C.POINTER(ChainOp), C.c_int, C.POINTER(vp), C.c_int,
                                             C.POINTER(vp)]),
         "clove_hip_graph_create": (vp, []),
@@ -351,6 +360,53 @@ def layer_norm(a: Tensor, gamma: Tensor, beta: Tensor) -> Tensor:
 
 def matmul(a: Tensor, b: Tensor) -> Tensor:
     return _handle(lib().clove_hip_matmul(a.handle, b.handle))
+
+
+# ---- backward passes and losses (backend.rs autograd closures) -------------
+
+def relu_backward(x: Tensor, grad_out: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_relu_backward(x.handle, grad_out.handle))
+
+
+def gelu_backward(x: Tensor, grad_out: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_gelu_backward(x.handle, grad_out.handle))
+
+
+def softmax_backward(y: Tensor, grad_out: Tensor) -> Tensor:
+    """dx = y * (grad_out - sum(grad_out * y)) per row, y = softmax(x)."""
+    return _handle(lib().clove_hip_softmax_backward(y.handle, grad_out.handle))
+
+
+def matmul_backward(a: Tensor, b: Tensor, grad_out: Tensor, want_a: bool = True,
+                    want_b: bool = True):
+    """(grad_out . b^T, a^T . grad_out); a skipped product is None."""
+    da, db = C.c_void_p(), C.c_void_p()
+    _check(lib().clove_hip_matmul_backward(a.handle, b.handle, grad_out.handle,
+                                           C.byref(da) if want_a else None,
+                                           C.byref(db) if want_b else None))
+    return (Tensor(da.value) if want_a else None), (Tensor(db.value) if want_b else None)
+
+
+def broadcast_grad(grad_out: Tensor, b_numel: int, negate: bool = False) -> Tensor:
+    """Gradient of add's (negate=False) or sub's (True) broadcast operand."""
+    return _handle(lib().clove_hip_broadcast_grad(grad_out.handle, b_numel, int(negate)))
+
+
+def cross_entropy(logits: Tensor, targets: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_cross_entropy(logits.handle, targets.handle))
+
+
+def cross_entropy_backward(logits: Tensor, targets: Tensor, grad_loss: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_cross_entropy_backward(logits.handle, targets.handle,
+                                                          grad_loss.handle))
+
+
+def mse(pred: Tensor, target: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_mse(pred.handle, target.handle))
+
+
+def mse_backward(pred: Tensor, target: Tensor, grad_loss: Tensor) -> Tensor:
+    return _handle(lib().clove_hip_mse_backward(pred.handle, target.handle, grad_loss.handle))
 
 
 def paged_attention(q: Tensor, k: Optional[Tensor], v: Optional[Tensor], kv_cache: Tensor,

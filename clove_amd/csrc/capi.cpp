@@ -309,6 +309,64 @@ int clove_hip_paged_kv_append(CTensor kv_cache, CTensor k, CTensor v, CTensor bl
     });
 }
 
+// ---- backward passes and losses ------------------------------------------
+
+CTensor clove_hip_relu_backward(CTensor x, CTensor grad_out) {
+    return guarded_tensor([&] { return HipBackend::relu_backward(as_node(x), as_node(grad_out)); });
+}
+
+CTensor clove_hip_gelu_backward(CTensor x, CTensor grad_out) {
+    return guarded_tensor([&] { return HipBackend::gelu_backward(as_node(x), as_node(grad_out)); });
+}
+
+CTensor clove_hip_softmax_backward(CTensor y, CTensor grad_out) {
+    return guarded_tensor(
+        [&] { return HipBackend::softmax_backward(as_node(y), as_node(grad_out)); });
+}
+
+int clove_hip_matmul_backward(CTensor a, CTensor b, CTensor grad_out, CTensor *grad_a,
+                              CTensor *grad_b) {
+    if (grad_a) *grad_a = nullptr;
+    if (grad_b) *grad_b = nullptr;
+    TensorNode da, db;
+    const int st = guarded([&] {
+        HipBackend::matmul_backward(as_node(a), as_node(b), as_node(grad_out),
+                                    grad_a ? &da : nullptr, grad_b ? &db : nullptr);
+    });
+    if (st == CLOVE_HIP_OK) {
+        if (grad_a) *grad_a = into_raw(std::move(da));
+        if (grad_b) *grad_b = into_raw(std::move(db));
+    }
+    return st;
+}
+
+CTensor clove_hip_broadcast_grad(CTensor grad_out, size_t b_numel, int negate) {
+    return guarded_tensor(
+        [&] { return HipBackend::broadcast_grad(as_node(grad_out), b_numel, negate != 0); });
+}
+
+CTensor clove_hip_cross_entropy(CTensor logits, CTensor targets) {
+    return guarded_tensor(
+        [&] { return HipBackend::cross_entropy(as_node(logits), as_node(targets)); });
+}
+
+CTensor clove_hip_cross_entropy_backward(CTensor logits, CTensor targets, CTensor grad_loss) {
+    return guarded_tensor([&] {
+        return HipBackend::cross_entropy_backward(as_node(logits), as_node(targets),
+                                                  as_node(grad_loss));
+    });
+}
+
+CTensor clove_hip_mse(CTensor pred, CTensor target) {
+    return guarded_tensor([&] { return HipBackend::mse(as_node(pred), as_node(target)); });
+}
+
+CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss) {
+    return guarded_tensor([&] {
+        return HipBackend::mse_backward(as_node(pred), as_node(target), as_node(grad_loss));
+    });
+}
+
 CTensor clove_hip_paged_gather_indices(CTensor block_tables, CTensor context_lens, int block_size,
                                        int max_ctx) {
     return guarded_tensor([&] {

@@ -37,13 +37,16 @@ __device__ __forceinline__ float cl_cos(float x) { return cosf(x); }    // backe
 __device__ __forceinline__ float cl_scale(float x, float s) { return x * s; }  // backend.rs:1694
 // ReluGrad(x, g): select(0, g, x > 0) (lazy.rs:1757-1763)
 __device__ __forceinline__ float cl_relu_grad(float x, float g) { return x > 0.0f ? g : 0.0f; }
-// GeluGrad(x, g): derivative of the tanh-form GELU times g (lazy.rs:1764-1779)
+// GeluGrad(x, g): derivative of the tanh-form GELU times g (fused WGSL
+// lazy.rs:1764-1779; CPU backward backend.rs:1965-1981, whose rounding this
+// follows: 3.0 * 0.044715 is folded in f32 first and meets x*x as one
+// operand, 0.5 * x * sech2 * c * (...) is evaluated left to right).
 __device__ __forceinline__ float cl_gelu_grad(float x, float g) {
     const float x3 = (x * x) * x;
     const float t = tanhf(CL_GELU_K * (x + 0.044715f * x3));
     const float sech2 = 1.0f - t * t;
     const float d = 0.5f * (1.0f + t) +
-                    0.5f * x * sech2 * CL_GELU_K * (1.0f + 0.134145f * x * x);
+                    0.5f * x * sech2 * CL_GELU_K * (1.0f + (3.0f * 0.044715f) * (x * x));
     return g * d;
 }
 

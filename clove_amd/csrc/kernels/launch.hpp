@@ -20,6 +20,34 @@ void softmax_rows(const float *x, float *y, size_t rows, size_t cols, hipStream_
 void layer_norm_rows(const float *x, const float *gamma, const float *beta, float *y,
                      size_t rows, size_t cols, float eps, hipStream_t s);
 
+// Backward rows (rowwise.hip): softmax backward and cross entropy.  The
+// cross-entropy kernels read f32 class indices for the first `used` rows; a
+// class >= cols sets *err_flag.  cross_entropy_rows writes one value per row
+// ((l[t] - max) - ln(sum exp)), which ordered_sum turns into the loss.
+void softmax_backward_rows(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
+                           hipStream_t s);
+void cross_entropy_rows(const float *logits, const float *targets, size_t used, size_t rows,
+                        size_t cols, float *row_values, int *err_flag, hipStream_t s);
+void cross_entropy_backward_rows(const float *logits, const float *targets, size_t used,
+                                 size_t rows, size_t cols, const float *grad_loss, float *grad,
+                                 int *err_flag, hipStream_t s);
+
+// reduce.hip -- deterministic reductions and the transpose.
+// gb[j] = (negate ? -1 : 1) * sum_{i % nb == j} g[i]; part holds
+// broadcast_grad_workspace(n, nb) floats.
+size_t broadcast_grad_workspace(size_t n, size_t nb);
+void broadcast_grad(const float *g, size_t n, size_t nb, bool negate, float *part, float *gb,
+                    hipStream_t s);
+// out[0] = sum((p - t)^2) / n; part holds sq_diff_workspace(n) floats.
+size_t sq_diff_workspace(size_t n);
+void mse_loss(const float *p, const float *t, size_t n, float *part, float *out, hipStream_t s);
+void mse_backward(const float *p, const float *t, size_t n, const float *grad_loss, float *grad,
+                  hipStream_t s);
+// out[0] = (sign * sum of x[0..n)) / div, summed in a fixed order.
+void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hipStream_t s);
+// out[C][R] = in[R][C].
+void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s);
+
 // gemm_f32.hip -- C[M,N] = A[M,K] . B[K,N], row-major f32, MFMA f32 accumulate.
 struct GemmPlan {
     int M, N, K;

@@ -1,0 +1,312 @@
+// reduce.hip -- deterministic reductions of the backward pass and the
+// losses, and the transpose the matmul backward uses.
+//
+// Reference: the broadcast-operand gradient of add / sub (CPU backend.rs:
+// 1527-1538, 1800-1810; WGSL backend.rs:596-645) and the MSE / cross-entropy
+// losses (CPU backend.rs:2661-2680, 2765-2772; WGSL lazy.rs:4379-4500).  The
+// WGSL versions add into one f32 through a compare-and-swap loop, so their
+// result depends on the order the workgroups arrive in (and the bias one
+// folds a whole workgroup into the first thread's bin).  Here every sum is
+// a fixed tree: partial sums in registers, combined in LDS in a fixed order,
+// then one small pass over the partials, so results repeat bit for bit.
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "launch.hpp"
+#include "wave.h"
+
+namespace clove {
+namespace k {
+
+namespace {
+
+// ---- gradient of a broadcast operand: gb[j] = sum_{i % nb == j} g[i] ------
+
+// nb >= 64: thread per column; the grid's y dimension splits the rows
+// (row r holds elements r*nb .. r*nb + nb - 1) into chunks of rows_per.
+// part[chunk][j] = sum over the chunk's rows, in row order.
+__global__ void __launch_bounds__(256) bcast_grad_cols_kernel(const float *__restrict__ g,
+                                                              uint64_t n, uint64_t nb,
+                                                              uint64_t rows_per,
+                                                              float *__restrict__ part) {
+    const uint64_t j = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (j >= nb) return;
+    const uint64_t r0 = (uint64_t)blockIdx.y * rows_per;
+    float s = 0.0f;
+    uint64_t i = r0 * nb + j;
+    for (uint64_t r = 0; r < rows_per && i < n; ++r, i += nb) s += g[i];
+    part[(uint64_t)blockIdx.y * nb + j] = s;
+}
+
+// The same with four consecutive columns per thread and 16-byte loads
+// (nb % 4 == 0, g 16-byte aligned); each column is still summed in row
+// order.  The row loop is unrolled so sixteen loads are in flight.
+__global__ void __launch_bounds__(256) bcast_grad_cols4_kernel(const float *__restrict__ g,
+                                                               uint64_t n, uint64_t nb,
+                                                               uint64_t rows_per,
+                                                               float *__restrict__ part) {
+    const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // column quad
+    const uint64_t nq = nb / 4;
+    if (q >= nq) return;
+    const uint64_t r0 = (uint64_t)blockIdx.y * rows_per;
+    const uint64_t rows = (n + nb - 1) / nb;
+    const uint64_t r1 = r0 + rows_per < rows ? r0 + rows_per : rows;
+    const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(g);
+    cl_f4 s = {0.f, 0.f, 0.f, 0.f};
+    uint64_t r = r0;
+    // full rows only in the unrolled part (n % nb == 0 for all but the last)
+    const uint64_t full = n / nb;
+    const uint64_t r_full = r1 < full ? r1 : full;
+    for (; r + 16 <= r_full; r += 16) {
+        cl_f4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) v[u] = __builtin_nontemporal_load(g4 + (r + u) * nq + q);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) s += v[u];
+    }
+    for (; r < r1; ++r) {
+        const uint64_t i = r * nb + 4 * q;
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+            if (i + c < n) s[c] += g[i + c];
+    }
+    *reinterpret_cast<cl_f4 *>(part + (uint64_t)blockIdx.y * nb + 4 * q) = s;
+}
+
+// nb < 64: T = nb * (256 / nb) threads each own one column, (base + t) % nb,
+// and sum every T-th element of the workgroup's chunk (chunk starts are
+// multiples of T, hence of nb); the threads of one column are then added
+// in thread order.  part[chunk][j].
+__global__ void __launch_bounds__(256) bcast_grad_flat_kernel(const float *__restrict__ g,
+                                                              uint64_t n, int nb, int iters,
+                                                              float *__restrict__ part) {
+    __shared__ float acc[256];
+    const int T = nb * (256 / nb);
+    const int t = threadIdx.x;
+    const uint64_t base = (uint64_t)blockIdx.x * T * iters;
+    float s = 0.0f;
+    if (t < T) {
+        uint64_t i = base + t;
+        for (int k = 0; k < iters && i < n; ++k, i += T) s += g[i];
+    }
+    acc[t] = s;
+    __syncthreads();
+    if (t < nb) {
+        float c = 0.0f;
+        for (int q = t; q < T; q += nb) c += acc[q];
+        part[(uint64_t)blockIdx.x * nb + t] = c;
+    }
+}
+
+// gb[j] = sign * sum over chunks of part[chunk][j].  A workgroup covers 32
+// columns with 8 groups of threads; group k sums chunks [k*per, (k+1)*per)
+// in order (loads issued eight at a time), and the 8 group sums meet in LDS
+// and are added in group order: a fixed order, so the result is
+// deterministic, with 8x the parallelism of one thread per column.
+__global__ void __launch_bounds__(256) bcast_grad_final_kernel(const float *__restrict__ part,
+                                                               uint64_t chunks, uint64_t nb,
+                                                               float sign,
+                                                               float *__restrict__ gb) {
+    __shared__ float grp[8][32];
+    const int cl = threadIdx.x & 31, k = threadIdx.x >> 5;
+    const uint64_t j = (uint64_t)blockIdx.x * 32 + cl;
+    const uint64_t per = (chunks + 7) / 8;
+    const uint64_t c0 = (uint64_t)k * per;
+    const uint64_t c1 = c0 + per < chunks ? c0 + per : chunks;
+    float s = 0.0f;
+    if (j < nb) {
+        uint64_t c = c0;
+        for (; c + 8 <= c1; c += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = part[(c + u) * nb + j];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) s += v[u];
+        }
+        for (; c < c1; ++c) s += part[c * nb + j];
+    }
+    grp[k][cl] = s;
+    __syncthreads();
+    if (k == 0 && j < nb) {
+        float t = grp[0][cl];
+#pragma unroll
+        for (int q = 1; q < 8; ++q) t += grp[q][cl];
+        gb[j] = sign * t;
+    }
+}
+
+// ---- scalar losses ------------------------------------------------------
+
+// Sum of squared differences over a chunk of CHUNK elements per workgroup,
+// combined in a fixed order: part[block].
+// VEC: 16-byte loads (p and t 16-byte aligned); the chunk's tail past n is
+// read element by element.
+constexpr int kSqChunk = 256 * 64;
+template <bool VEC>
+__global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float *__restrict__ p,
+                                                              const float *__restrict__ t,
+                                                              uint64_t n,
+                                                              float *__restrict__ part) {
+    __shared__ float wsum[4];
+    const uint64_t base = (uint64_t)blockIdx.x * kSqChunk;
+    float s = 0.0f;
+    if (VEC && base + kSqChunk <= n) {
+        const cl_f4 *p4 = reinterpret_cast<const cl_f4 *>(p + base);
+        const cl_f4 *t4 = reinterpret_cast<const cl_f4 *>(t + base);
+        cl_f4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+        for (int k = 0; k < kSqChunk / 1024; ++k) {
+            const cl_f4 d = __builtin_nontemporal_load(p4 + k * 256 + threadIdx.x) -
+                            __builtin_nontemporal_load(t4 + k * 256 + threadIdx.x);
+            acc += d * d;
+        }
+        s = hsum4(acc);
+    } else {
+        for (int k = 0; k < kSqChunk / 256; ++k) {
+            const uint64_t i = base + (uint64_t)k * 256 + threadIdx.x;
+            if (i < n) {
+                const float d = p[i] - t[i];
+                s += d * d;
+            }
+        }
+    }
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) part[blockIdx.x] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+}
+
+// out[0] = (sign * sum of x[0..n)) / div, one workgroup, fixed order.
+// Thread t sums x[t], x[t + 256], ... with eight loads in flight (a single
+// workgroup has nothing else to hide its load latency behind).
+__global__ void __launch_bounds__(256) ordered_sum_kernel(const float *__restrict__ x, uint64_t n,
+                                                          float sign, float div,
+                                                          float *__restrict__ out) {
+    __shared__ float wsum[4];
+    float s = 0.0f;
+    uint64_t i = threadIdx.x;
+    for (; i + 7 * 256 < n; i += 8 * 256) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = x[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+    }
+    for (; i < n; i += 256) s += x[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) out[0] = (sign * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]))) / div;
+}
+
+// MSE backward (backend.rs:2780-2790): grad = 2 * (p - t) * g / n.
+__global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restrict__ p,
+                                                           const float *__restrict__ t,
+                                                           uint64_t n,
+                                                           const float *__restrict__ grad_loss,
+                                                           float *__restrict__ grad) {
+    const float g = grad_loss[0];
+    const float nf = (float)n;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+         i += (uint64_t)gridDim.x * 256)
+        grad[i] = 2.0f * (p[i] - t[i]) * g / nf;
+}
+
+// ---- transpose: out[c][r] = in[r][c] for an R x C matrix ------------------
+// 64x64 tiles through LDS (pitch 65 against bank conflicts); 256 threads,
+// each moving 16 elements.  Edge tiles are bounds-checked.
+__global__ void __launch_bounds__(256) transpose_kernel(const float *__restrict__ in,
+                                                        float *__restrict__ out, int R, int C) {
+    __shared__ float tile[64][65];
+    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // 64 x 4
+    const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int r = r0 + ty + 4 * k, c = c0 + tx;
+        if (r < R && c < C) tile[ty + 4 * k][tx] = in[(size_t)r * C + c];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const int c = c0 + ty + 4 * k, r = r0 + tx;
+        if (r < R && c < C) out[(size_t)c * R + r] = tile[tx][ty + 4 * k];
+    }
+}
+
+// Rows per chunk of the column kernel: 32 (enough workgroups to fill the
+// chip at 4096 x 4096), or more when that would need more than 16384
+// chunks (the grid's y dimension).
+size_t cols_rows_per(size_t rows) {
+    if (rows <= 32) return rows ? rows : 1;
+    const size_t need = (rows + 16383) / 16384;
+    return need > 32 ? need : 32;
+}
+
+}  // namespace
+
+size_t broadcast_grad_workspace(size_t n, size_t nb) {
+    if (nb == 0 || n == 0) return 0;
+    if (nb >= 64) {
+        const size_t rows = (n + nb - 1) / nb;
+        const size_t rows_per = cols_rows_per(rows);
+        return ((rows + rows_per - 1) / rows_per) * nb;
+    }
+    const size_t T = nb * (256 / nb), per = T * 64;
+    return ((n + per - 1) / per) * nb;
+}
+
+void broadcast_grad(const float *g, size_t n, size_t nb, bool negate, float *part, float *gb,
+                    hipStream_t s) {
+    if (nb == 0) return;
+    size_t chunks;
+    if (nb >= 64) {
+        const size_t rows = (n + nb - 1) / nb;
+        const size_t rows_per = cols_rows_per(rows);
+        chunks = (rows + rows_per - 1) / rows_per;
+        if (chunks && nb % 4 == 0 && (reinterpret_cast<uintptr_t>(g) & 15) == 0) {
+            const dim3 grid((unsigned)((nb / 4 + 255) / 256), (unsigned)chunks);
+            bcast_grad_cols4_kernel<<<grid, 256, 0, s>>>(g, n, nb, rows_per, part);
+        } else if (chunks) {
+            const dim3 grid((unsigned)((nb + 255) / 256), (unsigned)chunks);
+            bcast_grad_cols_kernel<<<grid, 256, 0, s>>>(g, n, nb, rows_per, part);
+        }
+    } else {
+        const size_t T = nb * (256 / nb), per = T * 64;
+        chunks = (n + per - 1) / per;
+        if (chunks) bcast_grad_flat_kernel<<<(unsigned)chunks, 256, 0, s>>>(g, n, (int)nb, 64, part);
+    }
+    bcast_grad_final_kernel<<<(unsigned)((nb + 31) / 32), 256, 0, s>>>(
+        part, chunks, nb, negate ? -1.0f : 1.0f, gb);
+}
+
+size_t sq_diff_workspace(size_t n) { return (n + kSqChunk - 1) / kSqChunk; }
+
+void mse_loss(const float *p, const float *t, size_t n, float *part, float *out, hipStream_t s) {
+    const size_t blocks = sq_diff_workspace(n);
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t)) & 15) == 0;
+    if (blocks && vec) sq_diff_partial_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
+    else if (blocks) sq_diff_partial_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
+    ordered_sum_kernel<<<1, 256, 0, s>>>(part, blocks, 1.0f, (float)n, out);
+}
+
+void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hipStream_t s) {
+    ordered_sum_kernel<<<1, 256, 0, s>>>(x, n, sign, div, out);
+}
+
+void mse_backward(const float *p, const float *t, size_t n, const float *grad_loss, float *grad,
+                  hipStream_t s) {
+    if (!n) return;
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    mse_backward_kernel<<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
+}
+
+void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s) {
+    if (!R || !C) return;
+    const dim3 grid((unsigned)((C + 63) / 64), (unsigned)((R + 63) / 64));
+    transpose_kernel<<<grid, 256, 0, s>>>(in, out, (int)R, (int)C);
+}
+
+}  // namespace k
+}  // namespace clove

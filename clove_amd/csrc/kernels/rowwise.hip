@@ -1,4 +1,5 @@
-// rowwise.hip -- row softmax and row layer norm.
+// rowwise.hip -- row softmax and row layer norm, and the row kernels of the
+// backward pass (softmax backward, cross entropy and its backward).
 //
 // Reference: the CPU kernels (softmax backend.rs:2102-2125, layer_norm
 // backend.rs:2380-2405) and the lazy WGSL (lazy.rs:4718-4737, 4786-4806),
@@ -178,6 +179,189 @@ __global__ void __launch_bounds__(256) layer_norm_loop_kernel(const float *__res
     for (int c = lane; c < cols; c += 64) yr[c] = ((xr[c] - mean) / sd) * gamma[c] + beta[c];
 }
 
+// ---- backward and loss rows ----------------------------------------------
+
+// Softmax backward (backend.rs:2163-2183): dx = y * (dy - sum(dy * y)) per
+// row, the row of y and of dy held in registers.
+template <int VPT>
+__global__ void __launch_bounds__(256) softmax_bw_wave_kernel(const float *__restrict__ y,
+                                                              const float *__restrict__ dy,
+                                                              float *__restrict__ dx, int rows,
+                                                              int cols) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nvec = cols >> 2;
+    const cl_f4 *yr = reinterpret_cast<const cl_f4 *>(y + row * (long)cols);
+    const cl_f4 *gr = reinterpret_cast<const cl_f4 *>(dy + row * (long)cols);
+    cl_f4 *o = reinterpret_cast<cl_f4 *>(dx + row * (long)cols);
+    cl_f4 vy[VPT], vg[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        const bool in = c < nvec;
+        vy[i] = in ? __builtin_nontemporal_load(yr + c) : (cl_f4){0.f, 0.f, 0.f, 0.f};
+        vg[i] = in ? __builtin_nontemporal_load(gr + c) : (cl_f4){0.f, 0.f, 0.f, 0.f};
+    }
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) s += hsum4(vg[i] * vy[i]);
+    s = wave_sum(s);
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nvec) __builtin_nontemporal_store(vy[i] * (vg[i] - s), o + c);
+    }
+}
+
+__global__ void __launch_bounds__(256) softmax_bw_loop_kernel(const float *__restrict__ y,
+                                                              const float *__restrict__ dy,
+                                                              float *__restrict__ dx, int rows,
+                                                              int cols) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float *yr = y + row * (long)cols, *gr = dy + row * (long)cols;
+    float *o = dx + row * (long)cols;
+    float s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s += gr[c] * yr[c];
+    s = wave_sum(s);
+    for (int c = lane; c < cols; c += 64) o[c] = yr[c] * (gr[c] - s);
+}
+
+// Rust's `f32 as usize` saturates: NaN and negative targets read class 0.
+__device__ __forceinline__ long target_class(float v) {
+    if (!(v > 0.0f)) return 0;
+    return v >= 9.0e18f ? (long)9.0e18 : (long)v;
+}
+
+// Cross entropy, one wave per row (backend.rs:2661-2680): row value
+// v = (l[t] - max) - ln(sum exp(l - max)); the loss is -sum(v) / rows, which
+// loss_final sums in a fixed order.  Rows at or past `used` (no target)
+// give 0; a class >= cols raises the error flag and gives 0.
+// MODE 0 writes v to rowv[row].  MODE 1 is the backward (backend.rs:
+// 2686-2712): grad = (exp(l - max) / sum - [j == t]) * g / rows.
+template <int VPT, int MODE>
+__global__ void __launch_bounds__(256) cross_entropy_wave_kernel(
+    const float *__restrict__ logits, const float *__restrict__ targets, long used, int rows,
+    int cols, const float *__restrict__ grad_loss, float *__restrict__ out, int *err_flag) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int nvec = cols >> 2;
+    cl_f4 *go = MODE == 1 ? reinterpret_cast<cl_f4 *>(out + row * (long)cols) : nullptr;
+    // The row's loads go out first: read after the target (and a branch on
+    // it), they would wait one memory latency per row.
+    const cl_f4 *lr = reinterpret_cast<const cl_f4 *>(logits + row * (long)cols);
+    cl_f4 v[VPT];
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        v[i] = c < nvec ? __builtin_nontemporal_load(lr + c)
+                        : (cl_f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+    }
+    long t = -1;
+    if (row < used) {
+        t = target_class(targets[row]);
+        if (t >= cols) {
+            if (lane == 0) *err_flag = 1;
+            t = -1;
+        }
+    }
+    if (t < 0) {  // no target (or a bad one): the row contributes nothing
+        if (MODE == 0) {
+            if (lane == 0) out[row] = 0.0f;
+        } else {
+            for (int c = lane; c < nvec; c += 64) go[c] = (cl_f4){0.f, 0.f, 0.f, 0.f};
+        }
+        return;
+    }
+    // l[t] from the registers of the lane that holds it (vector t/4 lives in
+    // lane (t/4) % 64, slot (t/4) / 64), not from a second global load.
+    float lt = 0.0f;
+    if (MODE == 0) {
+        const int tv = (int)(t >> 2), ts = (int)(t & 3);
+#pragma unroll
+        for (int i = 0; i < VPT; ++i)
+            if (lane + 64 * i == tv) lt = v[i][ts];
+        lt = __shfl(lt, tv & 63, 64);
+    }
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) m = fmaxf(m, hmax4(v[i]));
+    m = wave_max(m);
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        if (lane + 64 * i < nvec) {
+            v[i] = (cl_f4){fast_exp(v[i].x - m), fast_exp(v[i].y - m), fast_exp(v[i].z - m),
+                           fast_exp(v[i].w - m)};
+            s += hsum4(v[i]);
+        }
+    }
+    s = wave_sum(s);
+    if (MODE == 0) {
+        if (lane == 0) out[row] = (lt - m) - logf(s);
+        return;
+    }
+    const float inv = 1.0f / s;
+    const float g = grad_loss[0];
+    const float fr = (float)rows;
+#pragma unroll
+    for (int i = 0; i < VPT; ++i) {
+        const int c = lane + 64 * i;
+        if (c < nvec) {
+            cl_f4 p = v[i] * inv;
+            const long j0 = 4l * c;
+            if (t >= j0 && t < j0 + 4) p[t - j0] -= 1.0f;
+            __builtin_nontemporal_store((p * g) / fr, go + c);
+        }
+    }
+}
+
+// Any width: the same, re-reading the row.
+template <int MODE>
+__global__ void __launch_bounds__(256) cross_entropy_loop_kernel(
+    const float *__restrict__ logits, const float *__restrict__ targets, long used, int rows,
+    int cols, const float *__restrict__ grad_loss, float *__restrict__ out, int *err_flag) {
+    const int lane = threadIdx.x & 63;
+    const long row = (long)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float *go = MODE == 1 ? out + row * (long)cols : nullptr;
+    long t = -1;
+    if (row < used) {
+        t = target_class(targets[row]);
+        if (t >= cols) {
+            if (lane == 0) *err_flag = 1;
+            t = -1;
+        }
+    }
+    if (t < 0) {
+        if (MODE == 0) {
+            if (lane == 0) out[row] = 0.0f;
+        } else {
+            for (int c = lane; c < cols; c += 64) go[c] = 0.0f;
+        }
+        return;
+    }
+    const float *lr = logits + row * (long)cols;
+    float m = -INFINITY;
+    for (int c = lane; c < cols; c += 64) m = fmaxf(m, lr[c]);
+    m = wave_max(m);
+    float s = 0.0f;
+    for (int c = lane; c < cols; c += 64) s += fast_exp(lr[c] - m);
+    s = wave_sum(s);
+    if (MODE == 0) {
+        if (lane == 0) out[row] = (lr[t] - m) - logf(s);
+        return;
+    }
+    const float inv = 1.0f / s, g = grad_loss[0], fr = (float)rows;
+    for (int c = lane; c < cols; c += 64) {
+        const float p = fast_exp(lr[c] - m) * inv - (c == t ? 1.0f : 0.0f);
+        go[c] = (p * g) / fr;
+    }
+}
+
 int pick_vpt(int cols) {
     if (cols % 4 != 0) return 0;
     const int need = (cols / 4 + 63) / 64;
@@ -223,6 +407,54 @@ void layer_norm_rows(const float *x, const float *gamma, const float *beta, floa
     case 32: layer_norm_wave_kernel<32><<<grid, 256, lds, s>>>(x, gamma, beta, y, r, c, eps); break;
     default: layer_norm_loop_kernel<<<grid, 256, 0, s>>>(x, gamma, beta, y, r, c, eps); break;
     }
+}
+
+void softmax_backward_rows(const float *y, const float *dy, float *dx, size_t rows, size_t cols,
+                           hipStream_t s) {
+    if (!rows || !cols) return;
+    const unsigned grid = (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int r = (int)rows, c = (int)cols;
+    const int vpt = (aligned16(y) && aligned16(dy) && aligned16(dx)) ? pick_vpt(c) : 0;
+    switch (vpt) {
+    case 1: softmax_bw_wave_kernel<1><<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    case 2: softmax_bw_wave_kernel<2><<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    case 4: softmax_bw_wave_kernel<4><<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    case 8: softmax_bw_wave_kernel<8><<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    case 16: softmax_bw_wave_kernel<16><<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    default: softmax_bw_loop_kernel<<<grid, 256, 0, s>>>(y, dy, dx, r, c); break;
+    }
+}
+
+template <int MODE>
+static void cross_entropy_launch(const float *logits, const float *targets, size_t used,
+                                 size_t rows, size_t cols, const float *grad_loss, float *out,
+                                 int *err_flag, hipStream_t s) {
+    const unsigned grid = (unsigned)((rows + kRowsPerBlock - 1) / kRowsPerBlock);
+    const int r = (int)rows, c = (int)cols;
+    const long u = (long)used;
+    const bool al = aligned16(logits) && (MODE == 0 || aligned16(out));
+    const int vpt = al ? pick_vpt(c) : 0;
+    switch (vpt) {
+    case 1: cross_entropy_wave_kernel<1, MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    case 2: cross_entropy_wave_kernel<2, MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    case 4: cross_entropy_wave_kernel<4, MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    case 8: cross_entropy_wave_kernel<8, MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    case 16: cross_entropy_wave_kernel<16, MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    default: cross_entropy_loop_kernel<MODE><<<grid, 256, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); break;
+    }
+}
+
+void cross_entropy_rows(const float *logits, const float *targets, size_t used, size_t rows,
+                        size_t cols, float *row_values, int *err_flag, hipStream_t s) {
+    if (!rows || !cols) return;
+    cross_entropy_launch<0>(logits, targets, used, rows, cols, nullptr, row_values, err_flag, s);
+}
+
+void cross_entropy_backward_rows(const float *logits, const float *targets, size_t used,
+                                 size_t rows, size_t cols, const float *grad_loss, float *grad,
+                                 int *err_flag, hipStream_t s) {
+    if (!rows || !cols) return;
+    cross_entropy_launch<1>(logits, targets, used, rows, cols, grad_loss, grad, err_flag, s);
 }
 
 }  // namespace k

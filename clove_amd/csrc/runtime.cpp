@@ -201,8 +201,9 @@ void synchronize() {
     if (flag) {
         CLOVE_HIP_CHECK(hipMemset(g_err_flag, 0, 4));
         fail(CLOVE_HIP_ERR_RANGE,
-             "an earlier paged_attention call met a block-table entry outside the KV pool "
-             "(those tokens were skipped)");
+             "an earlier call met an index out of range: a block-table entry outside the KV "
+             "pool (those tokens were skipped) or a cross-entropy target >= the number of "
+             "classes (that row counted 0)");
     }
 }
 

@@ -80,6 +80,21 @@ struct HipBackend {
                                            const TensorNode &context_lens, int block_size,
                                            int max_ctx);
 
+    // Backward passes and losses (grad.cpp; the autograd closures of
+    // backend.rs).
+    static TensorNode relu_backward(const TensorNode &x, const TensorNode &grad_out);
+    static TensorNode gelu_backward(const TensorNode &x, const TensorNode &grad_out);
+    static TensorNode softmax_backward(const TensorNode &y, const TensorNode &grad_out);
+    static void matmul_backward(const TensorNode &a, const TensorNode &b, const TensorNode &grad_out,
+                                TensorNode *grad_a, TensorNode *grad_b);
+    static TensorNode broadcast_grad(const TensorNode &grad_out, size_t b_numel, bool negate);
+    static TensorNode cross_entropy(const TensorNode &logits, const TensorNode &targets);
+    static TensorNode cross_entropy_backward(const TensorNode &logits, const TensorNode &targets,
+                                             const TensorNode &grad_loss);
+    static TensorNode mse(const TensorNode &pred, const TensorNode &target);
+    static TensorNode mse_backward(const TensorNode &pred, const TensorNode &target,
+                                   const TensorNode &grad_loss);
+
     // Launch-only forms writing into caller-provided outputs (used by the
     // planner, whose buffers are pre-assigned).
     static void softmax_into(const Tensor &a, Tensor &out);

@@ -186,6 +186,49 @@ CTensor clove_hip_paged_gather_indices(CTensor block_tables, CTensor context_len
                                        int block_size, int max_ctx);
 
 /* ---------------------------------------------------------------------- */
+/* Backward passes and losses: the autograd closures WgpuBackend attaches  */
+/* to its ops (backend.rs), as device ops returning new tensors.  Every    */
+/* reduction sums in a fixed order (the reference's WGSL uses f32          */
+/* compare-and-swap atomics), so results repeat bit for bit.               */
+/* ---------------------------------------------------------------------- */
+
+/* backend.rs:1858-1870 (relu backward): grad_out where x > 0, else 0 (x or
+ * relu(x) may be passed: both are positive at the same places). */
+CTensor clove_hip_relu_backward(CTensor x, CTensor grad_out);
+/* backend.rs:1965-1981 (gelu backward): grad_out times the derivative of
+ * the tanh-form GELU at x. */
+CTensor clove_hip_gelu_backward(CTensor x, CTensor grad_out);
+/* backend.rs:2163-2183 (softmax backward): from y = softmax(x) and
+ * grad_out, per row dx = y * (grad_out - sum(grad_out * y)). */
+CTensor clove_hip_softmax_backward(CTensor y, CTensor grad_out);
+/* backend.rs:1314-1360 (matmul backward): *grad_a = grad_out . b^T (with
+ * a's shape), *grad_b = a^T . grad_out ([k, n]); grad_out holds m*n
+ * elements (m = product of a's leading dims).  Either output pointer may be
+ * NULL to skip that product.  Returns a status. */
+int clove_hip_matmul_backward(CTensor a, CTensor b, CTensor grad_out, CTensor *grad_a,
+                              CTensor *grad_b);
+/* backend.rs:1527-1538 (add) and 1800-1810 (sub): gradient of the
+ * broadcast operand b, gb[i % b_numel] += grad_out[i] (negate = 0, add) or
+ * -= (negate = 1, sub); f32 [b_numel].  (The reference's WGSL version folds
+ * each workgroup into one bin through a CAS loop, backend.rs:596-645.) */
+CTensor clove_hip_broadcast_grad(CTensor grad_out, size_t b_numel, int negate);
+/* backend.rs:2661-2680 (cross entropy): logits f32 [rows, cols] (rows = all
+ * leading dims), targets f32 class indices; the first min(rows,
+ * numel(targets)) rows contribute -log softmax(row)[target] and the sum is
+ * divided by rows.  Returns f32 [1, 1].  A class >= cols (a panic in the
+ * reference) is reported as CLOVE_HIP_ERR_RANGE by the next synchronising
+ * call. */
+CTensor clove_hip_cross_entropy(CTensor logits, CTensor targets);
+/* backend.rs:2686-2712: (softmax(row) - onehot(target)) * grad_loss / rows,
+ * rows without a target get 0; grad_loss is a 1-element tensor. */
+CTensor clove_hip_cross_entropy_backward(CTensor logits, CTensor targets, CTensor grad_loss);
+/* backend.rs:2765-2772 (mse): mean over pred's elements of
+ * (pred - target)^2; f32 [1, 1]. */
+CTensor clove_hip_mse(CTensor pred, CTensor target);
+/* backend.rs:2780-2790: 2 * (pred - target) * grad_loss / numel(pred). */
+CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss);
+
+/* ---------------------------------------------------------------------- */
 /* Fused elementwise chain: the counterpart of Step::Fused                 */
 /* (codegen lazy.rs:1694-1838, broadcast rule lazy.rs:1600-1608).         */
 /* ---------------------------------------------------------------------- */

@@ -57,6 +57,18 @@ def lib() -> C.CDLL:
                                                  C.c_int, C.c_int, C.c_int, C.c_int, C.c_float,
                                                  C.POINTER(C.c_double)]
         L.oracle_paged_slots.argtypes = [i32p, C.c_int, i32p, C.c_int, C.c_int, C.c_int, i32p]
+        L.oracle_relu_backward.argtypes = [fp, fp, sz, fp]
+        L.oracle_gelu_backward.argtypes = [fp, fp, sz, fp]
+        L.oracle_softmax_backward.argtypes = [fp, fp, sz, sz, fp]
+        L.oracle_matmul_backward_rows.argtypes = [fp, fp, fp, sz, sz, sz, sz, sz, sz, sz, fp, fp]
+        L.oracle_bias_grad.argtypes = [fp, sz, sz, C.c_int, fp]
+        L.oracle_cross_entropy.argtypes = [fp, fp, sz, sz, sz, fp]
+        L.oracle_cross_entropy.restype = C.c_int
+        L.oracle_cross_entropy_backward.argtypes = [fp, fp, sz, sz, sz, C.c_float, fp]
+        L.oracle_cross_entropy_backward.restype = C.c_int
+        L.oracle_mse.argtypes = [fp, fp, sz]
+        L.oracle_mse.restype = C.c_float
+        L.oracle_mse_backward.argtypes = [fp, fp, sz, C.c_float, fp]
         L.oracle_threads.restype = C.c_int
         L.oracle_set_threads.argtypes = [C.c_int]
         _lib = L
@@ -295,3 +307,91 @@ def mlp_forward(x, w1, b1, w2, b2):
     (nn.rs:115-118: matmul then add with b[i % out]), relu and softmax."""
     h = relu(add(matmul(x, w1), b1))
     return softmax(add(matmul(h, w2), b2))
+
+
+# ---------------------------------------------------------------------------
+# backward passes and losses
+# ---------------------------------------------------------------------------
+
+def relu_backward(x, g):
+    """backend.rs:1858-1870: g where relu's output (equivalently x) > 0."""
+    x, g = _f32(x), _f32(g)
+    out = np.empty_like(x)
+    lib().oracle_relu_backward(_f(x), _f(g), x.size, _f(out))
+    return out
+
+
+def gelu_backward(x, g):
+    """backend.rs:1965-1981: g times the tanh-form GELU derivative."""
+    x, g = _f32(x), _f32(g)
+    out = np.empty_like(x)
+    lib().oracle_gelu_backward(_f(x), _f(g), x.size, _f(out))
+    return out
+
+
+def softmax_backward(y, dy):
+    """backend.rs:2163-2183: dx = y * (dy - sum(dy * y)) per row."""
+    y, dy = _f32(y), _f32(dy)
+    cols = y.shape[-1]
+    out = np.empty_like(y)
+    lib().oracle_softmax_backward(_f(y), _f(dy), y.size // cols, cols, _f(out))
+    return out
+
+
+def matmul_backward(a, b, dc, da_rows: Optional[tuple] = None, db_rows: Optional[tuple] = None):
+    """backend.rs:1314-1360: dA = dC . B^T and dB = A^T . dC as sequential
+    f32 dots.  da_rows / db_rows restrict the computed rows (others stay 0)."""
+    a, b, dc = _f32(a), _f32(b), _f32(dc)
+    k = a.shape[-1]
+    m = a.size // k
+    n = b.shape[1]
+    da = np.zeros((m, k), np.float32)
+    db = np.zeros((k, n), np.float32)
+    r0, r1 = da_rows or (0, m)
+    s0, s1 = db_rows or (0, k)
+    lib().oracle_matmul_backward_rows(_f(a), _f(b), _f(dc), m, k, n, r0, r1, s0, s1, _f(da), _f(db))
+    return da.reshape(a.shape), db
+
+
+def bias_grad(g, nb: int, negate: bool = False):
+    """backend.rs:1527-1538 (add) / 1800-1810 (sub): the b operand's gradient,
+    gb[i % nb] (+/-)= g[i] folded in index order."""
+    g = _f32(g)
+    out = np.empty(nb, np.float32)
+    lib().oracle_bias_grad(_f(g), g.size, nb, int(negate), _f(out))
+    return out
+
+
+def cross_entropy(logits, targets):
+    """backend.rs:2661-2680: mean over rows of logsumexp(row) - row[target]."""
+    l, t = _f32(logits), _f32(targets)
+    out = np.zeros(1, np.float32)
+    cols = l.shape[-1]
+    if lib().oracle_cross_entropy(_f(l), _f(t), t.size, l.size // cols, cols, _f(out)) != 0:
+        raise IndexError("cross_entropy: target index out of range")
+    return out.reshape(1, 1)
+
+
+def cross_entropy_backward(logits, targets, g: float = 1.0):
+    """backend.rs:2686-2712: (softmax(row) - onehot(target)) * g / rows."""
+    l, t = _f32(logits), _f32(targets)
+    out = np.empty_like(l)
+    cols = l.shape[-1]
+    if lib().oracle_cross_entropy_backward(_f(l), _f(t), t.size, l.size // cols, cols, g,
+                                           _f(out)) != 0:
+        raise IndexError("cross_entropy: target index out of range")
+    return out
+
+
+def mse(p, t):
+    """backend.rs:2765-2772: mean of (p - t)^2."""
+    p, t = _f32(p), _f32(t)
+    return np.array([[lib().oracle_mse(_f(p), _f(t), p.size)]], np.float32)
+
+
+def mse_backward(p, t, g: float = 1.0):
+    """backend.rs:2780-2790: 2 * (p - t) * g / n."""
+    p, t = _f32(p), _f32(t)
+    out = np.empty_like(p)
+    lib().oracle_mse_backward(_f(p), _f(t), p.size, g, _f(out))
+    return out

@@ -456,3 +456,201 @@ void oracle_paged_slots(const int32_t *block_tables, int max_blocks, const int32
                     ? block_tables[(size_t)b * max_blocks + t / block_size] * block_size + t % block_size
                     : -1;
 }
+
+/* ------------------------------------------------------------------ */
+/* backward passes and losses (the autograd closures of backend.rs)    */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    const float *x, *g;
+    float *out;
+    float s;
+} bw_ctx;
+
+/* backend.rs:1858-1870 (relu backward): p_grad[i] = out[i] > 0 ? g[i] : 0
+ * with out = relu(x); out > 0 exactly when x > 0, so x may be passed. */
+static void relu_bw_body(size_t b, size_t e, void *p) {
+    bw_ctx *c = (bw_ctx *)p;
+    for (size_t i = b; i < e; ++i) c->out[i] = c->x[i] > 0.0f ? c->g[i] : 0.0f;
+}
+void oracle_relu_backward(const float *x, const float *g, size_t n, float *out) {
+    bw_ctx c = {x, g, out, 0.f};
+    parallel_for(n, relu_bw_body, &c);
+}
+
+/* backend.rs:1965-1981 (gelu backward), left to right as Rust evaluates it:
+ *   c = (2/pi).sqrt(); inner = c * (x + 0.044715 * x.powi(3));
+ *   sech2 = 1 - inner.tanh().powi(2);
+ *   d = 0.5 * (1 + inner.tanh()) + 0.5 * x * sech2 * c * (1 + 3.0 * 0.044715 * x.powi(2));
+ *   p_grad = g * d
+ * 3.0 * 0.044715 is folded in f32 before it meets x*x, as Rust folds it. */
+static void gelu_bw_body(size_t b, size_t e, void *p) {
+    bw_ctx *c = (bw_ctx *)p;
+    const float k = gelu_c();
+    const float k3 = 3.0f * 0.044715f;
+    for (size_t i = b; i < e; ++i) {
+        const float x = c->x[i];
+        const float x3 = (x * x) * x;
+        const float t = tanhf(k * (x + 0.044715f * x3));
+        const float sech2 = 1.0f - t * t;
+        const float d = 0.5f * (1.0f + t) + 0.5f * x * sech2 * k * (1.0f + k3 * (x * x));
+        c->out[i] = c->g[i] * d;
+    }
+}
+void oracle_gelu_backward(const float *x, const float *g, size_t n, float *out) {
+    bw_ctx c = {x, g, out, 0.f};
+    parallel_for(n, gelu_bw_body, &c);
+}
+
+/* backend.rs:2163-2183 (softmax backward): s = sum_j dy[j]*y[j] as a
+ * sequential fold, then dx[j] = y[j] * (dy[j] - s). */
+static void softmax_bw_rows(size_t r0, size_t r1, void *p) {
+    row_ctx *c = (row_ctx *)p;
+    const size_t cols = c->cols;
+    for (size_t i = r0; i < r1; ++i) {
+        const float *y = c->a + i * cols, *dy = c->g + i * cols;
+        float *o = c->out + i * cols;
+        float s = 0.0f;
+        for (size_t j = 0; j < cols; ++j) s += dy[j] * y[j];
+        for (size_t j = 0; j < cols; ++j) o[j] = y[j] * (dy[j] - s);
+    }
+}
+void oracle_softmax_backward(const float *y, const float *dy, size_t rows, size_t cols,
+                             float *dx) {
+    row_ctx c = {y, dy, NULL, cols, dx};
+    parallel_for(rows, softmax_bw_rows, &c);
+}
+
+/* backend.rs:1314-1360 (matmul backward), both loops sequential f32 dots:
+ *   dA[r][c] = sum_{i<n} dC[r*n + i] * B[c*n + i]     (dA = dC . B^T, m x k)
+ *   dB[r][c] = sum_{i<m} A[i*k + r] * dC[i*n + c]     (dB = A^T . dC, k x n)
+ * Rows [r0, r1) of each are computed (a bounded sample for the baseline). */
+typedef struct {
+    const float *a, *b, *dc;
+    size_t m, k, n;
+    float *out;
+} mmb_ctx;
+static void mmb_da_rows(size_t r0, size_t r1, void *p) {
+    mmb_ctx *c = (mmb_ctx *)p;
+    for (size_t r = r0; r < r1; ++r)
+        for (size_t col = 0; col < c->k; ++col) {
+            float s = 0.0f;
+            for (size_t i = 0; i < c->n; ++i) s += c->dc[r * c->n + i] * c->b[col * c->n + i];
+            c->out[r * c->k + col] = s;
+        }
+}
+static void mmb_db_rows(size_t r0, size_t r1, void *p) {
+    mmb_ctx *c = (mmb_ctx *)p;
+    for (size_t r = r0; r < r1; ++r)
+        for (size_t col = 0; col < c->n; ++col) {
+            float s = 0.0f;
+            for (size_t i = 0; i < c->m; ++i) s += c->a[i * c->k + r] * c->dc[i * c->n + col];
+            c->out[r * c->n + col] = s;
+        }
+}
+typedef struct {
+    range_fn fn;
+    mmb_ctx *c;
+    size_t r0;
+} offset_ctx;
+static void offset_body(size_t b, size_t e, void *p) {
+    offset_ctx *o = (offset_ctx *)p;
+    o->fn(o->r0 + b, o->r0 + e, o->c);
+}
+void oracle_matmul_backward_rows(const float *a, const float *b, const float *dc, size_t m,
+                                 size_t k, size_t n, size_t da_r0, size_t da_r1, size_t db_r0,
+                                 size_t db_r1, float *da, float *db) {
+    mmb_ctx c1 = {a, b, dc, m, k, n, da};
+    offset_ctx o1 = {mmb_da_rows, &c1, da_r0};
+    if (da && da_r1 > da_r0) parallel_for(da_r1 - da_r0, offset_body, &o1);
+    mmb_ctx c2 = {a, b, dc, m, k, n, db};
+    offset_ctx o2 = {mmb_db_rows, &c2, db_r0};
+    if (db && db_r1 > db_r0) parallel_for(db_r1 - db_r0, offset_body, &o2);
+}
+
+/* backend.rs:1527-1538 (add backward, b operand): gb[i % nb] += g[i] over
+ * i in order; backend.rs:1800-1810 (sub): gb[i % nb] -= g[i].  One thread:
+ * the fold order is the reference's. */
+void oracle_bias_grad(const float *g, size_t n, size_t nb, int negate, float *gb) {
+    for (size_t j = 0; j < nb; ++j) gb[j] = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        if (negate) gb[i % nb] -= g[i];
+        else gb[i % nb] += g[i];
+    }
+}
+
+/* Rust's `f32 as usize` saturates: NaN and negatives give 0. */
+static size_t target_index(float v) {
+    if (!(v > 0.0f)) return 0;
+    if (v >= 18446744073709551615.0f) return (size_t)-1;
+    return (size_t)v;
+}
+
+/* backend.rs:2661-2680 (cross entropy): per row, max folded from -inf,
+ * sum_exp = sum exp(l - max) sequentially, total -= (l[t] - max) - ln(sum_exp)
+ * over rows in order; loss = total / rows.  Only the first
+ * min(rows, ntargets) rows contribute (`targets.iter().enumerate().take(rows)`).
+ * Returns -1 (Rust would panic indexing the row) when a target is >= cols. */
+int oracle_cross_entropy(const float *logits, const float *targets, size_t ntargets,
+                         size_t rows, size_t cols, float *loss) {
+    float total = 0.0f;
+    const size_t used = ntargets < rows ? ntargets : rows;
+    for (size_t i = 0; i < used; ++i) {
+        const float *l = logits + i * cols;
+        float mx = -INFINITY;
+        for (size_t j = 0; j < cols; ++j) mx = fmaxf(mx, l[j]);
+        float s = 0.0f;
+        for (size_t j = 0; j < cols; ++j) s += expf(l[j] - mx);
+        const size_t t = target_index(targets[i]);
+        if (t >= cols) return -1;
+        total -= (l[t] - mx) - logf(s);
+    }
+    *loss = total / (float)rows;
+    return 0;
+}
+
+/* backend.rs:2686-2712 (cross entropy backward): per row, the same max and
+ * exps (stored, summed sequentially), prob = exps[j] / sum_exp and
+ * grad = (prob - [j == t]) * g / rows, evaluated left to right; rows past
+ * the targets keep a zero gradient. */
+int oracle_cross_entropy_backward(const float *logits, const float *targets, size_t ntargets,
+                                  size_t rows, size_t cols, float g, float *grad) {
+    const size_t used = ntargets < rows ? ntargets : rows;
+    memset(grad, 0, rows * cols * sizeof(float));
+    for (size_t i = 0; i < used; ++i) {
+        const float *l = logits + i * cols;
+        float *o = grad + i * cols;
+        float mx = -INFINITY;
+        for (size_t j = 0; j < cols; ++j) mx = fmaxf(mx, l[j]);
+        float s = 0.0f;
+        for (size_t j = 0; j < cols; ++j) {
+            o[j] = expf(l[j] - mx);
+            s += o[j];
+        }
+        const size_t t = target_index(targets[i]);
+        if (t >= cols) return -1;
+        for (size_t j = 0; j < cols; ++j) {
+            const float prob = o[j] / s;
+            const float tv = j == t ? 1.0f : 0.0f;
+            o[j] = (prob - tv) * g / (float)rows;
+        }
+    }
+    return 0;
+}
+
+/* backend.rs:2765-2772 (mse): sum of (p - t).powi(2) as a sequential fold,
+ * divided by n. */
+float oracle_mse(const float *p, const float *t, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) {
+        const float d = p[i] - t[i];
+        s += d * d;
+    }
+    return s / (float)n;
+}
+
+/* backend.rs:2780-2790 (mse backward): grad = 2.0 * (p - t) * g / n. */
+void oracle_mse_backward(const float *p, const float *t, size_t n, float g, float *grad) {
+    const float nf = (float)n;
+    for (size_t i = 0; i < n; ++i) grad[i] = 2.0f * (p[i] - t[i]) * g / nf;
+}

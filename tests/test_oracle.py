@@ -369,3 +369,179 @@ def test_paged_kv_append_is_the_cache_write():
     assert sorted(map(tuple, changed.tolist())) == want
     assert np.array_equal(oracle.paged_attention(q, None, None, kv2, bt, cl)[1:],
                           oracle.paged_attention(q, kn, vn, kv, bt, cl)[1:])
+
+
+# ---------------------------------------------------------------------------
+# backward passes and losses
+# ---------------------------------------------------------------------------
+
+def _torch():
+    return pytest.importorskip("torch")
+
+
+def test_relu_backward_exact():
+    g = rng(40)
+    x = g.standard_normal(5000).astype(np.float32)
+    x[:3] = [0.0, -0.0, np.nan]
+    go = g.standard_normal(5000).astype(np.float32)
+    got = oracle.relu_backward(x, go)
+    assert np.array_equal(got, np.where(x > 0, go, np.float32(0)))
+    # relu's output gives the same mask as its input
+    assert np.array_equal(oracle.relu_backward(oracle.relu(x), go), got)
+
+
+def test_gelu_backward_against_torch_autograd():
+    torch = _torch()
+    g = rng(41)
+    x = np.concatenate([g.standard_normal(20000).astype(np.float32) * 3,
+                        np.linspace(-8, 8, 1601, dtype=np.float32)])
+    go = g.standard_normal(x.size).astype(np.float32)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_()
+    torch.nn.functional.gelu(xt, approximate="tanh").backward(torch.from_numpy(go.astype(np.float64)))
+    # The reference's f32 formula loses absolute (not relative) accuracy where
+    # its terms cancel: near the derivative's zero (x ~ -0.75), and at |x| ~ 8
+    # where 1 + tanh cancels and 1 - t^2 (~6e-8 absolute error) is scaled by
+    # x*c*(1 + 0.134x^2) ~ 30.  So the error bound is relative to the result
+    # plus absolute in the derivative, times |grad_out|.
+    got, want = oracle.gelu_backward(x, go), xt.grad.numpy()
+    d_abs = np.where(np.abs(x) < 3, 2e-7, 3e-6)
+    assert np.all(np.abs(got - want) <= 3e-6 * np.abs(want) + d_abs * np.abs(go) + 1e-30)
+    # the derivative at 0 is exactly 1/2
+    assert oracle.gelu_backward(np.zeros(1, np.float32), np.ones(1, np.float32))[0] == 0.5
+
+
+def test_gelu_backward_against_central_difference():
+    # independent of torch: (gelu(x+h) - gelu(x-h)) / 2h in float64
+    x = np.linspace(-6, 6, 241).astype(np.float64)
+    c = np.sqrt(2 / np.pi)
+    gelu = lambda v: 0.5 * v * (1 + np.tanh(c * (v + 0.044715 * v ** 3)))
+    h = 1e-5
+    fd = (gelu(x + h) - gelu(x - h)) / (2 * h)
+    got = oracle.gelu_backward(x.astype(np.float32), np.ones_like(x, dtype=np.float32))
+    assert_close(got, fd, rtol=1e-5, atol=1e-6, what="gelu backward vs finite difference")
+
+
+def test_softmax_backward_against_torch_autograd():
+    torch = _torch()
+    g = rng(42)
+    x = g.normal(0, 2, (48, 257)).astype(np.float32)
+    dy = g.standard_normal((48, 257)).astype(np.float32)
+    xt = torch.from_numpy(x.astype(np.float64)).requires_grad_()
+    torch.softmax(xt, dim=-1).backward(torch.from_numpy(dy.astype(np.float64)))
+    y = oracle.softmax(x)
+    assert_close(oracle.softmax_backward(y, dy), xt.grad.numpy(), rtol=1e-4, atol=1e-7,
+                 what="softmax backward")
+
+
+def test_softmax_backward_closed_forms():
+    g = rng(43)
+    y = oracle.softmax(g.standard_normal((16, 100)).astype(np.float32))
+    # a constant upstream gradient has no effect on softmax: dx = 0
+    dx = oracle.softmax_backward(y, np.full_like(y, 3.0))
+    assert np.abs(dx).max() < 1e-6
+    # rows of dx always sum to 0 (sum_j y_j (g_j - s) = s - s)
+    dx = oracle.softmax_backward(y, g.standard_normal(y.shape).astype(np.float32))
+    assert np.abs(dx.sum(axis=1)).max() < 1e-5
+
+
+@pytest.mark.parametrize("m,k,n", [(5, 7, 3), (17, 33, 9), (64, 128, 10)])
+def test_matmul_backward_against_numpy_float64(m, k, n):
+    g = rng(m + k + n)
+    a = g.standard_normal((m, k)).astype(np.float32)
+    b = g.standard_normal((k, n)).astype(np.float32)
+    dc = g.standard_normal((m, n)).astype(np.float32)
+    da, db = oracle.matmul_backward(a, b, dc)
+    ad, bd, cd = (v.astype(np.float64) for v in (a, b, dc))
+    # non-square shapes: a transposed operand would not even have the shape
+    assert da.shape == (m, k) and db.shape == (k, n)
+    u = np.finfo(np.float32).eps
+    assert np.all(np.abs(da - cd @ bd.T) <= n * u * (np.abs(cd) @ np.abs(bd).T) + 1e-30)
+    assert np.all(np.abs(db - ad.T @ cd) <= m * u * (np.abs(ad).T @ np.abs(cd)) + 1e-30)
+
+
+def test_matmul_backward_against_torch_autograd():
+    torch = _torch()
+    g = rng(44)
+    a = g.standard_normal((2, 6, 11)).astype(np.float32)
+    b = g.standard_normal((11, 4)).astype(np.float32)
+    dc = g.standard_normal((2, 6, 4)).astype(np.float32)
+    at = torch.from_numpy(a.astype(np.float64)).requires_grad_()
+    bt = torch.from_numpy(b.astype(np.float64)).requires_grad_()
+    (at @ bt).backward(torch.from_numpy(dc.astype(np.float64)))
+    da, db = oracle.matmul_backward(a, b, dc)
+    assert da.shape == a.shape
+    assert_close(da, at.grad.numpy(), rtol=1e-5, atol=1e-5, what="dA")
+    assert_close(db, bt.grad.numpy(), rtol=1e-5, atol=1e-5, what="dB")
+
+
+@pytest.mark.parametrize("n,nb", [(4096, 64), (1000, 7), (999, 10), (12, 1), (50, 50)])
+def test_bias_grad_against_numpy(n, nb):
+    g = rng(n + nb)
+    go = g.integers(-8, 9, n).astype(np.float32)  # small integers: every sum is exact
+    want = np.zeros(nb, np.float64)
+    np.add.at(want, np.arange(n) % nb, go.astype(np.float64))
+    assert np.array_equal(oracle.bias_grad(go, nb), want.astype(np.float32))
+    assert np.array_equal(oracle.bias_grad(go, nb, negate=True), (-want).astype(np.float32))
+
+
+def test_bias_grad_is_an_in_order_fold():
+    # i % 1 == 0 for all i: (1e8 + 1) + (-1e8) folds to 0 in f32 order
+    assert oracle.bias_grad(np.array([1e8, 1.0, -1e8], np.float32), 1)[0] == 0.0
+
+
+def test_cross_entropy_against_torch_float64():
+    torch = _torch()
+    g = rng(45)
+    logits = g.normal(0, 3, (37, 23)).astype(np.float32)
+    t = g.integers(0, 23, 37).astype(np.float32)
+    want = torch.nn.functional.cross_entropy(torch.from_numpy(logits.astype(np.float64)),
+                                             torch.from_numpy(t.astype(np.int64))).item()
+    got = oracle.cross_entropy(logits, t)
+    assert got.shape == (1, 1)
+    assert abs(got[0, 0] - want) <= 1e-5 * abs(want)
+    # uniform logits: the loss is ln(cols) whatever the targets
+    assert abs(oracle.cross_entropy(np.zeros((5, 8), np.float32), t[:5] % 8)[0, 0]
+               - np.log(8)) < 1e-6
+
+
+def test_cross_entropy_rows_and_bad_targets():
+    g = rng(46)
+    logits = g.standard_normal((6, 5)).astype(np.float32)
+    t = np.array([0, 4, 2], np.float32)  # only 3 targets: 3 rows count, divided by 6
+    full = oracle.cross_entropy(logits[:3], t)[0, 0] * 3 / 6
+    assert abs(oracle.cross_entropy(logits, t)[0, 0] - full) < 1e-6
+    # negative and NaN targets saturate to class 0 like Rust's `as usize`
+    a = oracle.cross_entropy(logits[:2], np.array([-3.0, np.nan], np.float32))
+    b = oracle.cross_entropy(logits[:2], np.array([0.0, 0.0], np.float32))
+    assert a[0, 0] == b[0, 0]
+    with pytest.raises(IndexError):
+        oracle.cross_entropy(logits, np.array([5.0], np.float32))
+
+
+def test_cross_entropy_backward_against_torch_autograd():
+    torch = _torch()
+    g = rng(47)
+    logits = g.normal(0, 2, (19, 31)).astype(np.float32)
+    t = g.integers(0, 31, 19).astype(np.float32)
+    lt = torch.from_numpy(logits.astype(np.float64)).requires_grad_()
+    (torch.nn.functional.cross_entropy(lt, torch.from_numpy(t.astype(np.int64))) * 2.5).backward()
+    got = oracle.cross_entropy_backward(logits, t, 2.5)
+    assert_close(got, lt.grad.numpy(), rtol=1e-5, atol=1e-8, what="cross entropy backward")
+    assert np.abs(got.sum(axis=1)).max() < 1e-6  # softmax minus one-hot sums to 0
+    # rows past the targets get no gradient
+    part = oracle.cross_entropy_backward(logits, t[:4], 1.0)
+    assert np.all(part[4:] == 0) and np.abs(part[:4]).max() > 0
+
+
+def test_mse_against_numpy_and_torch():
+    torch = _torch()
+    g = rng(48)
+    p = g.standard_normal((33, 17)).astype(np.float32)
+    t = g.standard_normal((33, 17)).astype(np.float32)
+    want = np.mean((p.astype(np.float64) - t) ** 2)
+    assert abs(oracle.mse(p, t)[0, 0] - want) <= 1e-6 * want
+    pt = torch.from_numpy(p.astype(np.float64)).requires_grad_()
+    (torch.nn.functional.mse_loss(pt, torch.from_numpy(t.astype(np.float64))) * 0.5).backward()
+    assert_close(oracle.mse_backward(p, t, 0.5), pt.grad.numpy(), rtol=1e-6, atol=1e-12,
+                 what="mse backward")
+    assert oracle.mse(p, p)[0, 0] == 0.0
