@@ -265,6 +265,48 @@ def bench_backward(ca, oracle, args, out):
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
             f"{per.mean() * 1e3:.1f} us")
+    # AdamW on a 4096x4096 parameter: reads w, g, m, v, writes w, m, v
+    w = ca.empty((4096, 4096)).fill_normal(11)
+    gw = ca.empty((4096, 4096)).fill_normal(12, 0.0, 65536.0)
+    m0 = ca.tensor(np.zeros(N, np.float32))
+    v0 = ca.tensor(np.zeros(N, np.float32))
+    step = [0]
+
+    def adamw_once():
+        step[0] += 1
+        ca.adamw_step([w], [gw], [m0], [v0], step[0])
+    wall, per = timed(ca, adamw_once, args.steps, args.warmup)
+    nbytes = 28 * N
+    gbs = nbytes / (per.mean() * 1e-3) / 1e9
+    part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4), "bytes": nbytes,
+            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    if oracle is not None:
+        wh, gh = w.numpy(), gw.numpy()
+        zh = np.zeros(N, np.float32)
+        t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1))
+        part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                "cores": oracle.threads(), "kind": "port",
+                                "sample": "full 16.7M-element parameter, one step"}
+    out["adamw_4096x4096"] = part
+    log(f"adamw 4096x4096: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
+        f"{per.mean() * 1e3:.1f} us")
+    # AdamW over the MLP's four parameters in one launch (latency-bound)
+    from clove_amd import workloads
+    mlp = [ca.tensor(p) for p in workloads.mlp_inputs(0)[1:]]
+    mlp_g = [ca.tensor(np.full(p.numel, 100.0, np.float32)) for p in mlp]
+    mlp_m = [ca.tensor(np.zeros(p.numel, np.float32)) for p in mlp]
+    mlp_v = [ca.tensor(np.zeros(p.numel, np.float32)) for p in mlp]
+    step2 = [0]
+
+    def adamw_mlp():
+        step2[0] += 1
+        ca.adamw_step(mlp, mlp_g, mlp_m, mlp_v, step2[0])
+    wall, per = timed(ca, adamw_mlp, args.steps, args.warmup)
+    out["adamw_mlp_params"] = {"value": round(wall * 1e3, 2),
+                               "unit": "us/step (wall, 4 tensors, 1 launch)",
+                               "gpu_us": round(per.mean() * 1e3, 2)}
+    log(f"adamw MLP parameters: {wall * 1e3:.1f} us/step wall")
+    del w, gw, m0, v0
     # matmul backward at 4096^3: grad_a and grad_b, two GEMMs and two transposes
     dc = ca.empty((4096, 4096)).fill_normal(8)
     steps = max(5, args.steps // 10)

@@ -116,6 +116,9 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_cross_entropy_backward": (vp, [vp, vp, vp]),
         "clove_hip_mse": (vp, [vp, vp]),
         "clove_hip_mse_backward": (vp, [vp, vp, vp]),
+        "clove_hip_adamw_step": (C.c_int, [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
+                                           C.POINTER(vp), C.c_int, f, f, f, f, f, f, f,
+                                           C.c_uint]),
         "clove_hip_fused_chain": (C.c_int, [C.POINTER(ChainOp), C.c_int, C.POINTER(vp), C.c_int,
                                             C.POINTER(vp)]),
         "clove_hip_graph_create": (vp, []),
@@ -407,6 +410,17 @@ def mse(pred: Tensor, target: Tensor) -> Tensor:
 
 def mse_backward(pred: Tensor, target: Tensor, grad_loss: Tensor) -> Tensor:
     return _handle(lib().clove_hip_mse_backward(pred.handle, target.handle, grad_loss.handle))
+
+
+def adamw_step(weights, grads, m, v, step: int, lr: float = 1e-3, beta1: float = 0.9,
+               beta2: float = 0.999, eps: float = 1e-8, weight_decay: float = 0.01,
+               loss_scale: float = 65536.0, clip: float = 1.0) -> None:
+    """One fused AdamW update in place on lists of weights / moments
+    (defaults: AdamW::new, optim.rs:226-240, and the step's clip of 1.0)."""
+    n = len(weights)
+    arr = lambda ts: (C.c_void_p * max(n, 1))(*[t.handle.value for t in ts])
+    _check(lib().clove_hip_adamw_step(arr(weights), arr(grads), arr(m), arr(v), n, lr, beta1,
+                                      beta2, eps, weight_decay, loss_scale, clip, step))
 
 
 def paged_attention(q: Tensor, k: Optional[Tensor], v: Optional[Tensor], kv_cache: Tensor,

@@ -367,6 +367,25 @@ CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss) 
     });
 }
 
+int clove_hip_adamw_step(CTensor *weights, CTensor *grads, CTensor *m, CTensor *v, int count,
+                         float lr, float beta1, float beta2, float eps, float weight_decay,
+                         float loss_scale, float clip, unsigned int step) {
+    return guarded([&] {
+        if (count < 0) clove::fail(CLOVE_HIP_ERR_INVALID, "adamw: count < 0");
+        if (count > 0 && (!weights || !grads || !m || !v))
+            clove::fail(CLOVE_HIP_ERR_INVALID, "adamw: a tensor array is NULL");
+        std::vector<const Tensor *> w(count), g(count), mm(count), vv(count);
+        for (int i = 0; i < count; ++i) {
+            w[i] = &deref(weights[i], "weights[i]");
+            g[i] = &deref(grads[i], "grads[i]");
+            mm[i] = &deref(m[i], "m[i]");
+            vv[i] = &deref(v[i], "v[i]");
+        }
+        HipBackend::adamw_step(w, g, mm, vv,
+                               {lr, beta1, beta2, eps, weight_decay, loss_scale, clip, step});
+    });
+}
+
 CTensor clove_hip_paged_gather_indices(CTensor block_tables, CTensor context_lens, int block_size,
                                        int max_ctx) {
     return guarded_tensor([&] {

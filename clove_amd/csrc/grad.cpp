@@ -7,6 +7,7 @@
 // use the row kernels (rowwise.hip), the deterministic reductions
 // (reduce.hip) and the MFMA GEMM.  Nothing here synchronises.
 #include <algorithm>
+#include <cmath>
 #include <cstdint>
 
 #include "common.hpp"
@@ -197,6 +198,47 @@ TensorNode HipBackend::mse_backward(const TensorNode &p_, const TensorNode &t_,
     TensorNode out = new_tensor(p.shape, CLOVE_HIP_F32);
     k::mse_backward(p.f32(), t.f32(), p.numel, gl.f32(), out->f32(), ctx().stream);
     return out;
+}
+
+// optim.rs:375-395: every parameter tensor w with its gradient g and
+// moments m, v (all f32, same element count) updated in place.  The bias
+// corrections 1 - beta^t use the host's powf on (float)step, as the
+// reference computes them.
+void HipBackend::adamw_step(const std::vector<const Tensor *> &w,
+                            const std::vector<const Tensor *> &g,
+                            const std::vector<const Tensor *> &m,
+                            const std::vector<const Tensor *> &v, const AdamWParams &p) {
+    const size_t count = w.size();
+    CLOVE_REQUIRE(g.size() == count && m.size() == count && v.size() == count,
+                  CLOVE_HIP_ERR_INVALID, "adamw: w, g, m, v lists differ in length");
+    CLOVE_REQUIRE(p.step >= 1, CLOVE_HIP_ERR_INVALID,
+                  "adamw: step counts from 1 (AdamW::step increments before updating)");
+    std::vector<float *> pw(count), pm(count), pv(count);
+    std::vector<const float *> pg(count);
+    std::vector<uint64_t> n(count);
+    for (size_t i = 0; i < count; ++i) {
+        const Tensor *t[4] = {w[i], g[i], m[i], v[i]};
+        const char *what[4] = {"w", "g", "m", "v"};
+        for (int j = 0; j < 4; ++j) {
+            CLOVE_REQUIRE(t[j] != nullptr, CLOVE_HIP_ERR_INVALID,
+                          std::string("adamw: ") + what[j] + "[" + std::to_string(i) + "] is NULL");
+            CLOVE_REQUIRE(t[j]->dtype == CLOVE_HIP_F32, CLOVE_HIP_ERR_INVALID,
+                          std::string("adamw: ") + what[j] + " must be f32");
+            CLOVE_REQUIRE(t[j]->numel == w[i]->numel, CLOVE_HIP_ERR_SHAPE,
+                          "adamw: tensor " + std::to_string(i) + " has mismatched sizes");
+        }
+        pw[i] = w[i]->f32();
+        pg[i] = g[i]->f32();
+        pm[i] = m[i]->f32();
+        pv[i] = v[i]->f32();
+        n[i] = w[i]->numel;
+    }
+    const float t = (float)p.step;
+    const k::AdamWHyper h{p.lr, p.beta1, p.beta2, p.eps, p.weight_decay, p.loss_scale, p.clip,
+                          1.0f - powf(p.beta1, t), 1.0f - powf(p.beta2, t)};
+    Context &c = ctx();
+    k::adamw_step(pw.data(), pg.data(), pm.data(), pv.data(), n.data(), (int)count, h, c.num_cus,
+                  c.stream);
 }
 
 }  // namespace clove

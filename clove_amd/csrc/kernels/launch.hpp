@@ -48,6 +48,16 @@ void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hi
 // out[C][R] = in[R][C].
 void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s);
 
+// optim.hip -- the fused AdamW update, in place on w, m, v, for `count`
+// parameter tensors (kAdamWMaxTensors per launch).  bias1 / bias2 are
+// 1 - beta1^t and 1 - beta2^t.
+constexpr int kAdamWMaxTensors = 16;
+struct AdamWHyper {
+    float lr, beta1, beta2, eps, weight_decay, loss_scale, clip, bias1, bias2;
+};
+void adamw_step(float *const *w, const float *const *g, float *const *m, float *const *v,
+                const uint64_t *n, int count, const AdamWHyper &h, int num_cus, hipStream_t s);
+
 // gemm_f32.hip -- C[M,N] = A[M,K] . B[K,N], row-major f32, MFMA f32 accumulate.
 struct GemmPlan {
     int M, N, K;

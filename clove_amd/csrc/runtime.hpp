@@ -94,6 +94,15 @@ struct HipBackend {
     static TensorNode mse(const TensorNode &pred, const TensorNode &target);
     static TensorNode mse_backward(const TensorNode &pred, const TensorNode &target,
                                    const TensorNode &grad_loss);
+    // optim.rs:375-395: one AdamW step in place on every (w, g, m, v).
+    struct AdamWParams {
+        float lr, beta1, beta2, eps, weight_decay, loss_scale, clip;
+        uint32_t step;
+    };
+    static void adamw_step(const std::vector<const Tensor *> &w,
+                           const std::vector<const Tensor *> &g,
+                           const std::vector<const Tensor *> &m,
+                           const std::vector<const Tensor *> &v, const AdamWParams &p);
 
     // Launch-only forms writing into caller-provided outputs (used by the
     // planner, whose buffers are pre-assigned).

@@ -228,6 +228,20 @@ CTensor clove_hip_mse(CTensor pred, CTensor target);
 /* backend.rs:2780-2790: 2 * (pred - target) * grad_loss / numel(pred). */
 CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss);
 
+/* optim.rs:375-395 (AdamW::step, the Rayon branch; WGSL :305-345): one
+ * fused AdamW update, in place on weights[i], m[i] and v[i] for i < count,
+ * with grads[i] the gradients (f32, one element count per i).  Per element:
+ * decoupled decay w -= lr*wd*w, g' = clamp(g / loss_scale, -clip, clip),
+ * m = b1*m + (1-b1)*g', v = b2*v + (1-b2)*g'*g', and
+ * w -= lr * (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps).  step is
+ * AdamW's step_count after its increment (1 on the first step); m and v
+ * start as zeros.  The reference uses beta1 0.9, beta2 0.999, eps 1e-8,
+ * weight_decay 0.01, loss_scale 65536 and clip 1.0.  One launch covers up
+ * to 16 tensors.  Returns a status. */
+int clove_hip_adamw_step(CTensor *weights, CTensor *grads, CTensor *m, CTensor *v, int count,
+                         float lr, float beta1, float beta2, float eps, float weight_decay,
+                         float loss_scale, float clip, unsigned int step);
+
 /* ---------------------------------------------------------------------- */
 /* Fused elementwise chain: the counterpart of Step::Fused                 */
 /* (codegen lazy.rs:1694-1838, broadcast rule lazy.rs:1600-1608).         */

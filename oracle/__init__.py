@@ -69,6 +69,8 @@ def lib() -> C.CDLL:
         L.oracle_mse.argtypes = [fp, fp, sz]
         L.oracle_mse.restype = C.c_float
         L.oracle_mse_backward.argtypes = [fp, fp, sz, C.c_float, fp]
+        L.oracle_adamw.argtypes = [fp, fp, fp, fp, sz, C.c_float, C.c_float, C.c_float, C.c_float,
+                                   C.c_float, C.c_float, C.c_float, C.c_uint32]
         L.oracle_threads.restype = C.c_int
         L.oracle_set_threads.argtypes = [C.c_int]
         _lib = L
@@ -395,3 +397,15 @@ def mse_backward(p, t, g: float = 1.0):
     out = np.empty_like(p)
     lib().oracle_mse_backward(_f(p), _f(t), p.size, g, _f(out))
     return out
+
+
+def adamw(w, g, m, v, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
+          weight_decay=0.01, loss_scale=65536.0, clip=1.0):
+    """optim.rs:375-395: one AdamW step; returns updated copies (w, m, v).
+    Defaults are AdamW::new's (optim.rs:226-240) and the clip of 1.0 the
+    step uses."""
+    w, m, v = (np.array(a, dtype=np.float32, copy=True) for a in (w, m, v))
+    g = _f32(g)
+    lib().oracle_adamw(_f(w), _f(g), _f(m), _f(v), w.size, lr, beta1, beta2, eps, weight_decay,
+                       loss_scale, clip, step)
+    return w, m, v

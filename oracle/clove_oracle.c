@@ -654,3 +654,52 @@ void oracle_mse_backward(const float *p, const float *t, size_t n, float g, floa
     const float nf = (float)n;
     for (size_t i = 0; i < n; ++i) grad[i] = 2.0f * (p[i] - t[i]) * g / nf;
 }
+
+/* ------------------------------------------------------------------ */
+/* AdamW (optim.rs:375-395, the Rayon branch of AdamW::step)          */
+/* ------------------------------------------------------------------ */
+
+typedef struct {
+    float *w, *m, *v;
+    const float *g;
+    float lr, b1, b2, eps, wd, scale, clip, bc1, bc2;
+} adamw_ctx;
+
+/* Rust's f32::clamp: NaN passes through. */
+static float clamp_rs(float x, float lo, float hi) {
+    if (x < lo) x = lo;
+    if (x > hi) x = hi;
+    return x;
+}
+
+/* Per element, in Rust's evaluation order:
+ *   w -= lr * wd * w;  g' = clamp(g / scale, -clip, clip);
+ *   m = b1 * m + (1 - b1) * g';  v = b2 * v + (1 - b2) * g' * g';
+ *   w -= lr * (m / (1 - b1^t)) / (sqrt(v / (1 - b2^t)) + eps)
+ * with 1 - b^t (powf) computed once by the caller, as t is per step. */
+static void adamw_body(size_t b, size_t e, void *p) {
+    adamw_ctx *c = (adamw_ctx *)p;
+    for (size_t i = b; i < e; ++i) {
+        float w = c->w[i];
+        w -= c->lr * c->wd * w;
+        const float gu = c->g[i] / c->scale;
+        const float g = clamp_rs(gu, -c->clip, c->clip);
+        const float m = c->b1 * c->m[i] + (1.0f - c->b1) * g;
+        const float v = c->b2 * c->v[i] + (1.0f - c->b2) * g * g;
+        c->m[i] = m;
+        c->v[i] = v;
+        const float m_hat = m / c->bc1;
+        const float v_hat = v / c->bc2;
+        w -= c->lr * m_hat / (sqrtf(v_hat) + c->eps);
+        c->w[i] = w;
+    }
+}
+
+/* In place on w, m, v.  step is AdamW::step_count after its increment. */
+void oracle_adamw(float *w, const float *g, float *m, float *v, size_t n, float lr, float b1,
+                  float b2, float eps, float wd, float scale, float clip, uint32_t step) {
+    const float t = (float)step;
+    adamw_ctx c = {w, m, v, g, lr, b1, b2, eps, wd, scale, clip,
+                   1.0f - powf(b1, t), 1.0f - powf(b2, t)};
+    parallel_for(n, adamw_body, &c);
+}

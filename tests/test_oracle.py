@@ -545,3 +545,47 @@ def test_mse_against_numpy_and_torch():
     assert_close(oracle.mse_backward(p, t, 0.5), pt.grad.numpy(), rtol=1e-6, atol=1e-12,
                  what="mse backward")
     assert oracle.mse(p, p)[0, 0] == 0.0
+
+
+# ---------------------------------------------------------------------------
+# AdamW
+# ---------------------------------------------------------------------------
+
+def test_adamw_against_torch_float64():
+    """Five steps against torch.optim.AdamW in float64 (decoupled decay,
+    bias-corrected moments: the same mathematics), fed the unscaled,
+    clipped gradients the reference step computes."""
+    torch = _torch()
+    g = rng(60)
+    w0 = g.standard_normal(1000).astype(np.float32)
+    grads = [(g.standard_normal(1000) * 65536 * 0.7).astype(np.float32) for _ in range(5)]
+    p = torch.nn.Parameter(torch.from_numpy(w0.astype(np.float64)))
+    opt = torch.optim.AdamW([p], lr=1e-3, betas=(0.9, 0.999), eps=1e-8, weight_decay=0.01)
+    w, m, v = w0, np.zeros_like(w0), np.zeros_like(w0)
+    for t, gr in enumerate(grads, start=1):
+        w, m, v = oracle.adamw(w, gr, m, v, t)
+        p.grad = torch.from_numpy(np.clip(gr.astype(np.float64) / 65536, -1, 1))
+        opt.step()
+    assert_close(w, p.detach().numpy(), rtol=1e-6, atol=1e-7, what="adamw 5 steps")
+
+
+def test_adamw_first_step_closed_form():
+    # step 1: m_hat = g', v_hat = g'^2, so w' = w(1 - lr wd) - lr g' / (|g'| + eps)
+    w = np.array([1.0, -2.0, 0.5, 3.0], np.float32)
+    gr = np.array([0.25, -5.0, 0.0, 1e-3], np.float32) * 65536
+    w1, m1, v1 = oracle.adamw(w, gr, np.zeros(4, np.float32), np.zeros(4, np.float32), 1)
+    gc = np.clip(gr.astype(np.float64) / 65536, -1, 1)
+    want = w * (1 - 1e-3 * 0.01) - 1e-3 * gc / (np.abs(gc) + 1e-8)
+    assert_close(w1, want, rtol=1e-6, atol=1e-9, what="adamw step 1")
+    # (1 - beta) is formed in f32: 1 - 0.999f = 0.00099998713..., not 1e-3
+    c1 = 1.0 - np.float64(np.float32(0.9))
+    c2 = np.float64(np.float32(1.0) - np.float32(0.999))
+    assert_close(m1, c1 * gc, rtol=1e-6, atol=0, what="m")
+    assert_close(v1, c2 * gc * gc, rtol=1e-6, atol=0, what="v")
+
+
+def test_adamw_nan_gradient_propagates():
+    # Rust's f32::clamp keeps NaN (a min/max clamp would turn it into -1)
+    w, m, v = oracle.adamw(np.ones(2, np.float32), np.array([np.nan, 1.0], np.float32),
+                           np.zeros(2, np.float32), np.zeros(2, np.float32), 1)
+    assert np.isnan(w[0]) and np.isnan(m[0]) and np.isfinite(w[1])
