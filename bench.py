@@ -354,6 +354,45 @@ def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
             "kind": "port", "sample": sample}
 
 
+def bench_attention(ca, oracle, args, out):
+    """Attention prefill (the fused FlashAttention step): B=1, S=4096, H=32,
+    D=128, causal + RoPE; algorithmic FLOPs 4*D*H*S(S+1)/2 (QK^T and PV over
+    the visible keys); FP32 MFMA roofline.  Also RoPE alone (HBM)."""
+    B, S, H, D = 1, 4096, 32, 128
+    q = ca.empty((B, S, H * D)).fill_normal(31)
+    k = ca.empty((B, S, H * D)).fill_normal(32)
+    v = ca.empty((B, S, H * D)).fill_normal(33)
+    steps = max(5, args.steps // 10)
+    wall, per = timed(ca, lambda: ca.flash_attention(q, k, v, H), steps, max(2, args.warmup // 5))
+    flops = 4.0 * D * H * S * (S + 1) / 2
+    tf = flops / (per.mean() * 1e-3) / 1e12
+    part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
+            "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
+    if oracle is not None:
+        qh, kh, vh = q.numpy(), k.numpy(), v.numpy()
+        rows = [255 + 256 * i for i in range(16)]  # mean visible keys ~ S/2, as over all rows
+        t_rope = cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(0, 0)), reps=1)
+        t_rows = 0.0
+        for r in rows:
+            t_rows += cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(r, r + 1)), reps=1)
+        t_rows = max(t_rows - len(rows) * t_rope, 0.0)
+        t = t_rope + t_rows * S / len(rows)
+        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                "cores": oracle.threads(), "kind": "port",
+                                "sample": f"{len(rows)} of {S} query rows (all heads) plus the "
+                                          "full RoPE of q and k, row time scaled"}
+    out["flash_attention_4096"] = part
+    log(f"attention prefill S=4096 H=32 D=128 causal+rope: {tf:.1f} TFLOP/s "
+        f"({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), {per.mean():.3f} ms")
+    x = ca.empty((1, S, H * D)).fill_normal(34)
+    wall, per = timed(ca, lambda: ca.rope(x, D), args.steps, args.warmup)
+    nbytes = 2 * 4 * S * H * D
+    gbs = nbytes / (per.mean() * 1e-3) / 1e9
+    out["rope"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
+                   "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    log(f"rope [4096, 4096]: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), {per.mean() * 1e3:.1f} us")
+
+
 # ---------------------------------------------------------------------------
 
 def main():
@@ -362,7 +401,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--parts", default="all",
-                    help="comma list of copy,bcast,rows,matmul,paged,mlp,backward or 'all' / "
+                    help="comma list of copy,bcast,rows,matmul,paged,mlp,backward,attention or "
+                         "'all' / "
                          "'none' "
                          "(the config 2 chain always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
@@ -379,7 +419,7 @@ def main():
     import clove_amd as ca
 
     ca.init(0)
-    parts = {"copy", "bcast", "rows", "matmul", "paged", "mlp", "backward"} \
+    parts = {"copy", "bcast", "rows", "matmul", "paged", "mlp", "backward", "attention"} \
         if args.parts == "all" else \
         set() if args.parts == "none" else set(args.parts.split(","))
     oracle = None
@@ -450,6 +490,8 @@ def main():
         bench_mlp(ca, oracle, args, out)
     if "backward" in parts:
         bench_backward(ca, oracle, args, out)
+    if "attention" in parts:
+        bench_attention(ca, oracle, args, out)
     if out:
         result["parts"] = out
     ca.synchronize()

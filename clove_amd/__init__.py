@@ -116,6 +116,8 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_cross_entropy_backward": (vp, [vp, vp, vp]),
         "clove_hip_mse": (vp, [vp, vp]),
         "clove_hip_mse_backward": (vp, [vp, vp, vp]),
+        "clove_hip_flash_attention": (vp, [vp, vp, vp, C.c_int, C.c_int, C.c_int, C.c_int, f]),
+        "clove_hip_rope": (vp, [vp, sz, sz]),
         "clove_hip_adamw_step": (C.c_int, [C.POINTER(vp), C.POINTER(vp), C.POINTER(vp),
                                            C.POINTER(vp), C.c_int, f, f, f, f, f, f, f,
                                            C.c_uint]),
@@ -410,6 +412,21 @@ def mse(pred: Tensor, target: Tensor) -> Tensor:
 
 def mse_backward(pred: Tensor, target: Tensor, grad_loss: Tensor) -> Tensor:
     return _handle(lib().clove_hip_mse_backward(pred.handle, target.handle, grad_loss.handle))
+
+
+ATTN_CAUSAL, ATTN_ROPE = 1, 2
+
+
+def flash_attention(q: Tensor, k: Tensor, v: Tensor, num_heads: int, q_pos: int = 0,
+                    k_pos: int = 0, flags: int = ATTN_CAUSAL | ATTN_ROPE,
+                    scale: float = 0.0) -> Tensor:
+    """Attention prefill (the fused FlashAttention step); scale 0 = 1/sqrt(D)."""
+    return _handle(lib().clove_hip_flash_attention(q.handle, k.handle, v.handle, num_heads,
+                                                   q_pos, k_pos, flags, scale))
+
+
+def rope(x: Tensor, head_dim: int, pos_offset: int = 0) -> Tensor:
+    return _handle(lib().clove_hip_rope(x.handle, pos_offset, head_dim))
 
 
 def adamw_step(weights, grads, m, v, step: int, lr: float = 1e-3, beta1: float = 0.9,

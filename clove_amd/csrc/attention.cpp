@@ -1,0 +1,96 @@
+// attention.cpp -- host side of the attention prefill and of RoPE: shape
+// rules, the RoPE frequency table, and the launches (kernels/flash_attention.hip).
+#include <cmath>
+#include <cstdint>
+
+#include "common.hpp"
+#include "kernels/launch.hpp"
+#include "runtime.hpp"
+
+namespace clove {
+
+namespace {
+
+const Tensor &need(const TensorNode &t, const char *what) {
+    CLOVE_REQUIRE(t != nullptr, CLOVE_HIP_ERR_INVALID, std::string(what) + " is NULL");
+    CLOVE_REQUIRE(t->dtype == CLOVE_HIP_F32, CLOVE_HIP_ERR_INVALID,
+                  std::string(what) + " must be an f32 tensor");
+    return *t;
+}
+
+bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// 10000^(i / head_dim) for even i, with the host's f32 powf: the divisor of
+// backend.rs:2818 (`abs_pos as f32 / 10000.0f32.powf(i as f32 / head_dim as f32)`).
+k::AttnFreq rope_freq(int head_dim) {
+    k::AttnFreq f{};
+    for (int i = 0; i < head_dim && i / 2 < 128; i += 2)
+        f.div[i / 2] = powf(10000.0f, (float)i / (float)head_dim);
+    return f;
+}
+
+// [B, S, X] (3-d) or [S, X] (2-d, B = 1)
+void bsx(const Tensor &t, const char *what, size_t *B, size_t *S, size_t *X) {
+    CLOVE_REQUIRE(t.shape.size() == 2 || t.shape.size() == 3, CLOVE_HIP_ERR_SHAPE,
+                  std::string(what) + " must be [S, X] or [B, S, X], got " + shape_str(t.shape));
+    *B = t.shape.size() == 3 ? t.shape[0] : 1;
+    *S = t.shape[t.shape.size() - 2];
+    *X = t.shape.back();
+}
+
+}  // namespace
+
+// lazy.rs:1621-1690 (the FlashAttention pattern) and :4821-4909 (its
+// kernel): q [B, S, H*D], k and v [B, Sk, H*D].  flags: causal mask on
+// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k.
+// scale <= 0 means 1/sqrt(D), the reference's.
+TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,
+                                       const TensorNode &v_, int num_heads, int q_pos, int k_pos,
+                                       int flags, float scale) {
+    const Tensor &q = need(q_, "q");
+    const Tensor &k = need(k_, "k");
+    const Tensor &v = need(v_, "v");
+    size_t B, S, X, Bk, Sk, Xk, Bv, Sv, Xv;
+    bsx(q, "q", &B, &S, &X);
+    bsx(k, "k", &Bk, &Sk, &Xk);
+    bsx(v, "v", &Bv, &Sv, &Xv);
+    CLOVE_REQUIRE(Bk == B && Bv == B && Xk == X && Xv == X && Sv == Sk, CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: q " + shape_str(q.shape) + ", k " + shape_str(k.shape) +
+                      ", v " + shape_str(v.shape) + " do not agree");
+    CLOVE_REQUIRE(num_heads >= 1 && X % (size_t)num_heads == 0, CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: num_heads must divide the last dimension");
+    const int D = (int)(X / (size_t)num_heads);
+    CLOVE_REQUIRE(k::attention_supported(D), CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: head_dim " + std::to_string(D) + " (64 and 128 have kernels)");
+    CLOVE_REQUIRE((flags & ~(k::ATTN_FLAG_CAUSAL | k::ATTN_FLAG_ROPE)) == 0,
+                  CLOVE_HIP_ERR_INVALID, "flash_attention: unknown flag");
+    CLOVE_REQUIRE(q_pos >= 0 && k_pos >= 0, CLOVE_HIP_ERR_INVALID,
+                  "flash_attention: positions must be >= 0");
+    CLOVE_REQUIRE(B * S < (1ull << 31) && B * Sk < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: too many tokens");
+    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
+    CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data),
+                  CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned");
+    const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
+    k::attention_prefill(q.f32(), k.f32(), v.f32(), out->f32(), (int)B, (int)S, (int)Sk,
+                         num_heads, D, q_pos, k_pos, flags, sc, rope_freq(D), ctx().stream);
+    return out;
+}
+
+// backend.rs:2797-2826: x [B, S, hidden] or [S, hidden].
+TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head_dim) {
+    const Tensor &x = need(x_, "x");
+    size_t B, S, X;
+    bsx(x, "x", &B, &S, &X);
+    CLOVE_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, CLOVE_HIP_ERR_SHAPE,
+                  "rope: head_dim must be even and at most 256");
+    CLOVE_REQUIRE(X % 2 == 0, CLOVE_HIP_ERR_SHAPE, "rope: the hidden size must be even");
+    CLOVE_REQUIRE(pos_offset + S < (1ull << 31) && X < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "rope: positions or hidden size exceed 2^31");
+    TensorNode out = new_tensor(x.shape, CLOVE_HIP_F32);
+    k::rope(x.f32(), out->f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
+            rope_freq((int)head_dim), ctx().stream);
+    return out;
+}
+
+}  // namespace clove

@@ -367,6 +367,18 @@ CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss) 
     });
 }
 
+CTensor clove_hip_flash_attention(CTensor q, CTensor k, CTensor v, int num_heads, int q_pos,
+                                  int k_pos, int flags, float scale) {
+    return guarded_tensor([&] {
+        return HipBackend::flash_attention(as_node(q), as_node(k), as_node(v), num_heads, q_pos,
+                                           k_pos, flags, scale);
+    });
+}
+
+CTensor clove_hip_rope(CTensor x, size_t pos_offset, size_t head_dim) {
+    return guarded_tensor([&] { return HipBackend::rope(as_node(x), pos_offset, head_dim); });
+}
+
 int clove_hip_adamw_step(CTensor *weights, CTensor *grads, CTensor *m, CTensor *v, int count,
                          float lr, float beta1, float beta2, float eps, float weight_decay,
                          float loss_scale, float clip, unsigned int step) {

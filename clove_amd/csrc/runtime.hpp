@@ -94,6 +94,11 @@ struct HipBackend {
     static TensorNode mse(const TensorNode &pred, const TensorNode &target);
     static TensorNode mse_backward(const TensorNode &pred, const TensorNode &target,
                                    const TensorNode &grad_loss);
+    // Attention prefill and RoPE (attention.cpp).
+    static TensorNode flash_attention(const TensorNode &q, const TensorNode &k,
+                                      const TensorNode &v, int num_heads, int q_pos, int k_pos,
+                                      int flags, float scale);
+    static TensorNode rope(const TensorNode &x, size_t pos_offset, size_t head_dim);
     // optim.rs:375-395: one AdamW step in place on every (w, g, m, v).
     struct AdamWParams {
         float lr, beta1, beta2, eps, weight_decay, loss_scale, clip;

@@ -228,6 +228,26 @@ CTensor clove_hip_mse(CTensor pred, CTensor target);
 /* backend.rs:2780-2790: 2 * (pred - target) * grad_loss / numel(pred). */
 CTensor clove_hip_mse_backward(CTensor pred, CTensor target, CTensor grad_loss);
 
+/* Attention prefill: the computation of the lazy path's fused FlashAttention
+ * step (pattern MatMul(Softmax(MatMul(rope(q), rope(k)))), v), lazy.rs:
+ * 1621-1690; kernel lazy.rs:4821-4909), with an exact exp (the reference
+ * uses (1 + x/8)^8), batched and multi-head.  q f32 [B, S, H*D] or [S, H*D];
+ * k, v f32 [B, Sk, H*D] (same rank as q).  num_heads = H; D = 64 or 128.
+ * flags: CLOVE_ATTN_CAUSAL masks keys with t + k_pos > s + q_pos;
+ * CLOVE_ATTN_ROPE rotates q and k at positions s + q_pos and t + k_pos as
+ * clove_hip_rope does (the reference kernel always does both).  scale <= 0
+ * selects 1/sqrt(D).  Returns out with q's shape; a query with no visible
+ * key gets zeros. */
+#define CLOVE_ATTN_CAUSAL 1
+#define CLOVE_ATTN_ROPE 2
+CTensor clove_hip_flash_attention(CTensor q, CTensor k, CTensor v, int num_heads, int q_pos,
+                                  int k_pos, int flags, float scale);
+/* backend.rs:221, 2797-2826 (rope): x f32 [B, S, hidden] or [S, hidden];
+ * pair (i, i+1) of each head_dim-wide head at position s + pos_offset
+ * rotates by theta = pos / 10000^(i / head_dim); dims past the last whole
+ * head come out 0, as in the reference.  head_dim even, at most 256. */
+CTensor clove_hip_rope(CTensor x, size_t pos_offset, size_t head_dim);
+
 /* optim.rs:375-395 (AdamW::step, the Rayon branch; WGSL :305-345): one
  * fused AdamW update, in place on weights[i], m[i] and v[i] for i < count,
  * with grads[i] the gradients (f32, one element count per i).  Per element:

@@ -71,6 +71,9 @@ def lib() -> C.CDLL:
         L.oracle_mse_backward.argtypes = [fp, fp, sz, C.c_float, fp]
         L.oracle_adamw.argtypes = [fp, fp, fp, fp, sz, C.c_float, C.c_float, C.c_float, C.c_float,
                                    C.c_float, C.c_float, C.c_float, C.c_uint32]
+        L.oracle_rope.argtypes = [fp, sz, sz, sz, sz, sz, fp]
+        L.oracle_attention.argtypes = [fp, fp, fp, sz, sz, sz, sz, sz, C.c_long, C.c_long, C.c_int,
+                                       C.c_float, sz, sz, fp]
         L.oracle_threads.restype = C.c_int
         L.oracle_set_threads.argtypes = [C.c_int]
         _lib = L
@@ -409,3 +412,36 @@ def adamw(w, g, m, v, step: int, lr=1e-3, beta1=0.9, beta2=0.999, eps=1e-8,
     lib().oracle_adamw(_f(w), _f(g), _f(m), _f(v), w.size, lr, beta1, beta2, eps, weight_decay,
                        loss_scale, clip, step)
     return w, m, v
+
+
+def rope(x, head_dim: int, pos_offset: int = 0):
+    """backend.rs:2797-2826: x [B, S, hidden] or [S, hidden]."""
+    x = _f32(x)
+    b, s_ = (x.shape[0], x.shape[1]) if x.ndim == 3 else (1, x.shape[0])
+    out = np.empty_like(x)
+    lib().oracle_rope(_f(x), b, s_, x.shape[-1], head_dim, pos_offset, _f(out))
+    return out
+
+
+ATTN_CAUSAL, ATTN_ROPE = 1, 2
+
+
+def attention(q, k, v, num_heads: int, q_pos: int = 0, k_pos: int = 0,
+              flags: int = ATTN_CAUSAL | ATTN_ROPE, scale: Optional[float] = None,
+              rows: Optional[tuple] = None):
+    """The prefill attention lazy.rs:4821-4909 fuses, with an exact exp:
+    q [B, S, H*D] (or [S, H*D]), k, v [B, Sk, H*D]; see clove_oracle.c.
+    rows = (s_lo, s_hi) computes only those query rows (others are 0)."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    two_d = q.ndim == 2
+    if two_d:
+        q, k, v = q[None], k[None], v[None]
+    B, S, HD = q.shape
+    Sk = k.shape[1]
+    D = HD // num_heads
+    sc = float(1.0 / np.sqrt(np.float32(D))) if scale is None else scale
+    out = np.zeros_like(q)
+    s_lo, s_hi = rows or (0, S)
+    lib().oracle_attention(_f(q), _f(k), _f(v), B, S, Sk, num_heads, D, q_pos, k_pos, flags,
+                           sc, s_lo, s_hi, _f(out))
+    return out[0] if two_d else out

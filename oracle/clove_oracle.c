@@ -703,3 +703,130 @@ void oracle_adamw(float *w, const float *g, float *m, float *v, size_t n, float 
                    1.0f - powf(b1, t), 1.0f - powf(b2, t)};
     parallel_for(n, adamw_body, &c);
 }
+
+/* ------------------------------------------------------------------ */
+/* RoPE and attention prefill                                          */
+/* ------------------------------------------------------------------ */
+
+/* backend.rs:2797-2826 (rope): x is [batch, seq, hidden], heads of head_dim
+ * (even) dims, hidden / head_dim whole heads; pair (i, i+1) of each head at
+ * position pos rotates by
+ * theta = (pos + pos_offset) / 10000^(i / head_dim), all in f32:
+ *   x1' = x1 cos - x2 sin,  x2' = x1 sin + x2 cos. */
+typedef struct {
+    const float *x;
+    float *out;
+    size_t seq, hidden, head_dim, pos_offset;
+} rope_ctx;
+static void rope_rows(size_t r0, size_t r1, void *p) {
+    rope_ctx *c = (rope_ctx *)p;
+    for (size_t r = r0; r < r1; ++r) {  /* r = b * seq + pos */
+        const size_t pos = r % c->seq;
+        const float ap = (float)(pos + c->pos_offset);
+        const float *x = c->x + r * c->hidden;
+        float *o = c->out + r * c->hidden;
+        for (size_t h = 0; h + c->head_dim <= c->hidden; h += c->head_dim)
+            for (size_t i = 0; i < c->head_dim; i += 2) {
+                const float theta = ap / powf(10000.0f, (float)i / (float)c->head_dim);
+                const float x1 = x[h + i], x2 = x[h + i + 1];
+                o[h + i] = x1 * cosf(theta) - x2 * sinf(theta);
+                o[h + i + 1] = x1 * sinf(theta) + x2 * cosf(theta);
+            }
+    }
+}
+void oracle_rope(const float *x, size_t batch, size_t seq, size_t hidden, size_t head_dim,
+                 size_t pos_offset, float *out) {
+    /* result starts as zeros (backend.rs:2800): dims past the last whole head stay 0 */
+    memset(out, 0, batch * seq * hidden * sizeof(float));
+    rope_ctx c = {x, out, seq, hidden, head_dim, pos_offset};
+    parallel_for(batch * seq, rope_rows, &c);
+}
+
+/* Attention prefill, the computation lazy.rs:4821-4909 fuses (FlashAttention
+ * step, pattern lazy.rs:1621-1690) with an exact exp: q [B, S, H*D], k and v
+ * [B, Sk, H*D]; with ATTN_ROPE q and k are rotated first (positions s + q_pos
+ * and t + k_pos); score_t = (q . k_t, a sequential f32 dot) * scale, keys
+ * with t + k_pos > s + q_pos skipped under ATTN_CAUSAL; the softmax is
+ * backend.rs:2102-2125's (max fold, exp, sequential sum, divide) and
+ * out = sum_t p_t v_t summed in key order.  A row with no key gets 0. */
+enum { ATTN_CAUSAL = 1, ATTN_ROPE = 2 };
+typedef struct {
+    const float *q, *k, *v;
+    float *out;
+    size_t S, Sk, H, D, s_lo, s_hi;
+    long q_pos, k_pos;
+    int flags;
+    float scale;
+} attn_ctx;
+static void attn_rows(size_t r0, size_t r1, void *p) {
+    attn_ctx *c = (attn_ctx *)p;
+    const size_t H = c->H, D = c->D, HD = H * D, ns = c->s_hi - c->s_lo;
+    float *sc = (float *)malloc(c->Sk * sizeof(float));
+    for (size_t r = r0; r < r1; ++r) { /* r = (b * H + h) * ns + (s - s_lo) */
+        const size_t s = c->s_lo + r % ns, bh = r / ns, h = bh % H, b = bh / H;
+        const float *q = c->q + (b * c->S + s) * HD + h * D;
+        const float *kb = c->k + b * c->Sk * HD + h * D;
+        const float *vb = c->v + b * c->Sk * HD + h * D;
+        float *o = c->out + (b * c->S + s) * HD + h * D;
+        float mx = -INFINITY;
+        size_t nk = 0;
+        for (size_t t = 0; t < c->Sk; ++t) {
+            if ((c->flags & ATTN_CAUSAL) && (long)t + c->k_pos > (long)s + c->q_pos) {
+                sc[t] = -INFINITY;
+                continue;
+            }
+            float dot = 0.0f;
+            const float *kt = kb + t * HD;
+            for (size_t d = 0; d < D; ++d) dot += q[d] * kt[d];
+            sc[t] = dot * c->scale;
+            mx = fmaxf(mx, sc[t]);
+            ++nk;
+        }
+        if (nk == 0) {
+            for (size_t d = 0; d < D; ++d) o[d] = 0.0f;
+            continue;
+        }
+        float sum = 0.0f;
+        for (size_t t = 0; t < c->Sk; ++t) {
+            const float e = sc[t] == -INFINITY ? 0.0f : expf(sc[t] - mx);
+            sc[t] = e;
+            sum += e;
+        }
+        for (size_t t = 0; t < c->Sk; ++t) sc[t] /= sum;
+        for (size_t d = 0; d < D; ++d) {
+            float acc = 0.0f;
+            for (size_t t = 0; t < c->Sk; ++t)
+                if (sc[t] != 0.0f) acc += sc[t] * vb[t * HD + d];
+            o[d] = acc;
+        }
+    }
+    free(sc);
+}
+
+/* q and k rotated once (the same per-element f32 operations as rope above,
+ * at positions s + q_pos / t + k_pos), then plain attention for the query
+ * rows [s_lo, s_hi) of every (batch, head); other rows of out are left. */
+void oracle_attention(const float *q, const float *k, const float *v, size_t B, size_t S,
+                      size_t Sk, size_t H, size_t D, long q_pos, long k_pos, int flags,
+                      float scale, size_t s_lo, size_t s_hi, float *out) {
+    const size_t HD = H * D;
+    float *qr = NULL, *kr = NULL;
+    if (flags & ATTN_ROPE) {
+        qr = (float *)malloc(B * S * HD * sizeof(float));
+        kr = (float *)malloc(B * Sk * HD * sizeof(float));
+        /* HD is a whole number of heads, so every element is rotated */
+        rope_ctx cq = {q, qr, S, HD, D, (size_t)q_pos};
+        parallel_for(B * S, rope_rows, &cq);
+        rope_ctx ck = {k, kr, Sk, HD, D, (size_t)k_pos};
+        parallel_for(B * Sk, rope_rows, &ck);
+        q = qr;
+        k = kr;
+    }
+    if (s_hi > S) s_hi = S;
+    if (s_lo < s_hi) {
+        attn_ctx c = {q, k, v, out, S, Sk, H, D, s_lo, s_hi, q_pos, k_pos, flags, scale};
+        parallel_for(B * H * (s_hi - s_lo), attn_rows, &c);
+    }
+    free(qr);
+    free(kr);
+}

@@ -1,0 +1,76 @@
+"""GPU parity: attention prefill (the fused FlashAttention step) and RoPE
+vs the oracle.
+
+Tolerances: RoPE 1e-5 relative + 1e-6 absolute (the device sin/cos differ
+from glibc's by an ulp or so; theta itself is formed identically);
+attention 2e-3 relative + 1e-5 absolute (the attention bound).
+"""
+import numpy as np
+import pytest
+
+import oracle
+from conftest import assert_close, rng
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape,head_dim,pos", [((2, 50, 64), 16, 7), ((10, 128), 128, 0),
+                                                ((3, 5, 20), 8, 3), ((1, 4096, 128), 128, 0)])
+def test_rope(hip, shape, head_dim, pos):
+    x = rng(sum(shape)).standard_normal(shape).astype(np.float32)
+    got = hip.rope(hip.tensor(x), head_dim, pos).numpy()
+    assert_close(got, oracle.rope(x, head_dim, pos), 1e-5, 1e-6 * max(1, shape[-2] / 64),
+                 f"rope {shape}")
+
+
+CASES = [
+    # B, S, Sk, H, D, flags, q_pos, k_pos
+    (1, 37, 37, 1, 64, 3, 0, 0),
+    (2, 130, 130, 3, 128, 3, 0, 0),
+    (1, 256, 256, 4, 64, 1, 0, 0),
+    (2, 100, 100, 2, 128, 0, 0, 0),
+    (1, 65, 200, 2, 64, 1, 135, 0),   # chunked prefill: 65 new queries after 135 cached keys
+    (1, 65, 200, 2, 128, 3, 135, 0),
+    (1, 1, 1, 1, 128, 3, 0, 0),
+    (1, 33, 31, 2, 64, 2, 0, 0),
+    (3, 200, 77, 1, 128, 0, 0, 0),
+]
+
+
+@pytest.mark.parametrize("B,S,Sk,H,D,flags,q_pos,k_pos", CASES)
+def test_flash_attention(hip, B, S, Sk, H, D, flags, q_pos, k_pos):
+    g = rng(B * 1000 + S * 7 + Sk + H + D + flags)
+    q = g.standard_normal((B, S, H * D)).astype(np.float32)
+    k = g.standard_normal((B, Sk, H * D)).astype(np.float32)
+    v = g.standard_normal((B, Sk, H * D)).astype(np.float32)
+    got = hip.flash_attention(hip.tensor(q), hip.tensor(k), hip.tensor(v), H, q_pos, k_pos,
+                              flags).numpy()
+    want = oracle.attention(q, k, v, H, q_pos, k_pos, flags)
+    assert_close(got, want, 2e-3, 1e-5, f"attention {B}x{S}x{Sk}x{H}x{D} flags={flags}")
+
+
+def test_flash_attention_2d_and_scale_and_errors(hip):
+    g = rng(90)
+    q, k, v = (g.standard_normal((70, 128)).astype(np.float32) for _ in range(3))
+    tq, tk, tv = hip.tensor(q), hip.tensor(k), hip.tensor(v)
+    got = hip.flash_attention(tq, tk, tv, 2, flags=3, scale=0.3).numpy()
+    assert_close(got, oracle.attention(q, k, v, 2, flags=3, scale=0.3), 2e-3, 1e-5, "2-d")
+    # all keys in the future: zeros
+    z = hip.flash_attention(tq, tk, tv, 1, q_pos=0, k_pos=100, flags=1).numpy()
+    assert np.all(z == 0)
+    with pytest.raises(hip.CloveError):  # head_dim 32 has no kernel
+        hip.flash_attention(tq, tk, tv, 4)
+    with pytest.raises(hip.CloveError):
+        hip.flash_attention(tq, hip.tensor(k[:, :64]), tv, 1)
+
+
+def test_flash_attention_prefill_4096_sampled(hip):
+    """B=1, S=4096, H=32, D=128, causal + RoPE: sampled query rows of every
+    head against the oracle (which computes only those rows)."""
+    g = rng(91)
+    B, S, H, D = 1, 4096, 32, 128
+    q, k, v = (g.standard_normal((B, S, H * D)).astype(np.float32) for _ in range(3))
+    got = hip.flash_attention(hip.tensor(q), hip.tensor(k), hip.tensor(v), H).numpy()
+    for lo, hi in ((0, 2), (127, 130), (2047, 2049), (4094, 4096)):
+        want = oracle.attention(q, k, v, H, rows=(lo, hi))
+        assert_close(got[:, lo:hi], want[:, lo:hi], 2e-3, 1e-5, f"rows {lo}..{hi}")

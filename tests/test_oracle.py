@@ -589,3 +589,75 @@ def test_adamw_nan_gradient_propagates():
     w, m, v = oracle.adamw(np.ones(2, np.float32), np.array([np.nan, 1.0], np.float32),
                            np.zeros(2, np.float32), np.zeros(2, np.float32), 1)
     assert np.isnan(w[0]) and np.isnan(m[0]) and np.isfinite(w[1])
+
+
+# ---------------------------------------------------------------------------
+# RoPE and attention prefill
+# ---------------------------------------------------------------------------
+
+def rope64(x, head_dim, pos_offset=0):
+    """RoPE in float64 with theta rounded as the reference forms it (f32
+    position / f32 powf), so only the rotation itself is float64."""
+    x = np.asarray(x, np.float64)
+    out = x.copy()
+    S = x.shape[-2]
+    for i in range(0, head_dim, 2):
+        f = np.float32(10000.0) ** (np.float32(i) / np.float32(head_dim))
+        pos = (np.arange(S) + pos_offset).astype(np.float32)
+        th = (pos / np.float32(f)).astype(np.float64)[:, None]
+        for h0 in range(0, x.shape[-1], head_dim):
+            x1, x2 = x[..., h0 + i], x[..., h0 + i + 1]
+            c, s = np.cos(th[:, 0]), np.sin(th[:, 0])
+            out[..., h0 + i] = x1 * c - x2 * s
+            out[..., h0 + i + 1] = x1 * s + x2 * c
+    return out
+
+
+def test_rope_against_float64_and_invariants():
+    g = rng(80)
+    x = g.standard_normal((2, 50, 4 * 16)).astype(np.float32)
+    got = oracle.rope(x, 16, pos_offset=7)
+    assert_close(got, rope64(x, 16, 7), rtol=1e-5, atol=2e-6, what="rope")
+    assert np.array_equal(oracle.rope(x[:, :1], 16, 0), x[:, :1])  # position 0: identity
+    # a rotation keeps every pair's norm
+    n0 = x[..., 0::2].astype(np.float64) ** 2 + x[..., 1::2].astype(np.float64) ** 2
+    n1 = got[..., 0::2].astype(np.float64) ** 2 + got[..., 1::2].astype(np.float64) ** 2
+    assert_close(n1, n0, rtol=1e-5, atol=1e-6, what="pair norms")
+
+
+@pytest.mark.parametrize("causal,use_rope", [(True, True), (True, False), (False, True),
+                                             (False, False)])
+def test_attention_against_torch_sdpa(causal, use_rope):
+    torch = _torch()
+    g = rng(81 + 2 * causal + use_rope)
+    B, S, H, D = 2, 37, 3, 32
+    q, k, v = (g.standard_normal((B, S, H * D)).astype(np.float32) for _ in range(3))
+    flags = (oracle.ATTN_CAUSAL if causal else 0) | (oracle.ATTN_ROPE if use_rope else 0)
+    got = oracle.attention(q, k, v, H, flags=flags)
+    qq, kk = (rope64(x, D) if use_rope else x.astype(np.float64) for x in (q, k))
+    to = lambda x: torch.from_numpy(np.ascontiguousarray(
+        x.reshape(B, S, H, D).transpose(0, 2, 1, 3)))
+    want = torch.nn.functional.scaled_dot_product_attention(
+        to(qq), to(kk), to(v.astype(np.float64)), is_causal=causal,
+        scale=float(np.float32(1) / np.sqrt(np.float32(D)))).numpy()
+    want = want.transpose(0, 2, 1, 3).reshape(B, S, H * D)
+    assert_close(got, want, rtol=1e-4, atol=2e-5, what=f"attention causal={causal} rope={use_rope}")
+
+
+def test_attention_closed_forms():
+    g = rng(82)
+    S, D = 20, 16
+    q, k, v = (g.standard_normal((S, D)).astype(np.float32) for _ in range(3))
+    causal = oracle.attention(q, k, v, 1, flags=oracle.ATTN_CAUSAL | oracle.ATTN_ROPE)
+    assert np.array_equal(causal[0], v[0])  # the first query sees only key 0
+    vc = np.tile(g.standard_normal((1, D)).astype(np.float32), (S, 1))
+    assert_close(oracle.attention(q, k, vc, 1), vc, rtol=1e-6, atol=1e-6, what="constant V")
+    # q = 0 without rope: uniform weights, the mean of the visible values
+    z = oracle.attention(np.zeros_like(q), k, v, 1, flags=oracle.ATTN_CAUSAL)
+    want = np.cumsum(v.astype(np.float64), axis=0) / np.arange(1, S + 1)[:, None]
+    assert_close(z, want, rtol=1e-5, atol=1e-6, what="q = 0 mean")
+    # positions: causal masking compares t + k_pos with s + q_pos
+    shifted = oracle.attention(q, k, v, 1, q_pos=5, k_pos=5, flags=oracle.ATTN_CAUSAL)
+    assert np.array_equal(shifted, oracle.attention(q, k, v, 1, flags=oracle.ATTN_CAUSAL))
+    none = oracle.attention(q, k, v, 1, q_pos=0, k_pos=100, flags=oracle.ATTN_CAUSAL)
+    assert np.all(none == 0)  # every key lies in the future
