@@ -1,5 +1,6 @@
 // attention.cpp -- host side of the attention prefill and of RoPE: shape
 // rules, the RoPE frequency table, and the launches (kernels/flash_attention.hip).
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -40,10 +41,18 @@ void bsx(const Tensor &t, const char *what, size_t *B, size_t *S, size_t *X) {
 
 }  // namespace
 
+// The (cos, sin) table for positions [pos0, pos0 + npos) and head_dim.
+TensorNode rope_table_for(int pos0, int npos, int head_dim) {
+    TensorNode tab = new_tensor({(size_t)npos * (size_t)head_dim}, CLOVE_HIP_F32);
+    k::rope_table(tab->f32(), pos0, npos, head_dim, rope_freq(head_dim), ctx().stream);
+    return tab;
+}
+
 // lazy.rs:1621-1690 (the FlashAttention pattern) and :4821-4909 (its
 // kernel): q [B, S, H*D], k and v [B, Sk, H*D].  flags: causal mask on
-// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k.
-// scale <= 0 means 1/sqrt(D), the reference's.
+// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k,
+// applied in one pass each before the kernel.  scale <= 0 means 1/sqrt(D),
+// the reference's.
 TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,
                                        const TensorNode &v_, int num_heads, int q_pos, int k_pos,
                                        int flags, float scale) {
@@ -62,18 +71,36 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
     const int D = (int)(X / (size_t)num_heads);
     CLOVE_REQUIRE(k::attention_supported(D), CLOVE_HIP_ERR_SHAPE,
                   "flash_attention: head_dim " + std::to_string(D) + " (64 and 128 have kernels)");
-    CLOVE_REQUIRE((flags & ~(k::ATTN_FLAG_CAUSAL | k::ATTN_FLAG_ROPE)) == 0,
-                  CLOVE_HIP_ERR_INVALID, "flash_attention: unknown flag");
+    CLOVE_REQUIRE((flags & ~(CLOVE_ATTN_CAUSAL | CLOVE_ATTN_ROPE)) == 0, CLOVE_HIP_ERR_INVALID,
+                  "flash_attention: unknown flag");
     CLOVE_REQUIRE(q_pos >= 0 && k_pos >= 0, CLOVE_HIP_ERR_INVALID,
                   "flash_attention: positions must be >= 0");
-    CLOVE_REQUIRE(B * S < (1ull << 31) && B * Sk < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
-                  "flash_attention: too many tokens");
-    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
+    CLOVE_REQUIRE(B * S < (1ull << 31) && B * Sk < (1ull << 31) &&
+                      (size_t)q_pos + S < (1ull << 30) && (size_t)k_pos + Sk < (1ull << 30),
+                  CLOVE_HIP_ERR_SHAPE, "flash_attention: too many tokens");
+    // the kernel addresses one batch's K or V rows with 32-bit byte offsets
+    CLOVE_REQUIRE(Sk * X * 4 < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: one batch's k or v exceeds 2 GiB");
     CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data),
                   CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned");
+    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
-    k::attention_prefill(q.f32(), k.f32(), v.f32(), out->f32(), (int)B, (int)S, (int)Sk,
-                         num_heads, D, q_pos, k_pos, flags, sc, rope_freq(D), ctx().stream);
+    hipStream_t s = ctx().stream;
+    const float *qp = q.f32(), *kp = k.f32();
+    TensorNode qr, kr;
+    if (flags & CLOVE_ATTN_ROPE) {
+        const int p0 = std::min(q_pos, k_pos);
+        const int p1 = (int)std::max((size_t)q_pos + S, (size_t)k_pos + Sk);
+        TensorNode tab = rope_table_for(p0, p1 - p0, D);
+        qr = new_tensor(q.shape, CLOVE_HIP_F32);
+        kr = new_tensor(k.shape, CLOVE_HIP_F32);
+        k::rope_apply(qp, qr->f32(), B * S, (int)S, (int)X, D, q_pos, tab->f32(), p0, s);
+        k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), p0, s);
+        qp = qr->f32();
+        kp = kr->f32();
+    }
+    k::attention_prefill(qp, kp, v.f32(), out->f32(), (int)B, (int)S, (int)Sk, num_heads, D,
+                         q_pos, k_pos, (flags & CLOVE_ATTN_CAUSAL) != 0, sc, s);
     return out;
 }
 
@@ -85,11 +112,13 @@ TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head
     CLOVE_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, CLOVE_HIP_ERR_SHAPE,
                   "rope: head_dim must be even and at most 256");
     CLOVE_REQUIRE(X % 2 == 0, CLOVE_HIP_ERR_SHAPE, "rope: the hidden size must be even");
-    CLOVE_REQUIRE(pos_offset + S < (1ull << 31) && X < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
-                  "rope: positions or hidden size exceed 2^31");
+    CLOVE_REQUIRE(pos_offset + S < (1ull << 30) && X < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
+                  "rope: positions or hidden size exceed 2^30");
     TensorNode out = new_tensor(x.shape, CLOVE_HIP_F32);
-    k::rope(x.f32(), out->f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
-            rope_freq((int)head_dim), ctx().stream);
+    if (x.numel == 0) return out;
+    TensorNode tab = rope_table_for((int)pos_offset, (int)S, (int)head_dim);
+    k::rope_apply(x.f32(), out->f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
+                  tab->f32(), (int)pos_offset, ctx().stream);
     return out;
 }
 

@@ -10,7 +10,9 @@
 //
 // One workgroup = 4 waves = 128 queries of one (batch, head); each wave owns
 // 32 queries.  Key blocks of 32 are staged through LDS (double-buffered, one
-// barrier per block; K is rotated while it is staged).  The products run on
+// barrier per block).  RoPE is applied before the kernel, once per element
+// (a rotation inside it would be repeated by every query block that stages
+// the same keys).  The products run on
 // v_mfma_f32_32x32x2_f32 in TRANSPOSED form:
 //   S^T = K . Q^T   (A = K tile from LDS, B = the wave's Q^T in registers)
 //   O^T += V^T . P^T (A = V^T from LDS, B = P^T straight from S^T's registers)
@@ -55,28 +57,14 @@ struct AttnArgs {
     int nqb;        // query blocks per (batch, head)
     int total;      // B * H * nqb
     int per_xcd;    // ceil(total / 8)
-    AttnFreq freq;  // 10000^(2j/D), j < D/2, computed on the host with powf
 };
 
 __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
 }
 
-// Rotates the pairs (x, y) and (z, w) of f4 v holding dims d0..d0+3 at
-// position pos (backend.rs:2819-2823: x1 cos - x2 sin, x1 sin + x2 cos).
-__device__ __forceinline__ cl_f4 rope4(cl_f4 v, int d0, float pos, const AttnFreq &f) {
-#pragma clang fp contract(off)
-    const float t0 = pos / f.div[d0 / 2];
-    const float t1 = pos / f.div[d0 / 2 + 1];
-    float s0, c0, s1, c1;
-    sincosf(t0, &s0, &c0);
-    sincosf(t1, &s1, &c1);
-    return (cl_f4){v.x * c0 - v.y * s0, v.x * s0 + v.y * c0, v.z * c1 - v.w * s1,
-                   v.z * s1 + v.w * c1};
-}
-
-template <int D, bool CAUSAL, bool ROPE>
-__global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
+template <int D, bool CAUSAL>
+__global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     constexpr int kPK = D + 4;  // K tile pitch (16-byte reads by 32 rows: no conflicts)
     constexpr int kPV = D + 8;  // V tile pitch (rows r and r+4 land 32 banks apart)
     constexpr int kG = D / 8;   // K-groups of 8 dims
@@ -103,15 +91,15 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
     const bool q_ok = query < a.S;
     const float *qrow = a.q + ((size_t)b * a.S + (q_ok ? query : 0)) * HD + (size_t)h * D;
 
-    // this wave's Q^T fragment: dims 8g + 4hh .. +3 of its query, rotated
+    // this wave's Q^T fragment: dims 8g + 4hh .. +3 of its query, times the
+    // softmax scale.  Scaling here also makes the Q loads complete before the
+    // key loop: first used inside it, they would make the compiler wait for
+    // every outstanding load (the next tile's included) at each block.
     cl_f4 qf[kG];
 #pragma unroll
-    for (int g = 0; g < kG; ++g) {
-        cl_f4 v = q_ok ? *reinterpret_cast<const cl_f4 *>(qrow + 8 * g + 4 * hh)
-                       : (cl_f4){0.f, 0.f, 0.f, 0.f};
-        if (ROPE) v = rope4(v, 8 * g + 4 * hh, (float)(query + a.q_pos), a.freq);
-        qf[g] = v;
-    }
+    for (int g = 0; g < kG; ++g)
+        qf[g] = (q_ok ? *reinterpret_cast<const cl_f4 *>(qrow + 8 * g + 4 * hh)
+                      : (cl_f4){0.f, 0.f, 0.f, 0.f}) * a.scale;
 
     // keys [0, k_end) can be visible to some query of the workgroup
     int k_end = a.Sk;
@@ -124,8 +112,17 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
     if (CAUSAL) k_wave = min(k_wave, min(q0 + wave * 32 + 31, a.S - 1) + a.q_pos - a.k_pos + 1);
     const int nblk = k_end > 0 ? (k_end + kBK - 1) / kBK : 0;
 
-    const float *kbase = a.k + (size_t)b * a.Sk * HD + (size_t)h * D;
-    const float *vbase = a.v + (size_t)b * a.Sk * HD + (size_t)h * D;
+    // K and V tiles come through buffer loads over this batch's [Sk, H*D]
+    // rows: a key past Sk gets an offset past the end and reads as zeros.  A
+    // guarded ordinary load would become a branch that the compiler closes
+    // with a wait for all loads, which exposes the whole load latency of
+    // every block instead of overlapping it with the block before.
+    constexpr uint32_t kOutside = 0x80000000u;  // the host keeps Sk*H*D*4 < 2^31
+    const uint32_t kv_bytes = (uint32_t)a.Sk * (uint32_t)HD * 4u;
+    const __amdgpu_buffer_rsrc_t rsrc_k = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.k + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float *>(a.v + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
     cl_f4 rk[kVec], rv[kVec];
     auto load_tile = [&](int kb) {
 #pragma unroll
@@ -133,23 +130,18 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
             const int idx = threadIdx.x + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
             const int t = kb + key;
-            if (t < a.Sk) {
-                rk[i] = *reinterpret_cast<const cl_f4 *>(kbase + (size_t)t * HD + 4 * dq);
-                rv[i] = *reinterpret_cast<const cl_f4 *>(vbase + (size_t)t * HD + 4 * dq);
-            } else {
-                rk[i] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-                rv[i] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-            }
+            const uint32_t off =
+                t < a.Sk ? ((uint32_t)t * (uint32_t)HD + (uint32_t)(h * D + 4 * dq)) * 4u : kOutside;
+            rk[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off, 0, 0));
+            rv[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off, 0, 0));
         }
     };
-    auto store_tile = [&](int kb, int buf) {
+    auto store_tile = [&](int buf) {
 #pragma unroll
         for (int i = 0; i < kVec; ++i) {
             const int idx = threadIdx.x + 256 * i;
             const int key = idx / (D / 4), dq = idx % (D / 4);
-            cl_f4 kv = rk[i];
-            if (ROPE) kv = rope4(kv, 4 * dq, (float)(kb + key + a.k_pos), a.freq);
-            *reinterpret_cast<cl_f4 *>(&sK[buf][key * kPK + 4 * dq]) = kv;
+            *reinterpret_cast<cl_f4 *>(&sK[buf][key * kPK + 4 * dq]) = rk[i];
             *reinterpret_cast<cl_f4 *>(&sV[buf][key * kPV + 4 * dq]) = rv[i];
         }
     };
@@ -163,7 +155,7 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
 
     if (nblk > 0) {
         load_tile(0);
-        store_tile(0, 0);
+        store_tile(0);
     }
     __syncthreads();
     for (int blk = 0; blk < nblk; ++blk) {
@@ -175,54 +167,91 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
         if (kb < k_wave) {
             const float *K = sK[cur];
             const float *V = sV[cur];
-            // S^T = K . Q^T: s[i] is the score of key kb + 8(i/4) + 4hh + i%4
-            f16v s;
+            // S^T = K . Q^T: s[i] is the score of key kb + 8(i/4) + 4hh + i%4.
+            // Even and odd K-groups go to two accumulators, so consecutive
+            // MFMAs do not wait on each other's results.
+            f16v s, s2;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) s[e] = 0.f;
-#pragma unroll
-            for (int g = 0; g < kG; ++g) {
-                const cl_f4 kf = *reinterpret_cast<const cl_f4 *>(K + l32 * kPK + 8 * g + 4 * hh);
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[g][t], s, 0, 0, 0);
+            for (int e = 0; e < 16; ++e) {
+                s[e] = 0.f;
+                s2[e] = 0.f;
             }
-            float mloc = -INFINITY;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int t = kb + 8 * (i / 4) + 4 * hh + (i % 4);
-                bool ok = t < a.Sk && q_ok;
-                if (CAUSAL) ok = ok && t + a.k_pos <= query + a.q_pos;
-                s[i] = ok ? s[i] * a.scale : -INFINITY;
-                mloc = fmaxf(mloc, s[i]);
+            for (int g = 0; g < kG; g += 2) {
+                const cl_f4 kf = *reinterpret_cast<const cl_f4 *>(K + l32 * kPK + 8 * g + 4 * hh);
+                const cl_f4 kf2 =
+                    *reinterpret_cast<const cl_f4 *>(K + l32 * kPK + 8 * (g + 1) + 4 * hh);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[g][t], s, 0, 0, 0);
+                    s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf2[t], qf[g + 1][t], s2, 0, 0, 0);
+                }
+            }
+            s += s2;
+            // A block the whole wave sees (every key < Sk and, under the causal
+            // mask, at or before the wave's first query) skips the mask.
+            const int qw0 = q0 + wave * 32;
+            bool full = kb + kBK <= a.Sk && qw0 + 32 <= a.S;
+            if (CAUSAL) full = full && kb + kBK - 1 + a.k_pos <= qw0 + a.q_pos;
+            float mloc = -INFINITY;
+            if (full) {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int t = kb + 8 * (i / 4) + 4 * hh + (i % 4);
+                    bool ok = t < a.Sk && q_ok;
+                    if (CAUSAL) ok = ok && t + a.k_pos <= query + a.q_pos;
+                    s[i] = ok ? s[i] : -INFINITY;
+                    mloc = fmaxf(mloc, s[i]);
+                }
             }
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            const float m_new = fmaxf(m, mloc);
-            // m_new = -inf: no visible key yet for this query; keep zeros
-            const float alpha = m_new == -INFINITY ? 1.0f : fast_exp(m - m_new);
+            // Lazy rescale: the running max m moves only when some query of the
+            // wave sees a score more than kSlack above it.  Scores up to
+            // m + kSlack give weights up to e^kSlack, harmless in f32, and the
+            // numerator O and the denominator lsum share m, so the result is
+            // the same; the 16*kJ-multiply rescale of O is skipped on most
+            // blocks.  (m = -inf, no visible key yet, always updates.)
+            constexpr float kSlack = 8.0f;
+            const bool grow = __any(mloc > m + kSlack);
+            if (grow) {
+                const float m_new = fmaxf(m, mloc);
+                const float alpha = m_new == -INFINITY ? 1.0f : fast_exp(m - m_new);
+                lsum *= alpha;
+#pragma unroll
+                for (int j = 0; j < kJ; ++j)
+#pragma unroll
+                    for (int e = 0; e < 16; ++e) o[j][e] *= alpha;
+                m = m_new;
+            }
             float ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                s[i] = s[i] == -INFINITY ? 0.0f : fast_exp(s[i] - m_new);
+                s[i] = s[i] == -INFINITY ? 0.0f : fast_exp(s[i] - m);
                 ps += s[i];
             }
             ps += __shfl_xor(ps, 32, 64);
-            lsum = lsum * alpha + ps;
-            m = m_new;
-            // O^T = alpha * O^T + V^T . P^T (step i pairs key 8(i/4)+i%4 of
-            // half 0 with key 8(i/4)+4+i%4 of half 1, as S^T's layout holds them)
+            lsum += ps;
+            // O^T += V^T . P^T (step i pairs key 8(i/4)+i%4 of half 0 with key
+            // 8(i/4)+4+i%4 of half 1, as S^T's layout holds them)
+            // the kJ output blocks are independent accumulators: consecutive
+            // MFMAs alternate between them
 #pragma unroll
-            for (int j = 0; j < kJ; ++j) {
+            for (int i = 0; i < 16; ++i) {
+                const int key = 8 * (i / 4) + 4 * hh + (i % 4);
 #pragma unroll
-                for (int e = 0; e < 16; ++e) o[j][e] *= alpha;
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = 8 * (i / 4) + 4 * hh + (i % 4);
+                for (int j = 0; j < kJ; ++j) {
                     const float vv = V[key * kPV + 32 * j + l32];
                     o[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, s[i], o[j], 0, 0, 0);
                 }
+                // bound how far the V reads are hoisted (all 64 at once cost 64
+                // registers and an occupancy step)
+                if (i % 4 == 3) __builtin_amdgcn_sched_barrier(0);
             }
         }
-        if (more) store_tile(kb + kBK, cur ^ 1);
+        if (more) store_tile(cur ^ 1);
         __syncthreads();
     }
 
@@ -240,32 +269,68 @@ __global__ void __launch_bounds__(256) attention_kernel(AttnArgs a) {
         }
 }
 
-// backend.rs:2797-2826: one thread per pair.
-__global__ void __launch_bounds__(256) rope_kernel(const float *__restrict__ x,
-                                                   float *__restrict__ out, uint64_t rows,
-                                                   int seq, int hidden, int head_dim,
-                                                   int pos_offset, AttnFreq f) {
+// RoPE table: tab[p][j] = (cos, sin) of theta = (pos0 + p) / div[j], the
+// angle of pair j (dims 2j, 2j+1) at position pos0 + p (backend.rs:2818).
+// Built once per call, so each (position, pair) pays one sincosf however
+// many heads and rows use it.
+__global__ void __launch_bounds__(256) rope_table_kernel(float2 *__restrict__ tab, int pos0,
+                                                         int npos, int pairs, AttnFreq f) {
 #pragma clang fp contract(off)
-    const int pairs_row = hidden / 2;
-    const uint64_t total = rows * (uint64_t)pairs_row;
-    for (uint64_t p = (uint64_t)blockIdx.x * 256 + threadIdx.x; p < total;
-         p += (uint64_t)gridDim.x * 256) {
-        const uint64_t r = p / pairs_row;
-        const int c = 2 * (int)(p % pairs_row);
-        const int head = c / head_dim, i = c % head_dim;
-        const uint64_t idx = r * hidden + c;
-        if ((head + 1) * head_dim > hidden) {  // past the last whole head: 0, as the
-            out[idx] = 0.0f;                    // reference's zero-filled result leaves it
-            out[idx + 1] = 0.0f;
-            continue;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= npos * pairs) return;
+    const int p = i / pairs, j = i % pairs;
+    const float theta = (float)(pos0 + p) / f.div[j];
+    float s, c;
+    sincosf(theta, &s, &c);
+    tab[i] = make_float2(c, s);
+}
+
+// backend.rs:2797-2826: x1' = x1 cos - x2 sin, x2' = x1 sin + x2 cos per pair
+// of every whole head; dims past the last whole head are written as 0.
+// VEC: one 16-byte vector (two pairs) per thread.
+template <bool VEC>
+__global__ void __launch_bounds__(256) rope_apply_kernel(const float *__restrict__ x,
+                                                         float *__restrict__ out, uint64_t rows,
+                                                         int seq, int hidden, int head_dim,
+                                                         int pos_offset, const float2 *tab,
+                                                         int tab_pos0) {
+#pragma clang fp contract(off)
+    const int per_row = VEC ? hidden / 4 : hidden / 2;  // work items per row
+    const int pairs = head_dim / 2;
+    const int whole = (hidden / head_dim) * head_dim;
+    const uint64_t total = rows * (uint64_t)per_row;
+    for (uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x; w < total;
+         w += (uint64_t)gridDim.x * 256) {
+        const uint64_t r = w / per_row;
+        const int c0 = (int)(w % per_row) * (VEC ? 4 : 2);
+        const int p = (int)(r % seq) + pos_offset - tab_pos0;
+        const float2 *trow = tab + (size_t)p * pairs;
+        const uint64_t idx = r * hidden + c0;
+        if (VEC) {
+            const cl_f4 v = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(x + idx));
+            cl_f4 o = {0.f, 0.f, 0.f, 0.f};
+            if (c0 < whole) {
+                const float2 t0 = trow[(c0 % head_dim) / 2];
+                o.x = v.x * t0.x - v.y * t0.y;
+                o.y = v.x * t0.y + v.y * t0.x;
+            }
+            if (c0 + 2 < whole) {
+                const float2 t1 = trow[((c0 + 2) % head_dim) / 2];
+                o.z = v.z * t1.x - v.w * t1.y;
+                o.w = v.z * t1.y + v.w * t1.x;
+            }
+            __builtin_nontemporal_store(o, reinterpret_cast<cl_f4 *>(out + idx));
+        } else {
+            float o0 = 0.0f, o1 = 0.0f;
+            if (c0 < whole) {
+                const float2 t = trow[(c0 % head_dim) / 2];
+                const float x1 = x[idx], x2 = x[idx + 1];
+                o0 = x1 * t.x - x2 * t.y;
+                o1 = x1 * t.y + x2 * t.x;
+            }
+            out[idx] = o0;
+            out[idx + 1] = o1;
         }
-        const float pos = (float)((int)(r % seq) + pos_offset);
-        const float theta = pos / f.div[i / 2];
-        float s, co;
-        sincosf(theta, &s, &co);
-        const float x1 = x[idx], x2 = x[idx + 1];
-        out[idx] = x1 * co - x2 * s;
-        out[idx + 1] = x1 * s + x2 * co;
     }
 }
 
@@ -274,36 +339,46 @@ __global__ void __launch_bounds__(256) rope_kernel(const float *__restrict__ x,
 bool attention_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
 
 void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
-                       int Sk, int H, int D, int q_pos, int k_pos, int flags, float scale,
-                       const AttnFreq &freq, hipStream_t s) {
+                       int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
+                       hipStream_t s) {
     if (B <= 0 || S <= 0 || H <= 0) return;
-    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0, 0, 0, freq};
+    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0, 0, 0};
     a.nqb = (S + kBQ - 1) / kBQ;
     a.total = B * H * a.nqb;
     a.per_xcd = (a.total + 7) / 8;
     const unsigned grid = (unsigned)(a.per_xcd * 8);
-    const bool causal = flags & ATTN_FLAG_CAUSAL, rope = flags & ATTN_FLAG_ROPE;
-#define CLOVE_ATTN(DD)                                                                    \
-    if (causal && rope) attention_kernel<DD, true, true><<<grid, 256, 0, s>>>(a);         \
-    else if (causal) attention_kernel<DD, true, false><<<grid, 256, 0, s>>>(a);           \
-    else if (rope) attention_kernel<DD, false, true><<<grid, 256, 0, s>>>(a);             \
-    else attention_kernel<DD, false, false><<<grid, 256, 0, s>>>(a);
     if (D == 64) {
-        CLOVE_ATTN(64)
+        if (causal) attention_kernel<64, true><<<grid, 256, 0, s>>>(a);
+        else attention_kernel<64, false><<<grid, 256, 0, s>>>(a);
     } else {
-        CLOVE_ATTN(128)
+        if (causal) attention_kernel<128, true><<<grid, 256, 0, s>>>(a);
+        else attention_kernel<128, false><<<grid, 256, 0, s>>>(a);
     }
-#undef CLOVE_ATTN
 }
 
-void rope(const float *x, float *out, size_t rows, int seq, int hidden, int head_dim,
-          int pos_offset, const AttnFreq &freq, hipStream_t s) {
-    const uint64_t total = rows * (uint64_t)(hidden / 2);
+void rope_table(float *tab, int pos0, int npos, int head_dim, const AttnFreq &freq,
+                hipStream_t s) {
+    const int n = npos * (head_dim / 2);
+    if (n <= 0) return;
+    rope_table_kernel<<<(unsigned)((n + 255) / 256), 256, 0, s>>>(
+        reinterpret_cast<float2 *>(tab), pos0, npos, head_dim / 2, freq);
+}
+
+void rope_apply(const float *x, float *out, size_t rows, int seq, int hidden, int head_dim,
+                int pos_offset, const float *tab, int tab_pos0, hipStream_t s) {
+    const bool vec = hidden % 4 == 0 &&
+                     ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
+    const uint64_t total = rows * (uint64_t)(vec ? hidden / 4 : hidden / 2);
     if (!total) return;
     uint64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
-    rope_kernel<<<(unsigned)blocks, 256, 0, s>>>(x, out, rows, seq, hidden, head_dim, pos_offset,
-                                                 freq);
+    const float2 *t = reinterpret_cast<const float2 *>(tab);
+    if (vec)
+        rope_apply_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(x, out, rows, seq, hidden,
+                                                                 head_dim, pos_offset, t, tab_pos0);
+    else
+        rope_apply_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(x, out, rows, seq, hidden,
+                                                                  head_dim, pos_offset, t, tab_pos0);
 }
 
 }  // namespace k

@@ -50,20 +50,22 @@ void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s);
 
 // flash_attention.hip -- attention prefill and RoPE.  q [B, S, H*D], k, v
 // [B, Sk, H*D], out [B, S, H*D], all 16-byte aligned; D in {64, 128}.
+bool attention_supported(int head_dim);
+void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
+                       int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
+                       hipStream_t s);
 // freq.div[j] = 10000^(2j / D) (powf on the host, as backend.rs:2818 forms it).
-enum { ATTN_FLAG_CAUSAL = 1, ATTN_FLAG_ROPE = 2 };
 struct AttnFreq {
     float div[128];
 };
-bool attention_supported(int head_dim);
-void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
-                       int Sk, int H, int D, int q_pos, int k_pos, int flags, float scale,
-                       const AttnFreq &freq, hipStream_t s);
-// x [rows, hidden] with rows = batch * seq; pairs of each head_dim-wide head
-// rotated at position (row % seq) + pos_offset; dims past the last whole
-// head are written as 0 (hidden even).
-void rope(const float *x, float *out, size_t rows, int seq, int hidden, int head_dim,
-          int pos_offset, const AttnFreq &freq, hipStream_t s);
+// tab (npos * head_dim/2 float pairs): (cos, sin) of (pos0 + p) / div[j].
+void rope_table(float *tab, int pos0, int npos, int head_dim, const AttnFreq &freq,
+                hipStream_t s);
+// x [rows, hidden], rows = batch * seq: pairs of each whole head_dim-wide head
+// rotated at position (row % seq) + pos_offset (the table row
+// pos - tab_pos0); dims past the last whole head are written as 0.
+void rope_apply(const float *x, float *out, size_t rows, int seq, int hidden, int head_dim,
+                int pos_offset, const float *tab, int tab_pos0, hipStream_t s);
 
 // optim.hip -- the fused AdamW update, in place on w, m, v, for `count`
 // parameter tensors (kAdamWMaxTensors per launch).  bias1 / bias2 are
