@@ -43,7 +43,31 @@ struct GemmArgs {
     float *ws;        // split-K partial tiles [splits][tiles][BM*BN]
     int M, N, K, tiles_n, k_per_split, splits;
     GemmEpilogue epi;
+    int tiles;        // tiles of C (the grid's x dimension is padded to 8 * per_xcd)
+    int per_xcd;      // ceil(tiles / 8)
 };
+
+// Tile order.  Workgroups are dealt to the 8 XCDs round-robin (workgroup L
+// runs on XCD L % 8), each with its own L2.  Workgroup L takes position
+// V = (L % 8) * per_xcd + L / 8 of a grouped order, so each XCD walks one
+// contiguous range of it; the grouped order visits kGroupM tile rows column
+// by column.  At 4096^3 (32 x 16 tiles of 128 x 256) an XCD then owns an
+// 8 x 8 block of tiles whose concurrently running workgroups share A and B
+// slabs in its L2 (the plain row-major order gave each XCD 2 tile columns
+// and all 32 tile rows, so every A slab was fetched for just two tiles).
+constexpr int kGroupM = 8;
+__device__ __forceinline__ bool gemm_tile(const GemmArgs &g, int *tile) {
+    const int L = blockIdx.x;
+    const int V = (L % 8) * g.per_xcd + L / 8;
+    if (V >= g.tiles) return false;
+    const int tiles_m = g.tiles / g.tiles_n;
+    const int group_size = kGroupM * g.tiles_n;
+    const int first = (V / group_size) * kGroupM;
+    const int rows = min(kGroupM, tiles_m - first);
+    const int r = V % group_size;
+    *tile = (first + r % rows) * g.tiles_n + r / rows;
+    return true;
+}
 
 // Epilogue: C = act(acc + bias[(row*N + col) % bias_n]), each step rounded
 // in f32 exactly as Clove's separate Add (backend.rs:1489) and ReLU
@@ -154,7 +178,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     const float *__restrict__ B = g.B;
     const int M = g.M, N = g.N, K = g.K;
 
-    const int tile = blockIdx.x;
+    int tile;
+    if (!gemm_tile(g, &tile)) return;  // padding of the grid (before any barrier)
     const int split = blockIdx.y;
     const int m0 = (tile / g.tiles_n) * BM;
     const int n0 = (tile % g.tiles_n) * BN;
@@ -239,7 +264,7 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     }
 
     // Split-K: park this split's tile; gemm_splitk_reduce sums the splits.
-    float *part = g.ws + ((size_t)split * gridDim.x + tile) * (BM * BN);
+    float *part = g.ws + ((size_t)split * g.tiles + tile) * (BM * BN);
 #pragma unroll
     for (int i = 0; i < Cfg::kBlocksM; ++i)
 #pragma unroll
@@ -483,7 +508,7 @@ const int kCfgBK[CFG_COUNT] = {32, 16, 16, 32, 16, 16};
 
 template <int BM, int BN, int BK, int WM, int WN>
 void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
-    const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
+    const dim3 grid((unsigned)(g.per_xcd * 8), (unsigned)p.splits);
     // The fused epilogue (bias modulo, GELU) costs registers; kernels without
     // one (and split-K kernels, whose reduce applies it) are built without it.
     const bool epi = p.splits == 1 &&
@@ -620,7 +645,8 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
         q.vec = false;
         q.interior = false;
     }
-    GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits, epi};
+    GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits, epi,
+               p.tiles, (p.tiles + 7) / 8};
     if (p.skinny) {
         const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
         launch_skinny(p, g, grid, s);
