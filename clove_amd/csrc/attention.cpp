@@ -81,6 +81,9 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
     // the kernel addresses one batch's K or V rows with 32-bit byte offsets
     CLOVE_REQUIRE(Sk * X * 4 < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
                   "flash_attention: one batch's k or v exceeds 2 GiB");
+    // one 256-thread workgroup per (batch, head, block of 128 queries)
+    CLOVE_REQUIRE(B * (size_t)num_heads * ((S + 127) / 128) * 256 < (1ull << 32),
+                  CLOVE_HIP_ERR_SHAPE, "flash_attention: too many query blocks for one grid");
     CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data),
                   CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned");
     TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);

@@ -26,10 +26,14 @@
 // read of K / Q gives lane half h the four d values 8g + 4h .. 8g + 4h + 3,
 // consumed one per MFMA step.
 //
-// Work order: the grid is walked so that all query blocks of one head land
-// on the same XCD (blocks are dispatched round-robin over the 8 XCDs), so a
-// head's K and V are fetched into one L2, and the heaviest (last, under the
-// causal mask) query blocks start first.
+// Work order: workgroup L takes query block nqb-1 - L/(B*H) of (batch, head)
+// L % (B*H).  Under the causal mask a query block's cost grows with its
+// index, so this starts the heaviest blocks of every head first (a
+// longest-first list schedule: with 64 slots per XCD at S = 4096, H = 32 its
+// makespan is the ideal 33 block-units, where walking one head after another
+// took 49).  Workgroups are dealt to the 8 XCDs round-robin (L % 8), so when
+// B*H is a multiple of 8 each XCD serves a fixed set of heads and their K
+// and V stay in its L2.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -55,8 +59,6 @@ struct AttnArgs {
     int q_pos, k_pos;
     float scale;
     int nqb;        // query blocks per (batch, head)
-    int total;      // B * H * nqb
-    int per_xcd;    // ceil(total / 8)
 };
 
 __device__ __forceinline__ float fast_exp(float x) {
@@ -74,13 +76,11 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     __shared__ __attribute__((aligned(16))) float sK[2][kBK * kPK];
     __shared__ __attribute__((aligned(16))) float sV[2][kBK * kPV];
 
-    // XCD-aware order: block L runs on XCD L % 8; consecutive work items
-    // (the query blocks of one head) go to the same XCD.
+    // heaviest query blocks first, heads interleaved (see the file comment)
     const int L = blockIdx.x;
-    const int work = (L % 8) * a.per_xcd + L / 8;
-    if (work >= a.total) return;
-    const int qb = a.nqb - 1 - work % a.nqb;  // heaviest first
-    const int bh = work / a.nqb;
+    const int BH = a.B * a.H;
+    const int qb = a.nqb - 1 - L / BH;
+    const int bh = L % BH;
     const int h = bh % a.H, b = bh / a.H;
 
     const int HD = a.H * D;
@@ -342,11 +342,9 @@ void attention_prefill(const float *q, const float *k, const float *v, float *ou
                        int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
                        hipStream_t s) {
     if (B <= 0 || S <= 0 || H <= 0) return;
-    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0, 0, 0};
+    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0};
     a.nqb = (S + kBQ - 1) / kBQ;
-    a.total = B * H * a.nqb;
-    a.per_xcd = (a.total + 7) / 8;
-    const unsigned grid = (unsigned)(a.per_xcd * 8);
+    const unsigned grid = (unsigned)(B * H * a.nqb);
     if (D == 64) {
         if (causal) attention_kernel<64, true><<<grid, 256, 0, s>>>(a);
         else attention_kernel<64, false><<<grid, 256, 0, s>>>(a);
