@@ -52,6 +52,21 @@ def test_context_edges_with_new_token(hip, ctx):
     assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"ctx={ctx} cached")
 
 
+@pytest.mark.parametrize("part", [2048, 2056, 4096])
+def test_long_partitions(hip, monkeypatch, part):
+    # Block size 8: a 2048-token partition holds 256 whole blocks, the most
+    # the kernel's register-held table covers (the pipelined path); 2056 and
+    # 4096 tokens exceed it and take the block-by-block path.  Contexts end
+    # on, just before and just after partition boundaries.
+    monkeypatch.setenv("CLOVE_PAGED_PART", str(part))
+    H, D, bs, B = 2, 64, 8, 4
+    ctx = [4103, 2048, 2057, 4096]
+    mb = 4104 // bs + 1
+    q, kn, vn, kv, bt, cl = make(part, B, H, D, bs, B * mb + 3, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"part={part}")
+
+
 def test_empty_context_writes_zeros(hip):
     q, kn, vn, kv, bt, cl = make(5, 3, 2, 64, 16, 40, 8, [0, 3, 0])
     out = run(hip, q, None, None, kv, bt, cl)
