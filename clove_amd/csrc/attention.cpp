@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <map>
 
 #include "common.hpp"
 #include "kernels/launch.hpp"
@@ -39,12 +40,47 @@ void bsx(const Tensor &t, const char *what, size_t *B, size_t *S, size_t *X) {
     *X = t.shape.back();
 }
 
+// One (cos, sin) table per head_dim covering positions [0, npos), built on
+// the first call that needs it and regrown (powers of two) when a call needs
+// later positions.  Every entry is a function of (position, pair, head_dim)
+// alone, so a cached table holds the same bits as a table built for the call.
+// It is rebuilt when the library's stream changes, so it is only ever read by
+// work enqueued after it on the stream that wrote it.  API calls hold the
+// API mutex, which also guards this map.
+struct RopeCache {
+    TensorNode tab;
+    int npos = 0;
+    hipStream_t stream = nullptr;
+};
+std::map<int, RopeCache> g_rope_cache;
+constexpr int64_t kRopeCacheMaxFloats = 16 << 20;  // 64 MiB per head_dim at most
+
 }  // namespace
 
-// The (cos, sin) table for positions [pos0, pos0 + npos) and head_dim.
-TensorNode rope_table_for(int pos0, int npos, int head_dim) {
+void rope_cache_clear() { g_rope_cache.clear(); }
+
+// A (cos, sin) table whose rows cover positions [pos0, pos0 + npos) for
+// head_dim; *tab_pos0 receives the position of the table's first row.
+TensorNode rope_table_for(int pos0, int npos, int head_dim, int *tab_pos0) {
+    hipStream_t s = ctx().stream;
+    const int64_t end = (int64_t)pos0 + npos;
+    int64_t n = 1024;
+    while (n < end) n *= 2;
+    if (n * head_dim <= kRopeCacheMaxFloats) {
+        RopeCache &c = g_rope_cache[head_dim];
+        if (c.tab == nullptr || c.npos < end || c.stream != s) {
+            if (c.npos > n) n = c.npos;
+            c.tab = new_tensor({(size_t)n * (size_t)head_dim}, CLOVE_HIP_F32);
+            k::rope_table(c.tab->f32(), 0, (int)n, head_dim, rope_freq(head_dim), s);
+            c.npos = (int)n;
+            c.stream = s;
+        }
+        *tab_pos0 = 0;
+        return c.tab;
+    }
     TensorNode tab = new_tensor({(size_t)npos * (size_t)head_dim}, CLOVE_HIP_F32);
-    k::rope_table(tab->f32(), pos0, npos, head_dim, rope_freq(head_dim), ctx().stream);
+    k::rope_table(tab->f32(), pos0, npos, head_dim, rope_freq(head_dim), s);
+    *tab_pos0 = pos0;
     return tab;
 }
 
@@ -94,11 +130,12 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
     if (flags & CLOVE_ATTN_ROPE) {
         const int p0 = std::min(q_pos, k_pos);
         const int p1 = (int)std::max((size_t)q_pos + S, (size_t)k_pos + Sk);
-        TensorNode tab = rope_table_for(p0, p1 - p0, D);
+        int t0 = 0;
+        TensorNode tab = rope_table_for(p0, p1 - p0, D, &t0);
         qr = new_tensor(q.shape, CLOVE_HIP_F32);
         kr = new_tensor(k.shape, CLOVE_HIP_F32);
-        k::rope_apply(qp, qr->f32(), B * S, (int)S, (int)X, D, q_pos, tab->f32(), p0, s);
-        k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), p0, s);
+        k::rope_apply(qp, qr->f32(), B * S, (int)S, (int)X, D, q_pos, tab->f32(), t0, s);
+        k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), t0, s);
         qp = qr->f32();
         kp = kr->f32();
     }
@@ -119,9 +156,10 @@ TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head
                   "rope: positions or hidden size exceed 2^30");
     TensorNode out = new_tensor(x.shape, CLOVE_HIP_F32);
     if (x.numel == 0) return out;
-    TensorNode tab = rope_table_for((int)pos_offset, (int)S, (int)head_dim);
+    int t0 = 0;
+    TensorNode tab = rope_table_for((int)pos_offset, (int)S, (int)head_dim, &t0);
     k::rope_apply(x.f32(), out->f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
-                  tab->f32(), (int)pos_offset, ctx().stream);
+                  tab->f32(), t0, ctx().stream);
     return out;
 }
 

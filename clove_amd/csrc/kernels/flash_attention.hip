@@ -287,49 +287,76 @@ __global__ void __launch_bounds__(256) rope_table_kernel(float2 *__restrict__ ta
 
 // backend.rs:2797-2826: x1' = x1 cos - x2 sin, x2' = x1 sin + x2 cos per pair
 // of every whole head; dims past the last whole head are written as 0.
-// VEC: one 16-byte vector (two pairs) per thread.
-template <bool VEC>
-__global__ void __launch_bounds__(256) rope_apply_kernel(const float *__restrict__ x,
+// One workgroup per row (grid-stride over rows): the row's position and its
+// table row are computed once, each thread then rotates 16-byte vectors
+// (two pairs), issuing up to four vector loads before any arithmetic.
+__global__ void __launch_bounds__(256) rope_rows_kernel(const float *__restrict__ x,
+                                                        float *__restrict__ out, uint64_t rows,
+                                                        int seq, int hidden, int head_dim,
+                                                        int pos_offset, const float2 *tab,
+                                                        int tab_pos0) {
+#pragma clang fp contract(off)
+    const int nv = hidden / 4;
+    const int pairs = head_dim / 2;
+    const int whole = (hidden / head_dim) * head_dim;
+    for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const int p = (int)(r % (uint64_t)seq) + pos_offset - tab_pos0;
+        const float2 *trow = tab + (size_t)p * pairs;
+        const float *xr = x + r * (uint64_t)hidden;
+        float *orow = out + r * (uint64_t)hidden;
+        for (int v0 = threadIdx.x; v0 < nv; v0 += 4 * 256) {
+            cl_f4 xv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int v = v0 + 256 * u;
+                if (v < nv)
+                    xv[u] = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(xr) + v);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int v = v0 + 256 * u;
+                if (v >= nv) continue;
+                const int c0 = 4 * v;
+                cl_f4 o = {0.f, 0.f, 0.f, 0.f};
+                if (c0 < whole) {
+                    const float2 t0 = trow[(c0 % head_dim) / 2];
+                    o.x = xv[u].x * t0.x - xv[u].y * t0.y;
+                    o.y = xv[u].x * t0.y + xv[u].y * t0.x;
+                }
+                if (c0 + 2 < whole) {
+                    const float2 t1 = trow[((c0 + 2) % head_dim) / 2];
+                    o.z = xv[u].z * t1.x - xv[u].w * t1.y;
+                    o.w = xv[u].z * t1.y + xv[u].w * t1.x;
+                }
+                __builtin_nontemporal_store(o, reinterpret_cast<cl_f4 *>(orow) + v);
+            }
+        }
+    }
+}
+
+// Pair-at-a-time form for rows whose vectors are not 16-byte aligned.
+__global__ void __launch_bounds__(256) rope_pairs_kernel(const float *__restrict__ x,
                                                          float *__restrict__ out, uint64_t rows,
                                                          int seq, int hidden, int head_dim,
                                                          int pos_offset, const float2 *tab,
                                                          int tab_pos0) {
 #pragma clang fp contract(off)
-    const int per_row = VEC ? hidden / 4 : hidden / 2;  // work items per row
     const int pairs = head_dim / 2;
     const int whole = (hidden / head_dim) * head_dim;
-    const uint64_t total = rows * (uint64_t)per_row;
-    for (uint64_t w = (uint64_t)blockIdx.x * 256 + threadIdx.x; w < total;
-         w += (uint64_t)gridDim.x * 256) {
-        const uint64_t r = w / per_row;
-        const int c0 = (int)(w % per_row) * (VEC ? 4 : 2);
-        const int p = (int)(r % seq) + pos_offset - tab_pos0;
+    for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const int p = (int)(r % (uint64_t)seq) + pos_offset - tab_pos0;
         const float2 *trow = tab + (size_t)p * pairs;
-        const uint64_t idx = r * hidden + c0;
-        if (VEC) {
-            const cl_f4 v = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(x + idx));
-            cl_f4 o = {0.f, 0.f, 0.f, 0.f};
-            if (c0 < whole) {
-                const float2 t0 = trow[(c0 % head_dim) / 2];
-                o.x = v.x * t0.x - v.y * t0.y;
-                o.y = v.x * t0.y + v.y * t0.x;
-            }
-            if (c0 + 2 < whole) {
-                const float2 t1 = trow[((c0 + 2) % head_dim) / 2];
-                o.z = v.z * t1.x - v.w * t1.y;
-                o.w = v.z * t1.y + v.w * t1.x;
-            }
-            __builtin_nontemporal_store(o, reinterpret_cast<cl_f4 *>(out + idx));
-        } else {
+        const uint64_t base = r * (uint64_t)hidden;
+        for (int c0 = 2 * threadIdx.x; c0 < hidden; c0 += 2 * 256) {
             float o0 = 0.0f, o1 = 0.0f;
             if (c0 < whole) {
                 const float2 t = trow[(c0 % head_dim) / 2];
-                const float x1 = x[idx], x2 = x[idx + 1];
+                const float x1 = x[base + c0], x2 = x[base + c0 + 1];
                 o0 = x1 * t.x - x2 * t.y;
                 o1 = x1 * t.y + x2 * t.x;
             }
-            out[idx] = o0;
-            out[idx + 1] = o1;
+            out[base + c0] = o0;
+            out[base + c0 + 1] = o1;
         }
     }
 }
@@ -364,19 +391,18 @@ void rope_table(float *tab, int pos0, int npos, int head_dim, const AttnFreq &fr
 
 void rope_apply(const float *x, float *out, size_t rows, int seq, int hidden, int head_dim,
                 int pos_offset, const float *tab, int tab_pos0, hipStream_t s) {
+    if (rows == 0 || hidden <= 0) return;
     const bool vec = hidden % 4 == 0 &&
                      ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
-    const uint64_t total = rows * (uint64_t)(vec ? hidden / 4 : hidden / 2);
-    if (!total) return;
-    uint64_t blocks = (total + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
+    // one workgroup per row, at most 64 per CU's worth of rows in flight
+    const unsigned grid = (unsigned)(rows < 16384 ? rows : 16384);
     const float2 *t = reinterpret_cast<const float2 *>(tab);
     if (vec)
-        rope_apply_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(x, out, rows, seq, hidden,
-                                                                 head_dim, pos_offset, t, tab_pos0);
+        rope_rows_kernel<<<grid, 256, 0, s>>>(x, out, rows, seq, hidden, head_dim, pos_offset, t,
+                                              tab_pos0);
     else
-        rope_apply_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(x, out, rows, seq, hidden,
-                                                                  head_dim, pos_offset, t, tab_pos0);
+        rope_pairs_kernel<<<grid, 256, 0, s>>>(x, out, rows, seq, hidden, head_dim, pos_offset, t,
+                                               tab_pos0);
 }
 
 }  // namespace k

@@ -174,6 +174,7 @@ void shutdown() {
     if (!g_ready) return;
     (void)hipStreamSynchronize(g_ctx.stream);
     jit_shutdown();
+    rope_cache_clear();
     for (hipEvent_t e : g_events) (void)hipEventDestroy(e);
     g_events.clear();
     dev_empty_cache();

@@ -47,6 +47,8 @@ int ew_arity(int opcode);
 void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *> &inputs,
                const std::vector<Tensor *> &outs, size_t numel);
 void jit_shutdown();
+// Drops the cached RoPE tables (attention.cpp); part of shutdown.
+void rope_cache_clear();
 // Diagnostics for tests: number of chains compiled so far.
 int jit_compiled_count();
 

@@ -23,6 +23,21 @@ def test_rope(hip, shape, head_dim, pos):
                  f"rope {shape}")
 
 
+def test_rope_cached_table_regrows(hip):
+    # The (cos, sin) table is cached per head_dim and regrown when a call needs
+    # later positions: every call matches the oracle, and a call repeated after
+    # the table grew gives the same bits (entries depend on position only).
+    x = rng(92).standard_normal((3, 40, 256)).astype(np.float32)
+    first = {}
+    for pos in (0, 3000, 70000, 3000, 0):
+        got = hip.rope(hip.tensor(x), 64, pos).numpy()
+        assert_close(got, oracle.rope(x, 64, pos), 1e-5, 1e-6 * max(1, (pos + 40) / 64),
+                     f"rope pos={pos}")
+        if pos in first:
+            assert np.array_equal(got, first[pos]), f"rope pos={pos} changed after regrowth"
+        first[pos] = got
+
+
 CASES = [
     # B, S, Sk, H, D, flags, q_pos, k_pos
     (1, 37, 37, 1, 64, 3, 0, 0),
@@ -34,6 +49,10 @@ CASES = [
     (1, 1, 1, 1, 128, 3, 0, 0),
     (1, 33, 31, 2, 64, 2, 0, 0),
     (3, 200, 77, 1, 128, 0, 0, 0),
+    # long runs of whole key blocks (the pipelined path of the kernel)
+    (1, 300, 700, 2, 64, 0, 0, 0),
+    (2, 129, 513, 3, 128, 2, 0, 0),
+    (1, 512, 512, 2, 128, 1, 0, 0),
 ]
 
 
