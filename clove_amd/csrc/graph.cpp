@@ -375,6 +375,13 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
                 st.act = nodes[act].op == CLOVE_OP_RELU ? 1 : 2;
                 absorbed.insert(act);
                 tail = act;
+            } else if (act >= 0 && nodes[act].op == CLOVE_OP_SOFTMAX && nodes[act].deps[0] == tail) {
+                // a classifier head (MatMul [-> Add] -> Softmax, rows over the
+                // last dim): one step; the GEMM applies the softmax itself
+                // when a tile holds whole rows, else it runs after the GEMM
+                st.act = 3;
+                absorbed.insert(act);
+                tail = act;
             }
             st.out = {tail};
         }
@@ -417,7 +424,7 @@ std::string Model::describe() const {
         }
         case Step::MATMUL:
             s << "MatMul" << (st.in.size() > 2 ? "+Add" : "")
-              << (st.act == 1 ? "+ReLU" : st.act == 2 ? "+GELU" : "");
+              << (st.act == 1 ? "+ReLU" : st.act == 2 ? "+GELU" : st.act == 3 ? "+Softmax" : "");
             break;
         case Step::SOFTMAX: s << "Softmax"; break;
         case Step::LAYER_NORM: s << "LayerNorm"; break;
@@ -487,6 +494,26 @@ std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const 
         if (it != bound.end()) return it->second;
         return view_of(id);
     };
+    // Outputs are fresh tensors, never aliases of model buffers or of each
+    // other.  An output that a step computes is written by that step straight
+    // into its fresh tensor (later steps read it from there), so no copy is
+    // needed; an output that is a graph input, or a node listed twice, is
+    // copied at the end.
+    std::vector<TensorNode> result(outputs.size());
+    for (size_t i = 0; i < outputs.size(); ++i) {
+        const int o = outputs[i];
+        if (bound.count(o) || views.count(o)) continue;
+        TensorNode t = new_tensor(eval_shape(o), CLOVE_HIP_F32);
+        auto v = std::make_unique<Tensor>();
+        v->owned = false;
+        v->dtype = CLOVE_HIP_F32;
+        v->shape = t->shape;
+        v->numel = t->numel;
+        v->data = t->data;
+        v->bytes = t->bytes;
+        views[o] = std::move(v);
+        result[i] = t;
+    }
 
     for (const Step &st : steps) {
         switch (st.kind) {
@@ -521,15 +548,15 @@ std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const 
         }
     }
 
-    // Fresh tensors for the outputs (device-to-device copies on the stream).
-    std::vector<TensorNode> result;
-    for (int o : outputs) {
-        const Tensor *src = arg(o);
+    // The outputs not written in place: device-to-device copies on the stream.
+    for (size_t i = 0; i < outputs.size(); ++i) {
+        if (result[i]) continue;
+        const Tensor *src = arg(outputs[i]);
         TensorNode t = new_tensor(src->shape, src->dtype);
         if (src->numel)
             CLOVE_HIP_CHECK(hipMemcpyAsync(t->data, src->data, src->numel * 4,
                                            hipMemcpyDeviceToDevice, ctx().stream));
-        result.push_back(t);
+        result[i] = t;
     }
     return result;
 }

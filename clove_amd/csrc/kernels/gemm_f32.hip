@@ -25,6 +25,7 @@
 // uses bounds-checked loads that fill zeros.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdint>
 
 #include "launch.hpp"
@@ -499,6 +500,123 @@ __global__ void __launch_bounds__(64 * W) gemm_skinny_kernel(GemmArgs g) {
     for (int j = 0; j < kPer; ++j) part[idx + j] = sum[j];
 }
 
+// Small path: products whose 16 x 16 tiles cannot fill the chip (the MLP
+// layers, decode-sized projections).  Every 16 x 16 tile of C gets one
+// workgroup of W waves that splits K inside the workgroup: wave w covers
+// [w * kpw, (w + 1) * kpw) and builds a full 16 x 16 partial on
+// v_mfma_f32_16x16x4_f32 straight from global memory, and the W partials
+// meet in LDS and are summed in wave order.  No workspace and no second
+// kernel, where the tiled split-K form needs a reduce launch; the sum is
+// deterministic for a given shape.  16 x 16 tiles (rather than 32 x 32) give
+// four times the workgroups, so a 64 x 128 product still spreads over 32 CUs.
+//
+// Operand layout of v_mfma_f32_16x16x4_f32: lane l supplies A[l%16][l/16]
+// and B[l/16][l%16] and holds D[4(l/16) + i][l%16] in accumulator element i.
+// A K-group of 16 is split as k = 16g + 4q + t: lane group q = l/16 reads
+// its four k values of A in one 16-byte load and MFMA step t consumes
+// component t, with B read one float per lane and step.
+// Needs K % 4 == 0, a 16-byte aligned A and A, B under 2 GiB (the plan
+// checks them).
+template <int W, bool EPI>
+__global__ void __launch_bounds__(64 * W) gemm_small_kernel(GemmArgs g) {
+    constexpr int kPitch = 17;
+    __shared__ float red[W * 16 * kPitch];
+    const int M = g.M, N = g.N, K = g.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int m0 = (blockIdx.x / g.tiles_n) * 16, n0 = (blockIdx.x % g.tiles_n) * 16;
+    const int kpw = g.k_per_split;  // a multiple of 16
+    const int kb = wave * kpw;
+    const int ke = min(kb + kpw, K);
+    constexpr uint32_t kOutside = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rsrc_a = make_rsrc(g.A, (uint32_t)((size_t)M * K * 4));
+    const __amdgpu_buffer_rsrc_t rsrc_b = make_rsrc(g.B, (uint32_t)((size_t)K * N * 4));
+    const int row = m0 + l16, col = n0 + l16;
+    const int k_lane = kb + 4 * q;
+    const uint32_t aoff = row < M && k_lane < K ? ((uint32_t)row * (uint32_t)K + (uint32_t)k_lane) * 4u
+                                                : kOutside;
+    const uint32_t boff = col < N && k_lane < K ? ((uint32_t)k_lane * (uint32_t)N + (uint32_t)col) * 4u
+                                                : kOutside;
+    const uint32_t row_bytes = (uint32_t)N * 4u;
+    const int groups = ke > kb ? (ke - kb + 15) / 16 : 0;
+
+    f4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < groups; g0 += 4) {
+        f4 aq[4];
+        float bq[4][4];
+        // every load of the batch is issued before its first MFMA; group gi
+        // is in range for lane group q iff k = kb + 16gi + 4q (and the next
+        // three, K % 4 == 0) is below ke
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int gi = g0 + d;
+            const bool ok = gi < groups && kb + 16 * gi + 4 * q < ke;
+            aq[d] = __builtin_bit_cast(
+                f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_a, (int)(ok ? aoff : kOutside),
+                                                          64 * gi, 0));
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                bq[d][t] = __builtin_bit_cast(
+                    float, __builtin_amdgcn_raw_buffer_load_b32(
+                               rsrc_b, (int)(ok ? boff : kOutside),
+                               (int)((uint32_t)(16 * gi + t) * row_bytes), 0));
+        }
+        // keep the batch whole: left alone, the scheduler turns it into a
+        // rolling pipeline a few loads deep and pays the load latency once
+        // per group instead of once per batch
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                acc = __builtin_amdgcn_mfma_f32_16x16x4f32(aq[d][t], bq[d][t], acc, 0, 0, 0);
+    }
+
+    float *mine = red + wave * 16 * kPitch;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mine[(4 * q + i) * kPitch + l16] = acc[i];
+    __syncthreads();
+    if (EPI && g.epi.act == GEMM_ACT_SOFTMAX) {
+        // The tile holds whole rows (N <= 16: the host only asks for this
+        // epilogue then).  Bias first, rounded as the separate Add would,
+        // then each row's softmax as the row kernel computes it: max, 2^x
+        // exponentials of (x - max) * log2 e, their sum, one reciprocal.
+        __shared__ float rowv[16][17];
+        GemmEpilogue eb = g.epi;
+        eb.act = GEMM_ACT_NONE;
+        for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * W) {
+            const int r = idx / 16, c = idx % 16;
+            float sum = red[r * kPitch + c];
+#pragma unroll
+            for (int w = 1; w < W; ++w) sum += red[w * 16 * kPitch + r * kPitch + c];
+            rowv[r][c] = c < N ? epilogue(eb, sum, m0 + r, c, N) : -INFINITY;
+        }
+        __syncthreads();
+        const int r = threadIdx.x, gr = m0 + r;
+        if (r < 16 && gr < M) {
+            float mx = -INFINITY;
+            for (int c = 0; c < N; ++c) mx = fmaxf(mx, rowv[r][c]);
+            float se = 0.0f;
+            for (int c = 0; c < N; ++c) {
+                rowv[r][c] = __builtin_amdgcn_exp2f((rowv[r][c] - mx) * 1.44269504088896341f);
+                se += rowv[r][c];
+            }
+            const float inv = 1.0f / se;
+            for (int c = 0; c < N; ++c) g.C[(size_t)gr * N + c] = rowv[r][c] * inv;
+        }
+        return;
+    }
+    for (int idx = threadIdx.x; idx < 16 * 16; idx += 64 * W) {
+        const int r = idx / 16, c = idx % 16;
+        float sum = red[r * kPitch + c];
+#pragma unroll
+        for (int w = 1; w < W; ++w) sum += red[w * 16 * kPitch + r * kPitch + c];
+        const int gr = m0 + r, gc = n0 + c;
+        if (gr < M && gc < N)
+            g.C[(size_t)gr * N + gc] = EPI ? epilogue(g.epi, sum, gr, gc, N) : sum;
+    }
+}
+
 // Tile configurations: (BM, BN, BK, WM, WN).
 enum { CFG_32x128 = 0, CFG_64x64 = 1, CFG_128x128 = 2, CFG_128x128_K32 = 3, CFG_256x128 = 4,
        CFG_128x256 = 5, CFG_COUNT = 6 };
@@ -548,6 +666,22 @@ void launch_skinny(const GemmPlan &p, const GemmArgs &g, dim3 grid, hipStream_t 
     else if (p.mb == 1) launch_skinny_w<1, 1, 8>(p, g, grid, s);
     else if (p.nb == 2) launch_skinny_w<2, 2, 4>(p, g, grid, s);
     else launch_skinny_w<2, 1, 8>(p, g, grid, s);
+}
+
+template <int W>
+void launch_small_w(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
+    const bool epi = g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE;
+    if (epi) gemm_small_kernel<W, true><<<(unsigned)p.tiles, 64 * W, 0, s>>>(g);
+    else gemm_small_kernel<W, false><<<(unsigned)p.tiles, 64 * W, 0, s>>>(g);
+}
+
+void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
+    switch (p.waves) {
+    case 2: launch_small_w<2>(p, g, s); break;
+    case 4: launch_small_w<4>(p, g, s); break;
+    case 8: launch_small_w<8>(p, g, s); break;
+    default: launch_small_w<16>(p, g, s); break;
+    }
 }
 
 }  // namespace
@@ -604,6 +738,26 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         p.vec = true;
         return p;
     }
+    // Small path: when the 16 x 16 tiles do not fill the chip and K <= 1024,
+    // split K inside one workgroup per tile (no workspace, one launch)
+    // instead of across workgroups with a reduce launch.  2-16 waves, each
+    // covering at most 64 k (whole 16-groups, one load batch).  Longer K
+    // keeps the tiled split-K form, which spreads over every CU.
+    const int tiles16 = ((M + 15) / 16) * ((N + 15) / 16);
+    if (force_cfg < 0 && K >= 4 && K % 4 == 0 && K <= 1024 && a_aligned && tiles16 <= num_cus &&
+        b_bytes < (1ull << 31) && (uint64_t)M * K * 4 < (1ull << 31)) {
+        p.small = true;
+        int w = 2;
+        while (w < 16 && w * 64 < K) w *= 2;
+        p.waves = w;
+        p.k_per_split = ((K + w - 1) / w + 15) / 16 * 16;
+        p.tiles_n = (N + 15) / 16;
+        p.tiles = tiles16;
+        p.splits = 1;
+        p.ws_floats = 0;
+        p.vec = true;
+        return p;
+    }
     // 128x256 tiles measured ~3% faster than 128x128 at 4096^3; they are used
     // whenever they alone still give every CU a tile.
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
@@ -647,6 +801,10 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
     }
     GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits, epi,
                p.tiles, (p.tiles + 7) / 8};
+    if (p.small) {
+        launch_small(p, g, s);
+        return;
+    }
     if (p.skinny) {
         const dim3 grid((unsigned)p.tiles, (unsigned)p.splits);
         launch_skinny(p, g, grid, s);

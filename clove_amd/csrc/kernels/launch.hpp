@@ -93,11 +93,17 @@ struct GemmPlan {
     int nb;            // 32-column blocks per wave (1, 2 or 4)
     int waves;         // waves per workgroup (K split inside the workgroup)
     int k_per_wave;    // a whole number of pipeline chunks
+    // Small path: one workgroup of `waves` waves per 16 x 16 tile of C, K
+    // split inside the workgroup (k_per_split k per wave); no workspace.
+    bool small;
 };
 // Optional epilogue fused into the GEMM store: bias add with Clove's
 // broadcast rule (bias read at flat index % bias_n) and an activation.
 enum { GEMM_BIAS_NONE = 0, GEMM_BIAS_COL = 1, GEMM_BIAS_SCALAR = 2, GEMM_BIAS_MOD = 3 };
-enum { GEMM_ACT_NONE = 0, GEMM_ACT_RELU = 1, GEMM_ACT_GELU = 2 };
+// GEMM_ACT_SOFTMAX is a row softmax over the last dimension after the bias;
+// only the small path with N <= 16 (one tile column holds whole rows) applies
+// it in the kernel; matmul_into runs a separate row softmax otherwise.
+enum { GEMM_ACT_NONE = 0, GEMM_ACT_RELU = 1, GEMM_ACT_GELU = 2, GEMM_ACT_SOFTMAX = 3 };
 struct GemmEpilogue {
     const float *bias = nullptr;
     uint64_t bias_n = 0;

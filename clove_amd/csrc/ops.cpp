@@ -179,7 +179,7 @@ void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, cons
                         : bias->numel == n ? k::GEMM_BIAS_COL
                                            : k::GEMM_BIAS_MOD;
     }
-    CLOVE_REQUIRE(act >= k::GEMM_ACT_NONE && act <= k::GEMM_ACT_GELU, CLOVE_HIP_ERR_INVALID,
+    CLOVE_REQUIRE(act >= k::GEMM_ACT_NONE && act <= k::GEMM_ACT_SOFTMAX, CLOVE_HIP_ERR_INVALID,
                   "unknown GEMM epilogue activation");
     epi.act = act;
     int sk_nb, sk_splits;
@@ -189,6 +189,15 @@ void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, cons
                                        a_aligned, sk_force, sk_nb, sk_splits);
     TensorNode ws;
     if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
+    if (act == k::GEMM_ACT_SOFTMAX && !(p.small && p.tiles_n == 1)) {
+        // only the small path with one tile column holds whole rows: product
+        // and bias into a temporary, then the row softmax into `out`
+        epi.act = k::GEMM_ACT_NONE;
+        TensorNode tmp = new_tensor(out.shape, CLOVE_HIP_F32);
+        k::gemm_f32(p, a.f32(), b.f32(), tmp->f32(), ws ? ws->f32() : nullptr, epi, c.stream);
+        softmax_into(*tmp, out);
+        return;
+    }
     k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, epi, c.stream);
 }
 

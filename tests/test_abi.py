@@ -96,11 +96,12 @@ def mlp_graph():
 
 def test_plan_mlp():
     # Linear::forward (matmul then bias add, nn.rs:115-118) and the ReLU fold
-    # into the GEMM's epilogue; the softmax stays a row step.
+    # into the GEMM's epilogue; the classifier head's softmax folds into the
+    # second GEMM (a row softmax over the last dim).
     g, y = mlp_graph()
     m = g.compile([y])
-    assert steps(m) == ["MatMul+Add+ReLU", "MatMul+Add", "Softmax"]
-    assert m.num_steps == 3
+    assert steps(m) == ["MatMul+Add+ReLU", "MatMul+Add+Softmax"]
+    assert m.num_steps == 2
     # liveness: the hidden layer's buffer is reused once the second GEMM has
     # read it
     assert "vbufs=2" in m.describe()

@@ -111,7 +111,9 @@ def test_gemm_epilogue_fusion(hip, m, k, n, bias_n, act):
 
 
 @pytest.mark.parametrize("m,k,n,bias_n,act", [(64, 784, 128, 128, "relu"), (32, 4096, 512, 512, "gelu"),
-                                               (300, 256, 192, 7, None), (1024, 512, 1024, 1, "gelu")])
+                                               (300, 256, 192, 7, None), (1024, 512, 1024, 1, "gelu"),
+                                               (64, 128, 10, 10, None), (70, 100, 50, 1, "relu"),
+                                               (40, 1024, 96, 96, "gelu")])
 def test_gemm_epilogue_matches_eager_bits(hip, m, k, n, bias_n, act):
     """The fused epilogue rounds in the unfused order: the planned
     GEMM+bias(+act) equals eager matmul, then add, then the activation, bit
@@ -183,3 +185,32 @@ def test_skinny_epilogue(hip, monkeypatch, plan, m, k, n, bias_n, act):
     assert np.array_equal(fused.numpy(), eager.numpy())
     want = getattr(oracle, act)(oracle.add(oracle.matmul(a, w), b))
     assert_close(fused.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "skinny epilogue")
+
+
+@pytest.mark.parametrize("m,k,n,bias_n", [(64, 128, 10, 10), (37, 64, 16, 1), (5, 8, 3, 0),
+                                           (64, 128, 17, 17), (64, 2048, 10, 10),
+                                           (300, 96, 12, 12)])
+def test_gemm_softmax_head(hip, m, k, n, bias_n):
+    """MatMul [-> Add] -> Softmax planned as one step.  N <= 16 on the small
+    GEMM path applies the row softmax in the GEMM's epilogue; N = 17 and
+    K = 2048 (tiled path) run the product then the row kernel.  The softmax
+    tolerance, against the oracle's composition."""
+    gg = rng(3 * m + k + n)
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, max(bias_n, 1)).astype(np.float32)
+    g = hip.Graph()
+    x, wi = g.input(f"{m},{k}"), g.input(f"{k},{n}")
+    y = g.op("matmul", x, wi)
+    ins = [a, w]
+    if bias_n:
+        bi = g.input(f"{bias_n}")
+        y = g.op("add", y, bi)
+        ins.append(b)
+    model = g.compile([g.op("softmax", y)])
+    assert model.num_steps == 1, model.describe()
+    (out,) = model.execute([hip.tensor(v) for v in ins])
+    pre = oracle.matmul(a, w)
+    if bias_n:
+        pre = oracle.add(pre, b)
+    assert_close(out.numpy(), oracle.softmax(pre), 1e-4, 1e-7, f"softmax head {m}x{k}x{n}")

@@ -119,3 +119,44 @@ def test_skinny_misaligned_a_falls_back(hip):
     av = hip.wrap(buf.device_ptr + 4, (m, k))
     check(hip.matmul(av, hip.tensor(b)).numpy(), oracle.matmul(a, b), "misaligned A")
     del av
+
+
+# The small path (16 x 16 tiles that cannot fill the chip, K <= 1024,
+# K % 4 == 0, 16-byte aligned A): one workgroup per tile, K split over
+# 2/4/8/16 waves inside it, partials summed in LDS in wave order.
+@pytest.mark.parametrize("m,k,n", [(1, 4, 1), (5, 8, 3), (33, 64, 65), (64, 128, 10),
+                                   (31, 200, 100), (64, 256, 64), (100, 500, 33),
+                                   (64, 784, 128), (96, 1024, 96), (250, 300, 250)])
+def test_small_path_shapes(hip, m, k, n):
+    g = rng(31 * m + k + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, oracle.matmul(a, b), f"small {m}x{k}x{n}")
+    assert np.array_equal(got, hip.matmul(ta, tb).numpy()), "small path is deterministic"
+
+
+@pytest.mark.parametrize("cfg", ["0", "1", "2"])
+def test_tiled_split_k_still_covered(hip, monkeypatch, cfg):
+    """Shapes the small path now takes, forced through the tiled split-K
+    kernels (CLOVE_GEMM_CFG turns the small path off), keep the same product
+    within the matmul bound."""
+    monkeypatch.setenv("CLOVE_GEMM_CFG", cfg)
+    for m, k, n in ((64, 784, 128), (64, 128, 10), (33, 64, 65)):
+        g = rng(41 * m + k + n)
+        a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+        b = g.normal(0, 1, (k, n)).astype(np.float32)
+        check(hip.matmul(hip.tensor(a), hip.tensor(b)).numpy(), oracle.matmul(a, b),
+              f"tiled cfg {cfg} {m}x{k}x{n}")
+
+
+def test_small_path_misaligned_a_falls_back(hip):
+    g = rng(23)
+    m, k, n = 40, 128, 72
+    a = g.normal(0, 1, (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    buf = hip.tensor(np.concatenate([[0.0], a.ravel()]).astype(np.float32))
+    av = hip.wrap(buf.device_ptr + 4, (m, k))
+    check(hip.matmul(av, hip.tensor(b)).numpy(), oracle.matmul(a, b), "misaligned A")
+    del av
