@@ -25,6 +25,8 @@
 // uses bounds-checked loads that fill zeros.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include <cmath>
 #include <cstdint>
 
@@ -655,6 +657,17 @@ __global__ void __launch_bounds__(64 * W) gemm_small_kernel(GemmArgs g) {
     }
 }
 
+// K = 0: C = epilogue(0) (bias and activation still apply).  A kernel rather
+// than a memset, so a caller capturing the stream into a graph records no
+// memset node.
+__global__ void __launch_bounds__(256) gemm_k0_kernel(float *__restrict__ C, int M, int N,
+                                                      GemmEpilogue epi) {
+    const uint64_t total = (uint64_t)M * N;
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < total;
+         i += (uint64_t)gridDim.x * 256)
+        C[i] = epilogue(epi, 0.0f, (int)(i / N), (int)(i % N), N);
+}
+
 // Tile configurations: (BM, BN, BK, WM, WN).
 enum { CFG_32x128 = 0, CFG_64x64 = 1, CFG_128x128 = 2, CFG_128x128_K32 = 3, CFG_256x128 = 4,
        CFG_128x256 = 5, CFG_COUNT = 6 };
@@ -738,6 +751,11 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     p.M = M;
     p.N = N;
     p.K = K;
+    if (M <= 0 || N <= 0 || K <= 0) {  // nothing to tile: gemm_f32 returns at
+        p.tiles = p.tiles_n = 1;         // once or (K = 0) writes epilogue(0)
+        p.splits = 1;
+        return p;
+    }
     // Skinny path: M <= 64 (one or two 32-row blocks per wave), K % 4 == 0,
     // a 16-byte aligned A and B under 2 GiB.  NB column blocks per wave: 4
     // for M <= 32, 2 for M <= 64, fewer when N is not a multiple.  It is
@@ -847,7 +865,9 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
               const GemmEpilogue &epi, hipStream_t s) {
     if (p.M <= 0 || p.N <= 0) return;
     if (p.K <= 0) {
-        (void)hipMemsetAsync(C, 0, (size_t)p.M * p.N * sizeof(float), s);
+        const uint64_t total = (uint64_t)p.M * p.N;
+        const uint64_t blocks = std::min<uint64_t>((total + 255) / 256, 16384);
+        gemm_k0_kernel<<<(unsigned)blocks, 256, 0, s>>>(C, p.M, p.N, epi);
         return;
     }
     GemmPlan q = p;

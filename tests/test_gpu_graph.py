@@ -214,3 +214,26 @@ def test_gemm_softmax_head(hip, m, k, n, bias_n):
     if bias_n:
         pre = oracle.add(pre, b)
     assert_close(out.numpy(), oracle.softmax(pre), 1e-4, 1e-7, f"softmax head {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("act", [None, "relu", "gelu", "softmax"])
+def test_gemm_k0_epilogue(hip, act):
+    """K = 0: the product is zero and the fused epilogue still applies
+    (act(0 + bias), or the row softmax of the bias)."""
+    m, n = 5, 7
+    b = rng(93).normal(0, 1, n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},0"), g.input(f"0,{n}"), g.input(f"{n}")
+    y = g.op("add", g.op("matmul", x, wi), bi)
+    if act:
+        y = g.op(act, y)
+    model = g.compile([y])
+    assert model.num_steps == 1, model.describe()
+    (out,) = model.execute([hip.tensor(np.zeros((m, 0), np.float32)),
+                            hip.tensor(np.zeros((0, n), np.float32)), hip.tensor(b)])
+    pre = np.broadcast_to(b, (m, n)).astype(np.float32)
+    want = getattr(oracle, act)(pre) if act else pre
+    assert_close(out.numpy(), want, 1e-5, 1e-7, f"K=0 {act}")
+    z = hip.matmul(hip.tensor(np.zeros((m, 0), np.float32)),
+                   hip.tensor(np.zeros((0, n), np.float32))).numpy()
+    assert z.shape == (m, n) and np.all(z == 0)

@@ -160,3 +160,13 @@ def test_small_path_misaligned_a_falls_back(hip):
     av = hip.wrap(buf.device_ptr + 4, (m, k))
     check(hip.matmul(av, hip.tensor(b)).numpy(), oracle.matmul(a, b), "misaligned A")
     del av
+
+
+@pytest.mark.parametrize("m,k,n", [(0, 5, 7), (5, 7, 0), (0, 0, 0), (5, 0, 7), (1, 0, 1)])
+def test_matmul_empty_dimensions(hip, m, k, n):
+    """Any zero dimension: the plan has nothing to tile (it used to divide by
+    the tile count), and K = 0 gives a zero product."""
+    a = np.zeros((m, k), np.float32)
+    b = np.zeros((k, n), np.float32)
+    got = hip.matmul(hip.tensor(a), hip.tensor(b)).numpy()
+    assert got.shape == (m, n) and np.all(got == 0)
