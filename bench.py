@@ -19,8 +19,10 @@ Rank 0 prints ONE JSON line on stdout:
                broadcast chain, softmax and layer norm (GB/s), 4096^3 and
                skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
                MLP plan (us per forward) and the backward passes and losses
-               (GB/s; the matmul backward in TFLOP/s), each with its roofline
-               fraction and a sampled CPU baseline.
+               (GB/s; the matmul backward in TFLOP/s), attention prefill
+               (TFLOP/s) and RoPE (GB/s), each with its roofline fraction and
+               a sampled CPU baseline; an HBM-bound part's `traffic` is the
+               measured bytes per step of its kernels from the same summary.
 Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
 exits with a message.
 """
@@ -173,6 +175,13 @@ def bench_matmul(ca, oracle, args, out):
     out["matmul_skinny_32"] = {"value": round(tfs, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
                                "gbs": round(gbs, 1),
                                "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    if not args.no_cpu:
+        ah32 = a32.numpy()
+        t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=1)
+        out["matmul_skinny_32"]["cpu_baseline"] = {
+            "value": round(2.0 * 32 * K * 4096 / t / 1e12, 5), "unit": "TFLOP/s",
+            "cores": oracle.threads(), "kind": "port",
+            "sample": "full 32x4096x4096 product (B transpose included)"}
     log(f"matmul 32x4096x4096: {tfs:.2f} TFLOP/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
         f"{per.mean() * 1e3:.1f} us")
 
@@ -390,7 +399,49 @@ def bench_attention(ca, oracle, args, out):
     gbs = nbytes / (per.mean() * 1e-3) / 1e9
     out["rope"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
                    "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+    if oracle is not None:
+        rows = 512
+        xs = x.read(0, rows * H * D).reshape(1, rows, H * D)
+        t = cpu_time(lambda: oracle.rope(xs, D), reps=1) * S / rows
+        out["rope"]["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                       "cores": oracle.threads(), "kind": "port",
+                                       "sample": f"{rows} of {S} positions, scaled"}
     log(f"rope [4096, 4096]: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), {per.mean() * 1e3:.1f} us")
+
+
+# The kernels one step of each HBM-bound part launches, as the rocprof summary
+# names them: a part's roofline.traffic is the measured HBM bytes per step when
+# every one of its kernels was in the FETCH_SIZE / WRITE_SIZE passes.
+PART_KERNELS = {
+    "copy_reference": ["clove_chain_flatten_b0"],
+    "chain_broadcast": ["clove_chain_mul_add_gelu_mul_b0020"],
+    "softmax": ["softmax_wave_kernel<16>"],
+    "layer_norm": ["layer_norm_wave_kernel<16>"],
+    "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 4>", "gemm_splitk_reduce"],
+    "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
+    "softmax_backward": ["softmax_bw_wave_kernel<16>"],
+    "gelu_backward": ["clove_chain_gelugrad_b00"],
+    "broadcast_grad": ["bcast_grad_cols4_kernel", "bcast_grad_final_kernel"],
+    "cross_entropy": ["cross_entropy_wave_kernel<16, 0>", "ordered_sum_kernel"],
+    "cross_entropy_backward": ["cross_entropy_wave_kernel<16, 1>"],
+    "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
+    "mse_backward": ["mse_backward_kernel"],
+    "rope": ["rope_rows_kernel"],
+}
+
+
+def add_part_traffic(out, path):
+    if not path or not os.path.exists(path):
+        return
+    with open(path) as f:
+        kernels = json.load(f).get("kernels", {})
+    for name, part in out.items():
+        names = PART_KERNELS.get(name)
+        roof = part.get("roofline")
+        if not names or not roof or roof.get("bound") != "hbm":
+            continue
+        if all(k in kernels for k in names):
+            roof["traffic"] = int(sum(kernels[k]["bytes_per_launch"] for k in names))
 
 
 # ---------------------------------------------------------------------------
@@ -493,6 +544,7 @@ def main():
     if "attention" in parts:
         bench_attention(ca, oracle, args, out)
     if out:
+        add_part_traffic(out, args.traffic)
         result["parts"] = out
     ca.synchronize()
     print(json.dumps(result), flush=True)
