@@ -389,6 +389,47 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
     }
     flush();
 
+    // 3b. Horizontal MatMul groups (lazy.rs:2443-2493): a run of consecutive
+    // MatMul steps none of which reads another's output becomes one step that
+    // runs as one grouped launch.  (The reference only checks each candidate
+    // against the first member's output; every earlier member is checked
+    // here.)
+    {
+        std::vector<Step> grouped;
+        for (size_t i = 0; i < steps.size();) {
+            if (steps[i].kind != Step::MATMUL) {
+                grouped.push_back(steps[i++]);
+                continue;
+            }
+            std::vector<Step> run{steps[i]};
+            std::set<int> written(steps[i].out.begin(), steps[i].out.end());
+            size_t j = i + 1;
+            for (; j < steps.size() && steps[j].kind == Step::MATMUL; ++j) {
+                bool reads_member = false;
+                for (int d : steps[j].in) reads_member = reads_member || written.count(d) > 0;
+                if (reads_member) break;
+                run.push_back(steps[j]);
+                written.insert(steps[j].out.begin(), steps[j].out.end());
+            }
+            if (run.size() == 1) {
+                grouped.push_back(run[0]);
+            } else {
+                Step g;
+                g.kind = Step::MATMUL_GROUP;
+                std::set<int> seen;
+                for (const Step &m : run) {
+                    for (int d : m.in)
+                        if (seen.insert(d).second) g.in.push_back(d);
+                    g.out.insert(g.out.end(), m.out.begin(), m.out.end());
+                }
+                g.members = run;
+                grouped.push_back(g);
+            }
+            i = j;
+        }
+        steps.swap(grouped);
+    }
+
     // 4. liveness: a virtual buffer is released after the last step reading it.
     std::map<int, int> last_use;
     for (size_t i = 0; i < steps.size(); ++i)
@@ -411,6 +452,11 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
     }
 }
 
+static std::string matmul_name(const Step &st) {
+    return std::string("MatMul") + (st.in.size() > 2 ? "+Add" : "") +
+           (st.act == 1 ? "+ReLU" : st.act == 2 ? "+GELU" : st.act == 3 ? "+Softmax" : "");
+}
+
 std::string Model::describe() const {
     std::ostringstream s;
     for (const Step &st : steps) {
@@ -422,9 +468,12 @@ std::string Model::describe() const {
             s << "]";
             break;
         }
-        case Step::MATMUL:
-            s << "MatMul" << (st.in.size() > 2 ? "+Add" : "")
-              << (st.act == 1 ? "+ReLU" : st.act == 2 ? "+GELU" : st.act == 3 ? "+Softmax" : "");
+        case Step::MATMUL: s << matmul_name(st); break;
+        case Step::MATMUL_GROUP:
+            s << "MatMulGroup[";
+            for (size_t i = 0; i < st.members.size(); ++i)
+                s << (i ? "," : "") << matmul_name(st.members[i]);
+            s << "]";
             break;
         case Step::SOFTMAX: s << "Softmax"; break;
         case Step::LAYER_NORM: s << "LayerNorm"; break;
@@ -530,6 +579,14 @@ std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const 
             HipBackend::matmul_into(*arg(st.in[0]), *arg(st.in[1]), *view_of(st.out[0]),
                                     st.in.size() > 2 ? arg(st.in[2]) : nullptr, st.act);
             break;
+        case Step::MATMUL_GROUP: {
+            std::vector<HipBackend::GemmMember> ms;
+            for (const Step &m : st.members)
+                ms.push_back({arg(m.in[0]), arg(m.in[1]), view_of(m.out[0]),
+                              m.in.size() > 2 ? arg(m.in[2]) : nullptr, m.act});
+            HipBackend::matmul_group_into(ms);
+            break;
+        }
         case Step::SOFTMAX:
             HipBackend::softmax_into(*arg(st.in[0]), *view_of(st.out[0]));
             break;

@@ -47,14 +47,16 @@ struct Graph {
 
 // Step (lazy.rs:1158-1376), hot-path kinds only.
 struct Step {
-    enum Kind { FUSED, MATMUL, SOFTMAX, LAYER_NORM, PAGED };
+    enum Kind { FUSED, MATMUL, SOFTMAX, LAYER_NORM, PAGED, MATMUL_GROUP };
     Kind kind = FUSED;
-    std::vector<int> in;    // node ids read
+    std::vector<int> in;    // node ids read (each once)
     std::vector<int> out;   // node ids written
     std::vector<ChainOp> chain;  // FUSED only
     SymPtr numel;                // FUSED only: index space
-    int act = 0;                 // MATMUL only: fused activation (0 none, 1 ReLU, 2 GELU);
-                                 // a third input, when present, is the fused bias
+    int act = 0;                 // MATMUL only: fused activation (0 none, 1 ReLU, 2 GELU,
+                                 // 3 row softmax); a third input, when present, is the
+                                 // fused bias
+    std::vector<Step> members;   // MATMUL_GROUP only: independent MATMUL steps
 };
 
 // CompiledModel (lazy.rs:2545-2555).

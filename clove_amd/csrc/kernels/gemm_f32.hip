@@ -536,14 +536,12 @@ struct SmallBatch {
     float b[4][4];
 };
 
+// One tile V of product g (the body of the small-path kernels).
 template <int W, int MB, int NBATCH, bool EPI>
-__global__ void __launch_bounds__(64 * W) gemm_small_kernel(GemmArgs g) {
+__device__ __forceinline__ void small_tile(const GemmArgs &g, int V) {
     constexpr int kRows = 16 * MB;
     constexpr int kPitch = 17;
     __shared__ float red[W * kRows * kPitch];
-    const int L = blockIdx.x;
-    const int V = (L % 8) * g.per_xcd + L / 8;
-    if (V >= g.tiles) return;
     const int M = g.M, N = g.N, K = g.K;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int l16 = lane & 15, q = lane >> 4;
@@ -655,6 +653,33 @@ __global__ void __launch_bounds__(64 * W) gemm_small_kernel(GemmArgs g) {
         if (gr < M && gc < N)
             g.C[(size_t)gr * N + gc] = EPI ? epilogue(g.epi, sum, gr, gc, N) : sum;
     }
+}
+
+template <int W, int MB, int NBATCH, bool EPI>
+__global__ void __launch_bounds__(64 * W) gemm_small_kernel(GemmArgs g) {
+    const int L = blockIdx.x;
+    const int V = (L % 8) * g.per_xcd + L / 8;
+    if (V >= g.tiles) return;
+    small_tile<W, MB, NBATCH, EPI>(g, V);
+}
+
+// Grouped form (the planner's horizontal MatMul groups): one launch covers
+// the tiles of up to kGemmGroupMax independent small-path products; workgroup
+// L runs tile L - starts[p] of the product p whose range holds it.  The
+// waves per workgroup are the largest any member needs (members with a
+// shorter K leave the extra waves' K ranges empty), one row block per tile.
+struct GroupedArgs {
+    GemmArgs prob[kGemmGroupMax];
+    int starts[kGemmGroupMax + 1];
+    int count;
+};
+
+template <int W>
+__global__ void __launch_bounds__(64 * W) gemm_small_grouped_kernel(GroupedArgs ga) {
+    const int L = blockIdx.x;
+    int p = 0;
+    while (p + 1 < ga.count && L >= ga.starts[p + 1]) ++p;
+    small_tile<W, 1, 1, true>(ga.prob[p], L - ga.starts[p]);
 }
 
 // K = 0: C = epilogue(0) (bias and activation still apply).  A kernel rather
@@ -859,6 +884,33 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     p.interior = p.vec && (M % BM == 0) && (N % BN == 0) && (K % BK == 0) &&
                  (p.k_per_split % BK == 0);
     return p;
+}
+
+void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float *const *B,
+                      float *const *C, const GemmEpilogue *epi, int count, hipStream_t s) {
+    if (count <= 0 || count > kGemmGroupMax) return;
+    GroupedArgs ga{};
+    int waves = 2, start = 0;
+    for (int i = 0; i < count; ++i) {
+        const GemmPlan &p = plans[i];
+        // one 16-row block per tile in the grouped kernel
+        const int tiles_n = (p.N + 15) / 16;
+        const int tiles = ((p.M + 15) / 16) * tiles_n;
+        ga.prob[i] = GemmArgs{A[i], B[i], C[i], nullptr, p.M, p.N, p.K, tiles_n, p.k_per_split, 1,
+                              epi[i], tiles, (tiles + 7) / 8};
+        ga.starts[i] = start;
+        start += tiles;
+        waves = std::max(waves, p.waves);
+    }
+    ga.starts[count] = start;
+    ga.count = count;
+    if (start == 0) return;
+    switch (waves) {
+    case 2: gemm_small_grouped_kernel<2><<<(unsigned)start, 128, 0, s>>>(ga); break;
+    case 4: gemm_small_grouped_kernel<4><<<(unsigned)start, 256, 0, s>>>(ga); break;
+    case 8: gemm_small_grouped_kernel<8><<<(unsigned)start, 512, 0, s>>>(ga); break;
+    default: gemm_small_grouped_kernel<16><<<(unsigned)start, 1024, 0, s>>>(ga); break;
+    }
 }
 
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,

@@ -110,6 +110,12 @@ struct GemmEpilogue {
     int bias_mode = GEMM_BIAS_NONE;
     int act = GEMM_ACT_NONE;
 };
+// Independent small-path products in one launch (the planner's horizontal
+// MatMul groups): at most kGemmGroupMax; every plan must be small and a
+// softmax epilogue needs N <= 16.
+constexpr int kGemmGroupMax = 8;
+void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float *const *B,
+                      float *const *C, const GemmEpilogue *epi, int count, hipStream_t s);
 // Picks the tile configuration and K split for a shape.  a_aligned: A is
 // 16-byte aligned (the skinny path needs it).  force_cfg >= 0 overrides the
 // configuration and turns the skinny path off; force_skinny takes the skinny

@@ -7,6 +7,7 @@
 // Elementwise ops run as one-op fused chains (jit.cpp), the same kernels the
 // lazy planner emits for longer chains, so eager and fused results are
 // produced by identical device code.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
@@ -162,31 +163,43 @@ static bool gemm_skinny_override(int *nb, int *splits) {
     return true;
 }
 
-void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, const Tensor *bias,
-                             int act) {
+// Validates one product and builds its epilogue and plan.
+static k::GemmPlan prepare_matmul(const Tensor &a, const Tensor &b, const Tensor *bias, int act,
+                                  k::GemmEpilogue *epi) {
     need_f32(a, "a");
     need_f32(b, "b");
     size_t m, kk, n;
     matmul_dims(a, b, &m, &kk, &n);
-    Context &c = ctx();
-    k::GemmEpilogue epi;
     if (bias) {
         need_f32(*bias, "bias");
         CLOVE_REQUIRE(bias->numel > 0, CLOVE_HIP_ERR_SHAPE, "bias is empty");
-        epi.bias = bias->f32();
-        epi.bias_n = bias->numel;
-        epi.bias_mode = bias->numel == 1 ? k::GEMM_BIAS_SCALAR
-                        : bias->numel == n ? k::GEMM_BIAS_COL
-                                           : k::GEMM_BIAS_MOD;
+        epi->bias = bias->f32();
+        epi->bias_n = bias->numel;
+        epi->bias_mode = bias->numel == 1 ? k::GEMM_BIAS_SCALAR
+                         : bias->numel == n ? k::GEMM_BIAS_COL
+                                            : k::GEMM_BIAS_MOD;
     }
     CLOVE_REQUIRE(act >= k::GEMM_ACT_NONE && act <= k::GEMM_ACT_SOFTMAX, CLOVE_HIP_ERR_INVALID,
                   "unknown GEMM epilogue activation");
-    epi.act = act;
+    epi->act = act;
     int sk_nb, sk_splits;
     const bool sk_force = gemm_skinny_override(&sk_nb, &sk_splits);
     const bool a_aligned = (reinterpret_cast<uintptr_t>(a.data) & 15) == 0;
-    const k::GemmPlan p = k::gemm_plan((int)m, (int)n, (int)kk, c.num_cus, gemm_cfg_override(),
-                                       a_aligned, sk_force, sk_nb, sk_splits);
+    return k::gemm_plan((int)m, (int)n, (int)kk, ctx().num_cus, gemm_cfg_override(), a_aligned,
+                        sk_force, sk_nb, sk_splits);
+}
+
+// A product the grouped small kernel can take: the small path, and for a
+// softmax epilogue whole rows in one 16-column tile.
+static bool groupable(const k::GemmPlan &p, int act) {
+    return p.small && (act != k::GEMM_ACT_SOFTMAX || p.N <= 16);
+}
+
+void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, const Tensor *bias,
+                             int act) {
+    k::GemmEpilogue epi;
+    const k::GemmPlan p = prepare_matmul(a, b, bias, act, &epi);
+    hipStream_t s = ctx().stream;
     TensorNode ws;
     if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
     if (act == k::GEMM_ACT_SOFTMAX && !(p.small && p.tiles_n == 1)) {
@@ -194,11 +207,42 @@ void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, cons
         // and bias into a temporary, then the row softmax into `out`
         epi.act = k::GEMM_ACT_NONE;
         TensorNode tmp = new_tensor(out.shape, CLOVE_HIP_F32);
-        k::gemm_f32(p, a.f32(), b.f32(), tmp->f32(), ws ? ws->f32() : nullptr, epi, c.stream);
+        k::gemm_f32(p, a.f32(), b.f32(), tmp->f32(), ws ? ws->f32() : nullptr, epi, s);
         softmax_into(*tmp, out);
         return;
     }
-    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, epi, c.stream);
+    k::gemm_f32(p, a.f32(), b.f32(), out.f32(), ws ? ws->f32() : nullptr, epi, s);
+}
+
+// The lazy path's horizontal MatMul group (lazy.rs:2443-2493, executed at
+// :3483-3557 as one compute pass with a dispatch per product): independent
+// products whose plans take the small path run in ONE grouped launch (up to
+// k::kGemmGroupMax per launch); the others run one by one.
+void HipBackend::matmul_group_into(const std::vector<GemmMember> &members) {
+    std::vector<k::GemmPlan> plans;
+    std::vector<const float *> A, B;
+    std::vector<float *> C;
+    std::vector<k::GemmEpilogue> epis;
+    std::vector<const GemmMember *> rest;
+    for (const GemmMember &g : members) {
+        k::GemmEpilogue epi;
+        const k::GemmPlan p = prepare_matmul(*g.a, *g.b, g.bias, g.act, &epi);
+        if (!groupable(p, g.act)) {
+            rest.push_back(&g);
+            continue;
+        }
+        plans.push_back(p);
+        A.push_back(g.a->f32());
+        B.push_back(g.b->f32());
+        C.push_back(g.out->f32());
+        epis.push_back(epi);
+    }
+    hipStream_t s = ctx().stream;
+    for (size_t i = 0; i < plans.size(); i += k::kGemmGroupMax) {
+        const int count = (int)std::min<size_t>(k::kGemmGroupMax, plans.size() - i);
+        k::gemm_f32_grouped(&plans[i], &A[i], &B[i], &C[i], &epis[i], count, s);
+    }
+    for (const GemmMember *g : rest) matmul_into(*g->a, *g->b, *g->out, g->bias, g->act);
 }
 
 // backend.rs:1282-1306: m = prod(a.shape[..last]), k = a.shape[last],

@@ -120,6 +120,14 @@ struct HipBackend {
     // act 0 none, 1 ReLU, 2 GELU (CLOVE_OP_* elementwise semantics).
     static void matmul_into(const Tensor &a, const Tensor &b, Tensor &out,
                             const Tensor *bias = nullptr, int act = 0);
+    // One member of a horizontal MatMul group: out = act(a.b + bias).
+    struct GemmMember {
+        const Tensor *a, *b;
+        Tensor *out;
+        const Tensor *bias;
+        int act;
+    };
+    static void matmul_group_into(const std::vector<GemmMember> &members);
     static void paged_attention_into(const Tensor &q, const Tensor *k, const Tensor *v,
                                      const Tensor &kv_cache, const Tensor &block_tables,
                                      const Tensor &context_lens, float scale, Tensor &out);

@@ -124,6 +124,35 @@ def test_plan_epilogue_fusion_only_for_sole_consumers():
     assert steps(m2) == ["MatMul", "Fused[Add]"]
 
 
+def test_plan_horizontal_matmul_group():
+    # lazy.rs:2443-2493: consecutive MatMul steps none of which reads another's
+    # output form one group (here a Q/K/V projection of one input, each with
+    # its own epilogue); a MatMul reading a member's output ends the group.
+    g = ca.Graph()
+    x = g.input("S0,64")
+    wq, wk, wv, bq = g.input("64,64"), g.input("64,64"), g.input("64,32"), g.input("64")
+    q = g.op("add", g.op("matmul", x, wq), bq)
+    k = g.op("relu", g.op("matmul", x, wk))
+    v = g.op("matmul", x, wv)
+    z = g.op("matmul", q, wk)                       # reads q: not in the group
+    m = g.compile([q, k, v, z])
+    assert steps(m) == ["MatMulGroup[MatMul+Add,MatMul+ReLU,MatMul]", "MatMul"]
+    # the shared input x is listed once among the group's inputs
+    first = m.describe().splitlines()[0]
+    ins = first[first.index("in=(") + 4:first.index(")")].split(",")
+    assert len(ins) == len(set(ins)) == 5
+
+
+def test_plan_dependent_matmuls_stay_apart():
+    g = ca.Graph()
+    x, w1, w2, w3 = g.input("4,8"), g.input("8,8"), g.input("8,8"), g.input("8,8")
+    a = g.op("matmul", x, w1)
+    b = g.op("matmul", x, w2)
+    c = g.op("matmul", b, w3)                       # reads the second member
+    m = g.compile([a, c])
+    assert steps(m) == ["MatMulGroup[MatMul,MatMul]", "MatMul"]
+
+
 def test_plan_dce_and_constant_folding():
     g = ca.Graph()
     a = g.input("4,4")

@@ -237,3 +237,50 @@ def test_gemm_k0_epilogue(hip, act):
     z = hip.matmul(hip.tensor(np.zeros((m, 0), np.float32)),
                    hip.tensor(np.zeros((0, n), np.float32))).numpy()
     assert z.shape == (m, n) and np.all(z == 0)
+
+
+def test_horizontal_matmul_group(hip):
+    """Independent MatMuls (lazy.rs:2443-2493) run as one grouped launch:
+    a Q/K/V-style projection of one input with bias, ReLU and a softmax
+    head, plus a K = 2048 product that the group runs on its own.  Each
+    output matches the eager composition bit for bit (the same per-wave K
+    ranges as a single launch) and the oracle within the matmul bound."""
+    S, E = 37, 64
+    gg = rng(94)
+    x = gg.normal(0, 1 / 8, (S, E)).astype(np.float32)
+    y = gg.normal(0, 1 / 45, (S, 2048)).astype(np.float32)
+    wq, wk = (gg.normal(0, 1, (E, E)).astype(np.float32) for _ in range(2))
+    wv = gg.normal(0, 1, (E, 32)).astype(np.float32)
+    wh = gg.normal(0, 1, (E, 10)).astype(np.float32)
+    wy = gg.normal(0, 1, (2048, 16)).astype(np.float32)
+    bq = gg.normal(0, 1, E).astype(np.float32)
+    bh = gg.normal(0, 1, 10).astype(np.float32)
+    g = hip.Graph()
+    ix, iy = g.input(f"{S},{E}"), g.input(f"{S},2048")
+    iwq, iwk, iwv, iwh, iwy = (g.input(f"{a},{b}") for a, b in
+                               ((E, E), (E, E), (E, 32), (E, 10), (2048, 16)))
+    ibq, ibh = g.input(f"{E}"), g.input("10")
+    q = g.op("add", g.op("matmul", ix, iwq), ibq)
+    k = g.op("relu", g.op("matmul", ix, iwk))
+    v = g.op("matmul", ix, iwv)
+    h = g.op("softmax", g.op("add", g.op("matmul", ix, iwh), ibh))
+    z = g.op("matmul", iy, iwy)
+    model = g.compile([q, k, v, h, z])
+    assert model.num_steps == 1 and model.describe().startswith("MatMulGroup["), model.describe()
+    t = hip.tensor
+    ins = [t(a) for a in (x, y, wq, wk, wv, wh, wy, bq, bh)]
+    outs = [o.numpy() for o in model.execute(ins)]
+    tx, ty, twq, twk, twv, twh, twy, tbq, tbh = ins
+    eager = [hip.add(hip.matmul(tx, twq), tbq), hip.relu(hip.matmul(tx, twk)),
+             hip.matmul(tx, twv), None, hip.matmul(ty, twy)]
+    for i, e in enumerate(eager):
+        if e is not None:
+            assert np.array_equal(outs[i], e.numpy()), f"member {i} differs from eager"
+    want = [oracle.add(oracle.matmul(x, wq), bq), oracle.relu(oracle.matmul(x, wk)),
+            oracle.matmul(x, wv), oracle.softmax(oracle.add(oracle.matmul(x, wh), bh)),
+            oracle.matmul(y, wy)]
+    for i, (got, w_) in enumerate(zip(outs, want)):
+        if i == 3:
+            assert_close(got, w_, 1e-4, 1e-7, "softmax head member")
+        else:
+            assert_close(got, w_, 2e-3, 1e-4 * float(np.abs(w_).max()), f"member {i}")
