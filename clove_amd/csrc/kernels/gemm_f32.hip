@@ -320,7 +320,7 @@ __global__ void __launch_bounds__(64) gemm_splitk_reduce(const float *__restrict
     }
 }
 
-// Skinny GEMM, M <= 32*MB (the 32-row decode-style product, the MLP layers).
+// Skinny GEMM, M <= 32*MB (the 32-row decode-style product).
 //
 // With M this small, B (K x N) is almost all of the HBM traffic and every B
 // element feeds at most MB MFMA steps, so the kernel is a stream over B that

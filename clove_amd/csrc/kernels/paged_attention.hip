@@ -174,57 +174,6 @@ __device__ __forceinline__ void fold_block(const PagedArgs &a, const float *kb, 
     st.m = m_new;
 }
 
-// Folds NB whole KV blocks (every row in range, no new-token row) into the
-// running state in one step: the K and V rows of all NB blocks are issued
-// before any arithmetic, so a wave keeps NB * 16 KiB in flight.  `off[n]`
-// is this lane's offset of block n's row `row` in a plane.
-template <int D, int BS, int NB>
-__device__ __forceinline__ void fold_full(const PagedArgs &a, const size_t (&off)[NB],
-                                          size_t row_stride, const cl_f4 (&q)[D / 64],
-                                          WaveState &st, cl_f4 (&o)[D / 64]) {
-    constexpr int NV = D / 64;
-    constexpr int STEPS = BS / 4;
-    constexpr int T = NB * STEPS;
-    cl_f4 kk[T][NV], vv[T][NV];
-#pragma unroll
-    for (int n = 0; n < NB; ++n)
-#pragma unroll
-        for (int s = 0; s < STEPS; ++s) {
-            const float *kp = a.k_cache + off[n] + (size_t)(4 * s) * row_stride;
-            const float *vp = a.v_cache + off[n] + (size_t)(4 * s) * row_stride;
-#pragma unroll
-            for (int j = 0; j < NV; ++j) {
-                kk[n * STEPS + s][j] = stream_load(kp + 64 * j);
-                vv[n * STEPS + s][j] = stream_load(vp + 64 * j);
-            }
-        }
-    float sc[T];
-    float bm = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < T; ++s) {
-        float d = dot4(q[0], kk[s][0]);
-#pragma unroll
-        for (int j = 1; j < NV; ++j) d += dot4(q[j], kk[s][j]);
-        sc[s] = row16_sum(d) * a.scale;
-        bm = fmaxf(bm, sc[s]);
-    }
-    bm = fmaxf(bm, __shfl_xor(bm, 16, 64));
-    bm = fmaxf(bm, __shfl_xor(bm, 32, 64));
-    const float m_new = fmaxf(st.m, bm);
-    const float alpha = (st.m == -INFINITY) ? 0.0f : fast_exp(st.m - m_new);
-    st.l *= alpha;
-#pragma unroll
-    for (int j = 0; j < NV; ++j) o[j] *= alpha;
-#pragma unroll
-    for (int s = 0; s < T; ++s) {
-        const float p = fast_exp(sc[s] - m_new);
-        st.l += p;
-#pragma unroll
-        for (int j = 0; j < NV; ++j) o[j] += p * vv[s][j];
-    }
-    st.m = m_new;
-}
-
 // The K and V rows of one whole KV block as this lane holds them: step s
 // covers rows 4s + (lane >> 4), piece j floats 64j + 4(lane & 15).
 template <int D, int BS>
@@ -246,8 +195,8 @@ __device__ __forceinline__ void issue_block(const PagedArgs &a, size_t off, size
         }
 }
 
-// Folds a block whose loads `issue_block` issued into the running state;
-// the same arithmetic, in the same order, as fold_full<D, BS, 1>.
+// Folds a block whose loads `issue_block` issued into the running state
+// (the arithmetic of fold_block without the per-token checks).
 template <int D, int BS>
 __device__ __forceinline__ void consume_block(const PagedArgs &a, const BlockRegs<D, BS> &r,
                                               const cl_f4 (&q)[D / 64], WaveState &st,
@@ -390,8 +339,9 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
                 if (lane == 0) atomicOr(a.err_flag, 1);
                 continue;
             }
-            const size_t one[1] = {(size_t)blk * BS * row_stride + lane_off};
-            fold_full<D, BS, 1>(a, one, row_stride, q, st, o);
+            BlockRegs<D, BS> r;
+            issue_block<D, BS>(a, (size_t)blk * BS * row_stride + lane_off, row_stride, r);
+            consume_block<D, BS>(a, r, q, st, o);
         }
     }
     if (tail_checked) {
