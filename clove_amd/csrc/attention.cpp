@@ -86,8 +86,8 @@ TensorNode rope_table_for(int pos0, int npos, int head_dim, int *tab_pos0) {
 
 // lazy.rs:1621-1690 (the FlashAttention pattern) and :4821-4909 (its
 // kernel): q [B, S, H*D], k and v [B, Sk, H*D].  flags: causal mask on
-// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k,
-// applied in one pass each before the kernel.  scale <= 0 means 1/sqrt(D),
+// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k (k
+// in one pass before the kernel, q inside it).  scale <= 0 means 1/sqrt(D),
 // the reference's.
 TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,
                                        const TensorNode &v_, int num_heads, int q_pos, int k_pos,
@@ -125,22 +125,22 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
     TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
     hipStream_t s = ctx().stream;
-    const float *qp = q.f32(), *kp = k.f32();
-    TensorNode qr, kr;
+    const float *kp = k.f32();
+    TensorNode kr, tab;
+    int t0 = 0;
     if (flags & CLOVE_ATTN_ROPE) {
+        // k is rotated in one pass (every query block stages the same keys);
+        // q is rotated inside the kernel, once per query, from the same table
         const int p0 = std::min(q_pos, k_pos);
         const int p1 = (int)std::max((size_t)q_pos + S, (size_t)k_pos + Sk);
-        int t0 = 0;
-        TensorNode tab = rope_table_for(p0, p1 - p0, D, &t0);
-        qr = new_tensor(q.shape, CLOVE_HIP_F32);
+        tab = rope_table_for(p0, p1 - p0, D, &t0);
         kr = new_tensor(k.shape, CLOVE_HIP_F32);
-        k::rope_apply(qp, qr->f32(), B * S, (int)S, (int)X, D, q_pos, tab->f32(), t0, s);
         k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), t0, s);
-        qp = qr->f32();
         kp = kr->f32();
     }
-    k::attention_prefill(qp, kp, v.f32(), out->f32(), (int)B, (int)S, (int)Sk, num_heads, D,
-                         q_pos, k_pos, (flags & CLOVE_ATTN_CAUSAL) != 0, sc, s);
+    k::attention_prefill(q.f32(), kp, v.f32(), out->f32(), (int)B, (int)S, (int)Sk, num_heads, D,
+                         q_pos, k_pos, (flags & CLOVE_ATTN_CAUSAL) != 0, sc,
+                         tab ? tab->f32() : nullptr, t0, s);
     return out;
 }
 

@@ -59,6 +59,8 @@ struct AttnArgs {
     int q_pos, k_pos;
     float scale;
     int nqb;        // query blocks per (batch, head)
+    const float2 *rope_tab;  // (cos, sin) per (position, pair) to rotate q, or null
+    int tab_pos0;            // position of rope_tab's first row
 };
 
 __device__ __forceinline__ float fast_exp(float x) {
@@ -95,11 +97,29 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     // softmax scale.  Scaling here also makes the Q loads complete before the
     // key loop: first used inside it, they would make the compiler wait for
     // every outstanding load (the next tile's included) at each block.
+    // With RoPE, q's pairs (dims 8g + 4hh + {0,1} and {2,3}, whole pairs in
+    // this lane) are rotated here, with the arithmetic of the RoPE pass
+    // (rope_rows_kernel), before the scale: the same values that pass would
+    // have stored, without its read and write of q.
+    const float2 *trow = a.rope_tab && q_ok
+                             ? a.rope_tab + (size_t)(query + a.q_pos - a.tab_pos0) * (D / 2)
+                             : nullptr;
     cl_f4 qf[kG];
 #pragma unroll
-    for (int g = 0; g < kG; ++g)
-        qf[g] = (q_ok ? *reinterpret_cast<const cl_f4 *>(qrow + 8 * g + 4 * hh)
-                      : (cl_f4){0.f, 0.f, 0.f, 0.f}) * a.scale;
+    for (int g = 0; g < kG; ++g) {
+        cl_f4 v = q_ok ? *reinterpret_cast<const cl_f4 *>(qrow + 8 * g + 4 * hh)
+                       : (cl_f4){0.f, 0.f, 0.f, 0.f};
+        if (trow) {
+            const float2 t0 = trow[4 * g + 2 * hh], t1 = trow[4 * g + 2 * hh + 1];
+            cl_f4 r;
+            r.x = v.x * t0.x - v.y * t0.y;
+            r.y = v.x * t0.y + v.y * t0.x;
+            r.z = v.z * t1.x - v.w * t1.y;
+            r.w = v.z * t1.y + v.w * t1.x;
+            v = r;
+        }
+        qf[g] = v * a.scale;
+    }
 
     // keys [0, k_end) can be visible to some query of the workgroup
     int k_end = a.Sk;
@@ -367,9 +387,10 @@ bool attention_supported(int head_dim) { return head_dim == 64 || head_dim == 12
 
 void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
                        int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
-                       hipStream_t s) {
+                       const float *q_rope_tab, int tab_pos0, hipStream_t s) {
     if (B <= 0 || S <= 0 || H <= 0) return;
-    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0};
+    AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0,
+               reinterpret_cast<const float2 *>(q_rope_tab), tab_pos0};
     a.nqb = (S + kBQ - 1) / kBQ;
     const unsigned grid = (unsigned)(B * H * a.nqb);
     if (D == 64) {

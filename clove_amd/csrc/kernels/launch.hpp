@@ -51,9 +51,13 @@ void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s);
 // flash_attention.hip -- attention prefill and RoPE.  q [B, S, H*D], k, v
 // [B, Sk, H*D], out [B, S, H*D], all 16-byte aligned; D in {64, 128}.
 bool attention_supported(int head_dim);
+// q_rope_tab: a (cos, sin) table (rope_table layout) whose rows cover
+// positions q_pos .. q_pos + S - 1 from tab_pos0, to rotate q inside the
+// kernel, or null (k must then already be rotated by the caller when RoPE
+// applies).
 void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
                        int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
-                       hipStream_t s);
+                       const float *q_rope_tab, int tab_pos0, hipStream_t s);
 // freq.div[j] = 10000^(2j / D) (powf on the host, as backend.rs:2818 forms it).
 struct AttnFreq {
     float div[128];

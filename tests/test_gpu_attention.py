@@ -49,7 +49,7 @@ CASES = [
     (1, 1, 1, 1, 128, 3, 0, 0),
     (1, 33, 31, 2, 64, 2, 0, 0),
     (3, 200, 77, 1, 128, 0, 0, 0),
-    # long runs of whole key blocks (the pipelined path of the kernel)
+    # long runs of whole key blocks
     (1, 300, 700, 2, 64, 0, 0, 0),
     (2, 129, 513, 3, 128, 2, 0, 0),
     (1, 512, 512, 2, 128, 1, 0, 0),
@@ -93,3 +93,19 @@ def test_flash_attention_prefill_4096_sampled(hip):
     for lo, hi in ((0, 2), (127, 130), (2047, 2049), (4094, 4096)):
         want = oracle.attention(q, k, v, H, rows=(lo, hi))
         assert_close(got[:, lo:hi], want[:, lo:hi], 2e-3, 1e-5, f"rows {lo}..{hi}")
+
+
+@pytest.mark.parametrize("B,S,Sk,H,D,flags,q_pos,k_pos", [(1, 130, 130, 2, 128, 3, 0, 0),
+                                                          (2, 65, 200, 3, 64, 2, 135, 0),
+                                                          (1, 300, 300, 1, 128, 3, 7, 7)])
+def test_attention_rope_equals_rope_then_attention(hip, B, S, Sk, H, D, flags, q_pos, k_pos):
+    """The RoPE flag rotates k in a pass and q inside the kernel; both use the
+    RoPE op's arithmetic and table, so the result equals rotating q and k with
+    the RoPE op and running attention without the flag, bit for bit."""
+    g = rng(95 + S)
+    q, k, v = (g.standard_normal((B, n, H * D)).astype(np.float32) for n in (S, Sk, Sk))
+    t = hip.tensor
+    fused = hip.flash_attention(t(q), t(k), t(v), H, q_pos, k_pos, flags).numpy()
+    qr, kr = hip.rope(t(q), D, q_pos), hip.rope(t(k), D, k_pos)
+    split = hip.flash_attention(qr, kr, t(v), H, q_pos, k_pos, flags & ~2).numpy()
+    assert np.array_equal(fused, split)
