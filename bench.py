@@ -372,7 +372,7 @@ def bench_attention(ca, oracle, args, out):
     k = ca.empty((B, S, H * D)).fill_normal(32)
     v = ca.empty((B, S, H * D)).fill_normal(33)
     steps = max(5, args.steps // 10)
-    wall, per = timed(ca, lambda: ca.flash_attention(q, k, v, H), steps, max(2, args.warmup // 5))
+    wall, per = timed(ca, lambda: ca.flash_attention(q, k, v, H), steps, max(10, args.warmup // 2))
     flops = 4.0 * D * H * S * (S + 1) / 2
     tf = flops / (per.mean() * 1e-3) / 1e12
     part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
