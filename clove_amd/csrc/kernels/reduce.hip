@@ -200,7 +200,21 @@ __global__ void __launch_bounds__(256) ordered_sum_kernel(const float *__restric
     if (threadIdx.x == 0) out[0] = (sign * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]))) / div;
 }
 
-// MSE backward (backend.rs:2780-2790): grad = 2 * (p - t) * g / n.
+// x / y correctly rounded, for a y shared by many x, from r = 1 / y (IEEE):
+// q0 = x r, then one FMA correction of the remainder (Markstein's method).
+// With r the correctly rounded reciprocal this is the IEEE quotient; checked
+// against x / y for every integer y up to 70000 over 2000 random x each
+// (normal range, both signs).  An infinite q0 (x infinite) is returned as is.
+__device__ __forceinline__ float div_exact(float x, float y, float r) {
+    const float q0 = x * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, y, x), r, q0);
+    return __builtin_isfinite(q0) ? q1 : q0;
+}
+
+// MSE backward (backend.rs:2780-2790): grad = 2 * (p - t) * g / n, each
+// step rounded in that order.  VEC: 16-byte streaming loads and stores over
+// the whole vectors (p, t, grad 16-byte aligned), the tail element by element.
+template <bool VEC>
 __global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restrict__ p,
                                                            const float *__restrict__ t,
                                                            uint64_t n,
@@ -208,9 +222,25 @@ __global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restri
                                                            float *__restrict__ grad) {
     const float g = grad_loss[0];
     const float nf = (float)n;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n;
-         i += (uint64_t)gridDim.x * 256)
-        grad[i] = 2.0f * (p[i] - t[i]) * g / nf;
+    const float rn = 1.0f / nf;
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    uint64_t tail = 0;
+    if (VEC) {
+        const uint64_t nv = n / 4;
+        const cl_f4 *p4 = reinterpret_cast<const cl_f4 *>(p);
+        const cl_f4 *t4 = reinterpret_cast<const cl_f4 *>(t);
+        cl_f4 *g4 = reinterpret_cast<cl_f4 *>(grad);
+        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nv; i += stride) {
+            const cl_f4 d = __builtin_nontemporal_load(p4 + i) - __builtin_nontemporal_load(t4 + i);
+            const cl_f4 x = 2.0f * d * g;
+            __builtin_nontemporal_store((cl_f4){div_exact(x.x, nf, rn), div_exact(x.y, nf, rn),
+                                                div_exact(x.z, nf, rn), div_exact(x.w, nf, rn)},
+                                        g4 + i);
+        }
+        tail = 4 * nv;
+    }
+    for (uint64_t i = tail + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+        grad[i] = div_exact(2.0f * (p[i] - t[i]) * g, nf, rn);
 }
 
 // ---- transpose: out[c][r] = in[r][c] for an R x C matrix ------------------
@@ -297,9 +327,15 @@ void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hi
 void mse_backward(const float *p, const float *t, size_t n, const float *grad_loss, float *grad,
                   hipStream_t s) {
     if (!n) return;
-    size_t blocks = (n + 255) / 256;
-    if (blocks > 65536) blocks = 65536;
-    mse_backward_kernel<<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
+    const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t) |
+                       reinterpret_cast<uintptr_t>(grad)) & 15) == 0;
+    // vectors per thread per pass: a grid of up to 8192 workgroups, the
+    // streaming kernels' shape
+    size_t blocks = ((vec ? n / 4 : n) + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    if (blocks == 0) blocks = 1;
+    if (vec) mse_backward_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
+    else mse_backward_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
 }
 
 void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s) {

@@ -38,6 +38,17 @@ __device__ __forceinline__ float fast_exp(float x) {
     return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
 }
 
+// x / y correctly rounded, for a y shared by many x, from r = 1 / y (IEEE):
+// q0 = x r, then one FMA correction of the remainder (Markstein's method).
+// With r the correctly rounded reciprocal this is the IEEE quotient; checked
+// against x / y for every integer y up to 70000 over 2000 random x each
+// (normal range, both signs).  An infinite q0 (x infinite) is returned as is.
+__device__ __forceinline__ float div_exact(float x, float y, float r) {
+    const float q0 = x * r;
+    const float q1 = __builtin_fmaf(__builtin_fmaf(-q0, y, x), r, q0);
+    return __builtin_isfinite(q0) ? q1 : q0;
+}
+
 template <int VPT>
 __global__ void __launch_bounds__(256) softmax_wave_kernel(const float *__restrict__ x,
                                                            float *__restrict__ y, int rows,
@@ -307,6 +318,7 @@ __global__ void __launch_bounds__(256) cross_entropy_wave_kernel(
     const float inv = 1.0f / s;
     const float g = grad_loss[0];
     const float fr = (float)rows;
+    const float rr = 1.0f / fr;
 #pragma unroll
     for (int i = 0; i < VPT; ++i) {
         const int c = lane + 64 * i;
@@ -314,7 +326,10 @@ __global__ void __launch_bounds__(256) cross_entropy_wave_kernel(
             cl_f4 p = v[i] * inv;
             const long j0 = 4l * c;
             if (t >= j0 && t < j0 + 4) p[t - j0] -= 1.0f;
-            __builtin_nontemporal_store((p * g) / fr, go + c);
+            const cl_f4 x = p * g;
+            __builtin_nontemporal_store((cl_f4){div_exact(x.x, fr, rr), div_exact(x.y, fr, rr),
+                                                div_exact(x.z, fr, rr), div_exact(x.w, fr, rr)},
+                                        go + c);
         }
     }
 }
