@@ -282,8 +282,9 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 
 // C[row][col] = sum over splits, in split order, of the parked tiles
 // (deterministic).  One thread per four consecutive columns of a tile row;
-// the loads of four splits are issued before they are added (the additions
-// stay in split order), and one-wave workgroups spread the few thousand
+// the loads of eight splits are issued before any of them is added (the
+// additions stay in split order; a load-then-add loop would pay one memory
+// round trip per split), and one-wave workgroups spread the few thousand
 // threads over all CUs.
 __global__ void __launch_bounds__(64) gemm_splitk_reduce(const float *__restrict__ ws,
                                                          float *__restrict__ C, int M, int N,
@@ -301,19 +302,18 @@ __global__ void __launch_bounds__(64) gemm_splitk_reduce(const float *__restrict
         const int col = (tile % tiles_n) * BN + c;
         if (row >= M || col >= N) continue;
         const float *src = ws + (size_t)tile * BM * BN + (size_t)r * BN + c;
-        f4 sum = *reinterpret_cast<const f4 *>(src);
-        int sp = 1;
-        for (; sp + 4 <= splits; sp += 4) {
-            const f4 v0 = *reinterpret_cast<const f4 *>(src + (size_t)sp * split_stride);
-            const f4 v1 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 1) * split_stride);
-            const f4 v2 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 2) * split_stride);
-            const f4 v3 = *reinterpret_cast<const f4 *>(src + (size_t)(sp + 3) * split_stride);
-            sum += v0;
-            sum += v1;
-            sum += v2;
-            sum += v3;
+        constexpr int kBatch = 8;
+        f4 sum = {0.f, 0.f, 0.f, 0.f};
+        for (int sp0 = 0; sp0 < splits; sp0 += kBatch) {
+            f4 v[kBatch];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)
+                if (sp0 + u < splits)
+                    v[u] = *reinterpret_cast<const f4 *>(src + (size_t)(sp0 + u) * split_stride);
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u)  // the first split is taken as is
+                if (sp0 + u < splits) sum = sp0 + u == 0 ? v[u] : sum + v[u];
         }
-        for (; sp < splits; ++sp) sum += *reinterpret_cast<const f4 *>(src + (size_t)sp * split_stride);
 #pragma unroll
         for (int q = 0; q < 4; ++q)
             if (col + q < N) C[(size_t)row * N + col + q] = epilogue(epi, sum[q], row, col + q, N);
@@ -358,6 +358,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void *base, ui
                                              0x00020000);
 }
 
+// Groups of 8 k values in flight per wave in the skinny kernel: two.  Deeper
+// pipelines put more of B in flight at once and ran slower on every skinny
+// shape measured (32x4096x4096: depth 1 20.1 us, 2 17.3 us, 4 18.6 us,
+// 8 19.8 us, 16 23.5 us; 64x11008x4096: 65.4 us at depth 2, 75 us at 4 or 8).
+constexpr int kSkinnyDepth = 2;
+
 template <int NB>
 __device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff,
                                        float *dst) {
@@ -381,7 +387,7 @@ __device__ __forceinline__ void load_b(__amdgpu_buffer_rsrc_t r, uint32_t voff, 
 
 template <int MB, int NB, int W, int CH>
 __global__ void __launch_bounds__(64 * W) gemm_skinny_kernel(GemmArgs g) {
-    constexpr int D = NB == 4 ? 4 : 8;           // 8-groups in flight per wave
+    constexpr int D = kSkinnyDepth;              // 8-groups in flight per wave
     constexpr int k_per_wave = 8 * D * CH;       // CH chunks of D groups
     constexpr int kRows = 32 * MB, kCols = 32 * NB;
     constexpr int kBlock = kRows * kCols;        // floats of one wave's partial tile
@@ -726,12 +732,13 @@ void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
 
 template <int MB, int NB, int W>
 void launch_skinny_w(const GemmPlan &p, const GemmArgs &g, dim3 grid, hipStream_t s) {
-    constexpr int chunk = 8 * (NB == 4 ? 4 : 8);  // k per chunk of pipeline groups
+    constexpr int chunk = 8 * kSkinnyDepth;      // k per chunk of pipeline groups
     switch (p.k_per_wave / chunk) {
     case 1: gemm_skinny_kernel<MB, NB, W, 1><<<grid, 64 * W, 0, s>>>(g); break;
     case 2: gemm_skinny_kernel<MB, NB, W, 2><<<grid, 64 * W, 0, s>>>(g); break;
     case 4: gemm_skinny_kernel<MB, NB, W, 4><<<grid, 64 * W, 0, s>>>(g); break;
-    default: gemm_skinny_kernel<MB, NB, W, 8><<<grid, 64 * W, 0, s>>>(g); break;
+    case 8: gemm_skinny_kernel<MB, NB, W, 8><<<grid, 64 * W, 0, s>>>(g); break;
+    default: gemm_skinny_kernel<MB, NB, W, 16><<<grid, 64 * W, 0, s>>>(g); break;
     }
 }
 
@@ -785,7 +792,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // a 16-byte aligned A and B under 2 GiB.  NB column blocks per wave: 4
     // for M <= 32, 2 for M <= 64, fewer when N is not a multiple.  It is
     // chosen for a B of 4 MiB and more: there it measured ahead of the tiled
-    // kernel (M=32, N=K=4096: 19.0 against 19.4 us, reduce included); on
+    // kernel (M=32, N=K=4096: 17.3 against 19.4 us, reduce included); on
     // small B the tiled split-K kernel finishes first (more parallelism per
     // MFMA chain), so the skinny path runs there only when forced.
     const uint64_t b_bytes = (uint64_t)K * (uint64_t)N * 4u;
@@ -831,7 +838,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         p.nb = nb;
         p.waves = (nb == 1 || (nb == 2 && p.mb == 1)) ? 8 : 4;
         const int W = p.waves;
-        const int chunk = 8 * (nb == 4 ? 4 : 8);
+        const int chunk = 8 * kSkinnyDepth;
         p.tiles_n = (N + 32 * nb - 1) / (32 * nb);
         p.tiles = p.tiles_n;
         // Splits: enough workgroups for every CU and one wave per SIMD
@@ -845,11 +852,11 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         if (force_skinny_splits > 0) splits = force_skinny_splits;
         if (splits > 64) splits = 64;
         if (splits < 1) splits = 1;
-        // k_per_wave is chunk * CH for CH in {1, 2, 4, 8} (kernel variants);
+        // k_per_wave is chunk * CH for CH in {1, 2, 4, 8, 16} (kernel variants);
         // a longer range takes more splits instead.
         const int kw_raw = (K + splits * W - 1) / (splits * W);
         int ch = 1;
-        while (ch < 8 && chunk * ch < kw_raw) ch *= 2;
+        while (ch < 16 && chunk * ch < kw_raw) ch *= 2;
         p.k_per_wave = chunk * ch;
         p.k_per_split = p.k_per_wave * W;
         p.splits = (K + p.k_per_split - 1) / p.k_per_split;
