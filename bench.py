@@ -4,6 +4,10 @@
 One "step" is one pass of the fused elementwise chain y = gelu(a*b + c) * d
 over the four 16,777,216-element f32 inputs of configuration 2 (the workload
 the headline metric is quoted on), with every input already resident in HBM.
+Consecutive steps of every HBM-bound part cycle through --sets (default 3)
+identical copies of its inputs: MI355X's 256 MB last-level cache (MALL) would
+otherwise still hold part of a step's inputs from the step before, which
+reads 2-8 points of HBM peak faster than HBM itself.
 Rank 0 prints ONE JSON line on stdout:
 
   value        whole-job algorithmic HBM GB/s of the step (5 x 64 MiB per step)
@@ -78,6 +82,18 @@ def timed(ca, launch, steps, warmup):
     return wall, Timing(wall, ca.event_elapsed(e0, e1) / steps)
 
 
+def rotating(launches):
+    """One launch callable per input set; each call of the result runs the
+    next set's, so consecutive steps read different copies of the inputs."""
+    i = [0]
+
+    def run():
+        f = launches[i[0] % len(launches)]
+        i[0] += 1
+        return f()
+    return run
+
+
 def cpu_time(fn, reps=3):
     best = []
     for _ in range(reps):
@@ -101,12 +117,16 @@ CHAIN = [("mul", -1, -2), ("add", 0, -3), ("gelu", 1), ("mul", 2, -4)]
 
 def bench_chain(ca, args, broadcast=False):
     n = 4096 * 4096
-    ins = [ca.empty((4096, 4096)).fill_normal(1 + i) for i in range(4)]
-    if broadcast:
-        ins[2] = ca.empty((4096,)).fill_normal(3)
+    sets = []
+    for _ in range(args.sets):  # identical copies (same seeds)
+        ins = [ca.empty((4096, 4096)).fill_normal(1 + i) for i in range(4)]
+        if broadcast:
+            ins[2] = ca.empty((4096,)).fill_normal(3)
+        sets.append(ins)
     nbytes = 4 * n * 5 if not broadcast else 4 * n * 4 + 4 * 4096
-    wall, per = timed(ca, ca.FusedChain(CHAIN, ins), args.steps, args.warmup)
-    return ins, nbytes, wall, per
+    wall, per = timed(ca, rotating([ca.FusedChain(CHAIN, ins) for ins in sets]), args.steps,
+                      args.warmup)
+    return sets[0], nbytes, wall, per
 
 
 def cpu_chain(oracle, ins_host):
@@ -116,13 +136,15 @@ def cpu_chain(oracle, ins_host):
 
 def bench_rows(ca, oracle, args, out):
     g = np.random.Generator(np.random.PCG64(2))
-    x = ca.empty((8192, 4096)).fill_normal(2, 0.0, 2.0)
+    xs_sets = [ca.empty((8192, 4096)).fill_normal(2, 0.0, 2.0) for _ in range(args.sets)]
+    x = xs_sets[0]
     gam = ca.tensor(g.uniform(0.5, 1.5, 4096).astype(np.float32))
     bet = ca.tensor(g.uniform(-0.1, 0.1, 4096).astype(np.float32))
     n = 8192 * 4096
     for name, launch, nbytes in (
-            ("softmax", lambda: ca.softmax(x), 2 * 4 * n),
-            ("layer_norm", lambda: ca.layer_norm(x, gam, bet), 2 * 4 * n + 2 * 4 * 4096)):
+            ("softmax", rotating([lambda x=x: ca.softmax(x) for x in xs_sets]), 2 * 4 * n),
+            ("layer_norm", rotating([lambda x=x: ca.layer_norm(x, gam, bet) for x in xs_sets]),
+             2 * 4 * n + 2 * 4 * 4096)):
         wall, per = timed(ca, launch, args.steps, args.warmup)
         gbs = nbytes / (per.mean() * 1e-3) / 1e9
         part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
@@ -168,7 +190,11 @@ def bench_matmul(ca, oracle, args, out):
     out["matmul_4096"] = part
     log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
         f"{per.mean():.3f} ms")
-    wall, per = timed(ca, lambda: ca.matmul(a32, b), args.steps, args.warmup)
+    # B (64 MiB) is what the skinny product streams: one copy per input set
+    bs = [b] + [ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64) for _ in range(args.sets - 1)]
+    wall, per = timed(ca, rotating([lambda bb=bb: ca.matmul(a32, bb) for bb in bs]), args.steps,
+                      args.warmup)
+    del bs[1:]
     nbytes = 4 * (32 * K + K * 4096 + 32 * 4096)
     gbs = nbytes / (per.mean() * 1e-3) / 1e9
     tfs = 2.0 * 32 * K * 4096 / (per.mean() * 1e-3) / 1e12
@@ -247,22 +273,27 @@ def bench_backward(ca, oracle, args, out):
     matmul backward: FP32 MFMA), CPU baseline on a bounded sample."""
     g = np.random.Generator(np.random.PCG64(7))
     R, Cc, N = 8192, 4096, 4096 * 4096
-    x = ca.empty((R, Cc)).fill_normal(2, 0.0, 2.0)
-    y = ca.softmax(x)
-    dy = ca.empty((R, Cc)).fill_normal(21)
     targets = ca.tensor(g.integers(0, Cc, R).astype(np.float32))
     one = ca.tensor(np.ones(1, np.float32))
-    a = ca.empty((4096, 4096)).fill_normal(5)
-    b = ca.empty((4096, 4096)).fill_normal(6)
+    sets = []
+    for _ in range(args.sets):  # identical copies (same seeds)
+        x = ca.empty((R, Cc)).fill_normal(2, 0.0, 2.0)
+        sets.append({"x": x, "y": ca.softmax(x), "dy": ca.empty((R, Cc)).fill_normal(21),
+                     "a": ca.empty((4096, 4096)).fill_normal(5),
+                     "b": ca.empty((4096, 4096)).fill_normal(6)})
+    x, y, dy, a, b = (sets[0][k] for k in ("x", "y", "dy", "a", "b"))
+
+    def each(f):
+        return rotating([lambda t=t: f(t) for t in sets])
     cases = [
-        ("softmax_backward", lambda: ca.softmax_backward(y, dy), 3 * 4 * R * Cc),
-        ("gelu_backward", lambda: ca.gelu_backward(a, b), 3 * 4 * N),
-        ("broadcast_grad", lambda: ca.broadcast_grad(a, 4096), 4 * N + 4 * 4096),
-        ("cross_entropy", lambda: ca.cross_entropy(x, targets), 4 * R * Cc + 4 * R),
-        ("cross_entropy_backward", lambda: ca.cross_entropy_backward(x, targets, one),
+        ("softmax_backward", each(lambda t: ca.softmax_backward(t["y"], t["dy"])), 3 * 4 * R * Cc),
+        ("gelu_backward", each(lambda t: ca.gelu_backward(t["a"], t["b"])), 3 * 4 * N),
+        ("broadcast_grad", each(lambda t: ca.broadcast_grad(t["a"], 4096)), 4 * N + 4 * 4096),
+        ("cross_entropy", each(lambda t: ca.cross_entropy(t["x"], targets)), 4 * R * Cc + 4 * R),
+        ("cross_entropy_backward", each(lambda t: ca.cross_entropy_backward(t["x"], targets, one)),
          2 * 4 * R * Cc + 4 * R),
-        ("mse", lambda: ca.mse(a, b), 2 * 4 * N),
-        ("mse_backward", lambda: ca.mse_backward(a, b, one), 3 * 4 * N),
+        ("mse", each(lambda t: ca.mse(t["a"], t["b"])), 2 * 4 * N),
+        ("mse_backward", each(lambda t: ca.mse_backward(t["a"], t["b"], one)), 3 * 4 * N),
     ]
     for name, launch, nbytes in cases:
         wall, per = timed(ca, launch, args.steps, args.warmup)
@@ -274,6 +305,7 @@ def bench_backward(ca, oracle, args, out):
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
             f"{per.mean() * 1e3:.1f} us")
+    del sets[1:]
     # AdamW on a 4096x4096 parameter: reads w, g, m, v, writes w, m, v
     w = ca.empty((4096, 4096)).fill_normal(11)
     gw = ca.empty((4096, 4096)).fill_normal(12, 0.0, 65536.0)
@@ -393,8 +425,11 @@ def bench_attention(ca, oracle, args, out):
     out["flash_attention_4096"] = part
     log(f"attention prefill S=4096 H=32 D=128 causal+rope: {tf:.1f} TFLOP/s "
         f"({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), {per.mean():.3f} ms")
-    x = ca.empty((1, S, H * D)).fill_normal(34)
-    wall, per = timed(ca, lambda: ca.rope(x, D), args.steps, args.warmup)
+    xs_sets = [ca.empty((1, S, H * D)).fill_normal(34) for _ in range(args.sets)]
+    x = xs_sets[0]
+    wall, per = timed(ca, rotating([lambda x=x: ca.rope(x, D) for x in xs_sets]), args.steps,
+                      args.warmup)
+    del xs_sets[1:]
     nbytes = 2 * 4 * S * H * D
     gbs = nbytes / (per.mean() * 1e-3) / 1e9
     out["rope"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
@@ -417,7 +452,7 @@ PART_KERNELS = {
     "chain_broadcast": ["clove_chain_mul_add_gelu_mul_b0020"],
     "softmax": ["softmax_wave_kernel<16>"],
     "layer_norm": ["layer_norm_wave_kernel<16>"],
-    "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 4>", "gemm_splitk_reduce"],
+    "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 8>", "gemm_splitk_reduce"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_wave_kernel<16>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
@@ -425,7 +460,7 @@ PART_KERNELS = {
     "cross_entropy": ["cross_entropy_wave_kernel<16, 0>", "ordered_sum_kernel"],
     "cross_entropy_backward": ["cross_entropy_wave_kernel<16, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
-    "mse_backward": ["mse_backward_kernel"],
+    "mse_backward": ["mse_backward_kernel<true>"],
     "rope": ["rope_rows_kernel"],
 }
 
@@ -457,11 +492,17 @@ def main():
                          "'none' "
                          "(the config 2 chain always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--sets", type=int, default=3,
+                    help="identical copies of each HBM-bound part's inputs that consecutive "
+                         "steps cycle through, so that no step finds its inputs in the 256 MB "
+                         "last-level cache (MALL) from the step before")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "hbm_traffic.json"),
                     help="JSON summary of the rocprof FETCH_SIZE/WRITE_SIZE passes "
                          "(bytes per launch of the chain kernel)")
     args = ap.parse_args()
 
+    if args.sets < 1:
+        ap.error("--sets must be at least 1")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
               "build (see DESIGN.md for how the path would shard)", file=sys.stderr)
@@ -495,7 +536,8 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
         "data": "synthetic (splitmix64 normal(0,1) streams, seeds 1-4)",
         "config": {"workload": "config 2: fused chain y = gelu(a*b+c)*d, 4 x [4096,4096] f32",
-                   "elements": 4096 * 4096, "bytes_per_step": nbytes},
+                   "elements": 4096 * 4096, "bytes_per_step": nbytes,
+                   "input_sets": args.sets},
         "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s", traffic),
     }
     if oracle is not None:
@@ -513,9 +555,11 @@ def main():
         # A plain copy through the same chain kernel (one Flatten op): the
         # practical streaming ceiling of this box, and the known-size kernel
         # that calibrates the HBM byte counters.
-        src = ca.empty((4096, 4096)).fill_normal(9)
-        cwall, cper = timed(ca, ca.FusedChain([("flatten", -1)], [src]), args.steps,
-                            args.warmup)
+        srcs = [ca.empty((4096, 4096)).fill_normal(9) for _ in range(args.sets)]
+        cwall, cper = timed(ca, rotating([ca.FusedChain([("flatten", -1)], [src])
+                                          for src in srcs]), args.steps, args.warmup)
+        src = srcs[0]
+        del srcs
         cbytes = 2 * 4 * 4096 * 4096
         gbs = cbytes / (cper.mean() * 1e-3) / 1e9
         out["copy_reference"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(cper.mean(), 4),
