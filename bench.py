@@ -18,7 +18,7 @@ Rank 0 prints ONE JSON line on stdout:
                rocprof FETCH_SIZE / WRITE_SIZE summary in profiles/
   cpu_baseline the CPU restatement of Clove's Rayon kernels (oracle/), four
                unfused passes as Clove's eager CPU path runs them, timed on
-               this host's cores
+               this host's cores; every CPU leg runs after all GPU timings
   parts        the other configurations measured in the same run: the
                broadcast chain, softmax and layer norm (GB/s), 4096^3 and
                skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
@@ -94,6 +94,16 @@ def rotating(launches):
     return run
 
 
+# CPU baseline legs, run after every GPU timing has finished: run in between,
+# they changed the GPU times of the parts timed after them (the cross-entropy
+# steps by up to 4 us).
+CPU_LEGS = []
+
+
+def defer(leg):
+    CPU_LEGS.append(leg)
+
+
 def cpu_time(fn, reps=3):
     best = []
     for _ in range(reps):
@@ -150,15 +160,17 @@ def bench_rows(ca, oracle, args, out):
         part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
                 "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         if not args.no_cpu:
-            rows = 1024  # sample: 1/8 of the rows
-            xs = x.read(0, rows * 4096).reshape(rows, 4096)
-            gh, bh = gam.numpy(), bet.numpy()
-            fn = (lambda: oracle.softmax(xs)) if name == "softmax" else \
-                (lambda: oracle.layer_norm(xs, gh, bh))
-            t = cpu_time(fn) * (8192 / rows)
-            part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": f"{rows} of 8192 rows, scaled"}
+            def leg(name=name, part=part, nbytes=nbytes):
+                rows = 1024  # sample: 1/8 of the rows
+                xs = x.read(0, rows * 4096).reshape(rows, 4096)
+                gh, bh = gam.numpy(), bet.numpy()
+                fn = (lambda: oracle.softmax(xs)) if name == "softmax" else \
+                    (lambda: oracle.layer_norm(xs, gh, bh))
+                t = cpu_time(fn) * (8192 / rows)
+                part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                        "cores": oracle.threads(), "kind": "port",
+                                        "sample": f"{rows} of 8192 rows, scaled"}
+            defer(leg)
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), {per.mean() * 1e3:.1f} us")
 
@@ -175,18 +187,26 @@ def bench_matmul(ca, oracle, args, out):
     part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
     if not args.no_cpu:
-        rows = 128
-        ah = a.read(0, rows * K).reshape(rows, K)
-        bh = b.numpy()
-        # rayon_matmul transposes B once, then computes rows; time both and
-        # scale only the row part to 4096 rows.
-        t_t = cpu_time(lambda: oracle.matmul(ah, bh, rows=(0, 0)), reps=1)
-        t_s = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
-        t = t_t + max(t_s - t_t, 0.0) * (4096 / rows)
-        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                "cores": oracle.threads(), "kind": "port",
-                                "sample": f"{rows} of 4096 output rows plus the B transpose, "
-                                          "row time scaled to 4096"}
+        def leg():
+            rows = 128
+            ah = a.read(0, rows * K).reshape(rows, K)
+            bh = b.numpy()
+            # rayon_matmul transposes B once, then computes rows; time both
+            # and scale only the row part to 4096 rows.
+            t_t = cpu_time(lambda: oracle.matmul(ah, bh, rows=(0, 0)), reps=1)
+            t_s = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
+            t = t_t + max(t_s - t_t, 0.0) * (4096 / rows)
+            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": f"{rows} of 4096 output rows plus the B "
+                                              "transpose, row time scaled to 4096"}
+            ah32 = a32.numpy()
+            t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=1)
+            out["matmul_skinny_32"]["cpu_baseline"] = {
+                "value": round(2.0 * 32 * K * 4096 / t / 1e12, 5), "unit": "TFLOP/s",
+                "cores": oracle.threads(), "kind": "port",
+                "sample": "full 32x4096x4096 product (B transpose included)"}
+        defer(leg)
     out["matmul_4096"] = part
     log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
         f"{per.mean():.3f} ms")
@@ -201,13 +221,6 @@ def bench_matmul(ca, oracle, args, out):
     out["matmul_skinny_32"] = {"value": round(tfs, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
                                "gbs": round(gbs, 1),
                                "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
-    if not args.no_cpu:
-        ah32 = a32.numpy()
-        t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=1)
-        out["matmul_skinny_32"]["cpu_baseline"] = {
-            "value": round(2.0 * 32 * K * 4096 / t / 1e12, 5), "unit": "TFLOP/s",
-            "cores": oracle.threads(), "kind": "port",
-            "sample": "full 32x4096x4096 product (B transpose included)"}
     log(f"matmul 32x4096x4096: {tfs:.2f} TFLOP/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
         f"{per.mean() * 1e3:.1f} us")
 
@@ -230,20 +243,23 @@ def bench_paged(ca, oracle, args, out):
             "gbs": round(gbs, 1), "bytes": nbytes, "context_tokens": int(ctx.sum()),
             "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if not args.no_cpu:
-        seqs = [0, 1, 2, 3]
-        plane, blk = nb * bs * H * D, bs * H * D
-        pool, sbt, scl = workloads.compact_pool(
-            lambda p, b: kv.read(p * plane + b * blk, blk).reshape(bs, H, D), bt, ctx, seqs, bs)
-        qh = q.numpy()[seqs]
-        t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl))
-        t_full = t * ctx.sum() / scl.sum()
-        part["cpu_baseline"] = {"value": round(B / t_full, 2), "unit": "tokens/s",
-                                "cores": oracle.threads(), "kind": "port",
-                                "sample": "4 of 32 sequences (all heads), scaled by context tokens"}
+        def leg():
+            seqs = [0, 1, 2, 3]
+            plane, blk = nb * bs * H * D, bs * H * D
+            pool, sbt, scl = workloads.compact_pool(
+                lambda p, b: kv.read(p * plane + b * blk, blk).reshape(bs, H, D), bt, ctx, seqs,
+                bs)
+            qh = q.numpy()[seqs]
+            t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl))
+            t_full = t * ctx.sum() / scl.sum()
+            part["cpu_baseline"] = {"value": round(B / t_full, 2), "unit": "tokens/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": "4 of 32 sequences (all heads), scaled by context "
+                                              "tokens"}
+        defer(leg)
     out["paged_decode"] = part
     log(f"paged decode: {B / sec:.0f} tokens/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM), "
         f"{per.mean() * 1e3:.1f} us")
-    del kv
 
 
 def bench_mlp(ca, oracle, args, out):
@@ -261,9 +277,11 @@ def bench_mlp(ca, oracle, args, out):
     part = {"value": round(wall * 1e3, 2), "unit": "us/forward (wall, plan of "
             f"{model.num_steps} steps)", "gpu_us": round(per.mean() * 1e3, 2)}
     if not args.no_cpu:
-        t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5)
-        part["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/forward",
-                                "cores": oracle.threads(), "kind": "port", "sample": "full"}
+        def leg():
+            t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5)
+            part["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/forward",
+                                    "cores": oracle.threads(), "kind": "port", "sample": "full"}
+        defer(leg)
     out["mlp_forward"] = part
     log(f"mlp plan: {wall * 1e3:.1f} us/forward wall, {per.mean() * 1e3:.1f} us GPU")
 
@@ -301,7 +319,9 @@ def bench_backward(ca, oracle, args, out):
         part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
                 "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         if oracle is not None:
-            part["cpu_baseline"] = cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes)
+            def leg(name=name, part=part, nbytes=nbytes):
+                part["cpu_baseline"] = cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes)
+            defer(leg)
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
             f"{per.mean() * 1e3:.1f} us")
@@ -322,12 +342,14 @@ def bench_backward(ca, oracle, args, out):
     part = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4), "bytes": nbytes,
             "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if oracle is not None:
-        wh, gh = w.numpy(), gw.numpy()
-        zh = np.zeros(N, np.float32)
-        t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1))
-        part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                "cores": oracle.threads(), "kind": "port",
-                                "sample": "full 16.7M-element parameter, one step"}
+        def leg(part=part, nbytes=nbytes):
+            wh, gh = w.numpy(), gw.numpy()
+            zh = np.zeros(N, np.float32)
+            t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1))
+            part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": "full 16.7M-element parameter, one step"}
+        defer(leg)
     out["adamw_4096x4096"] = part
     log(f"adamw 4096x4096: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
         f"{per.mean() * 1e3:.1f} us")
@@ -347,7 +369,6 @@ def bench_backward(ca, oracle, args, out):
                                "unit": "us/step (wall, 4 tensors, 1 launch)",
                                "gpu_us": round(per.mean() * 1e3, 2)}
     log(f"adamw MLP parameters: {wall * 1e3:.1f} us/step wall")
-    del w, gw, m0, v0
     # matmul backward at 4096^3: grad_a and grad_b, two GEMMs and two transposes
     dc = ca.empty((4096, 4096)).fill_normal(8)
     steps = max(5, args.steps // 10)
@@ -357,14 +378,17 @@ def bench_backward(ca, oracle, args, out):
     part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
     if oracle is not None:
-        rows = 16
-        ah, bh, dch = a.numpy(), b.numpy(), dc.numpy()
-        t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch, da_rows=(0, rows),
-                                                    db_rows=(0, rows)), reps=1)
-        t *= 4096 / rows
-        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                "cores": oracle.threads(), "kind": "port",
-                                "sample": f"{rows} of 4096 rows of grad_a and of grad_b, scaled"}
+        def leg(part=part):
+            rows = 16
+            ah, bh, dch = a.numpy(), b.numpy(), dc.numpy()
+            t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch, da_rows=(0, rows),
+                                                        db_rows=(0, rows)), reps=1)
+            t *= 4096 / rows
+            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": f"{rows} of 4096 rows of grad_a and of grad_b, "
+                                              "scaled"}
+        defer(leg)
     out["matmul_backward_4096"] = part
     log(f"matmul backward 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA "
         f"peak), {per.mean():.3f} ms")
@@ -410,18 +434,21 @@ def bench_attention(ca, oracle, args, out):
     part = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
     if oracle is not None:
-        qh, kh, vh = q.numpy(), k.numpy(), v.numpy()
-        rows = [255 + 256 * i for i in range(16)]  # mean visible keys ~ S/2, as over all rows
-        t_rope = cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(0, 0)), reps=1)
-        t_rows = 0.0
-        for r in rows:
-            t_rows += cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(r, r + 1)), reps=1)
-        t_rows = max(t_rows - len(rows) * t_rope, 0.0)
-        t = t_rope + t_rows * S / len(rows)
-        part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                "cores": oracle.threads(), "kind": "port",
-                                "sample": f"{len(rows)} of {S} query rows (all heads) plus the "
-                                          "full RoPE of q and k, row time scaled"}
+        def leg():
+            qh, kh, vh = q.numpy(), k.numpy(), v.numpy()
+            rows = [255 + 256 * i for i in range(16)]  # mean visible keys ~ S/2, as over all rows
+            t_rope = cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(0, 0)), reps=1)
+            t_rows = 0.0
+            for r in rows:
+                t_rows += cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(r, r + 1)),
+                                   reps=1)
+            t_rows = max(t_rows - len(rows) * t_rope, 0.0)
+            t = t_rope + t_rows * S / len(rows)
+            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
+                                    "cores": oracle.threads(), "kind": "port",
+                                    "sample": f"{len(rows)} of {S} query rows (all heads) plus "
+                                              "the full RoPE of q and k, row time scaled"}
+        defer(leg)
     out["flash_attention_4096"] = part
     log(f"attention prefill S=4096 H=32 D=128 causal+rope: {tf:.1f} TFLOP/s "
         f"({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), {per.mean():.3f} ms")
@@ -435,12 +462,14 @@ def bench_attention(ca, oracle, args, out):
     out["rope"] = {"value": round(gbs, 1), "unit": "GB/s", "ms": round(per.mean(), 4),
                    "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if oracle is not None:
-        rows = 512
-        xs = x.read(0, rows * H * D).reshape(1, rows, H * D)
-        t = cpu_time(lambda: oracle.rope(xs, D), reps=1) * S / rows
-        out["rope"]["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                       "cores": oracle.threads(), "kind": "port",
-                                       "sample": f"{rows} of {S} positions, scaled"}
+        def leg2():
+            rows = 512
+            xs = x.read(0, rows * H * D).reshape(1, rows, H * D)
+            t = cpu_time(lambda: oracle.rope(xs, D), reps=1) * S / rows
+            out["rope"]["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                           "cores": oracle.threads(), "kind": "port",
+                                           "sample": f"{rows} of {S} positions, scaled"}
+        defer(leg2)
     log(f"rope [4096, 4096]: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), {per.mean() * 1e3:.1f} us")
 
 
@@ -450,15 +479,15 @@ def bench_attention(ca, oracle, args, out):
 PART_KERNELS = {
     "copy_reference": ["clove_chain_flatten_b0"],
     "chain_broadcast": ["clove_chain_mul_add_gelu_mul_b0020"],
-    "softmax": ["softmax_wave_kernel<16>"],
+    "softmax": ["softmax_block_kernel<2>"],
     "layer_norm": ["layer_norm_wave_kernel<16>"],
     "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 8>", "gemm_splitk_reduce"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
-    "softmax_backward": ["softmax_bw_wave_kernel<16>"],
+    "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
     "broadcast_grad": ["bcast_grad_cols4_kernel", "bcast_grad_final_kernel"],
-    "cross_entropy": ["cross_entropy_wave_kernel<16, 0>", "ordered_sum_kernel"],
-    "cross_entropy_backward": ["cross_entropy_wave_kernel<16, 1>"],
+    "cross_entropy": ["cross_entropy_block_kernel<2, 0>", "ordered_sum_kernel"],
+    "cross_entropy_backward": ["cross_entropy_block_kernel<2, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
     "mse_backward": ["mse_backward_kernel<true>"],
     "rope": ["rope_rows_kernel"],
@@ -541,14 +570,14 @@ def main():
         "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s", traffic),
     }
     if oracle is not None:
-        host = [ins[i].numpy() for i in range(4)]
-        t = cpu_time(cpu_chain(oracle, host))
-        result["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                  "cores": oracle.threads(), "kind": "port",
-                                  "sample": "full config 2 workload, 4 unfused passes "
-                                            "(Clove's eager CPU path), median of 3"}
-        del host
-    del ins
+        def leg():
+            host = [ins[i].numpy() for i in range(4)]
+            t = cpu_time(cpu_chain(oracle, host))
+            result["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
+                                      "cores": oracle.threads(), "kind": "port",
+                                      "sample": "full config 2 workload, 4 unfused passes "
+                                                "(Clove's eager CPU path), median of 3"}
+        defer(leg)
 
     out = {}
     if "copy" in parts:
@@ -587,6 +616,10 @@ def main():
         bench_backward(ca, oracle, args, out)
     if "attention" in parts:
         bench_attention(ca, oracle, args, out)
+    ca.synchronize()
+    for leg in CPU_LEGS:
+        leg()
+    CPU_LEGS.clear()
     if out:
         add_part_traffic(out, args.traffic)
         result["parts"] = out

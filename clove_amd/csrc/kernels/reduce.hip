@@ -101,13 +101,15 @@ __global__ void __launch_bounds__(256) bcast_grad_flat_kernel(const float *__res
 
 // gb[j] = sign * sum over chunks of part[chunk][j].  A workgroup covers 32
 // columns with 8 groups of threads; group k sums chunks [k*per, (k+1)*per)
-// in order (loads issued eight at a time), and the 8 group sums meet in LDS
-// and are added in group order: a fixed order, so the result is
-// deterministic, with 8x the parallelism of one thread per column.
+// in order, and the 8 group sums meet in LDS and are added in group order: a
+// fixed order, so the result is deterministic, with 8x the parallelism of
+// one thread per column.  A group's loads go out 16 at a time before any is
+// added (each load-then-add would cost a memory round trip).
 __global__ void __launch_bounds__(256) bcast_grad_final_kernel(const float *__restrict__ part,
                                                                uint64_t chunks, uint64_t nb,
                                                                float sign,
                                                                float *__restrict__ gb) {
+    constexpr int kBatch = 16;
     __shared__ float grp[8][32];
     const int cl = threadIdx.x & 31, k = threadIdx.x >> 5;
     const uint64_t j = (uint64_t)blockIdx.x * 32 + cl;
@@ -116,15 +118,15 @@ __global__ void __launch_bounds__(256) bcast_grad_final_kernel(const float *__re
     const uint64_t c1 = c0 + per < chunks ? c0 + per : chunks;
     float s = 0.0f;
     if (j < nb) {
-        uint64_t c = c0;
-        for (; c + 8 <= c1; c += 8) {
-            float v[8];
+        for (uint64_t c = c0; c < c1; c += kBatch) {
+            float v[kBatch];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = part[(c + u) * nb + j];
+            for (int u = 0; u < kBatch; ++u)
+                if (c + u < c1) v[u] = part[(c + u) * nb + j];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) s += v[u];
+            for (int u = 0; u < kBatch; ++u)
+                if (c + u < c1) s += v[u];
         }
-        for (; c < c1; ++c) s += part[c * nb + j];
     }
     grp[k][cl] = s;
     __syncthreads();
@@ -178,26 +180,38 @@ __global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float *__res
 }
 
 // out[0] = (sign * sum of x[0..n)) / div, one workgroup, fixed order.
-// Thread t sums x[t], x[t + 256], ... with eight loads in flight (a single
-// workgroup has nothing else to hide its load latency behind).
-__global__ void __launch_bounds__(256) ordered_sum_kernel(const float *__restrict__ x, uint64_t n,
-                                                          float sign, float div,
-                                                          float *__restrict__ out) {
-    __shared__ float wsum[4];
+// Thread t sums x[t], x[t + 1024], ... in order; the 16 wave sums are added
+// in wave order.  A single workgroup has nothing else to hide its load
+// latency behind, so each thread's loads go out eight at a time before any
+// is added: up to 8192 values cost one memory round trip.
+constexpr int kSumThreads = 1024;
+__global__ void __launch_bounds__(kSumThreads) ordered_sum_kernel(const float *__restrict__ x,
+                                                                  uint64_t n, float sign,
+                                                                  float div,
+                                                                  float *__restrict__ out) {
+    constexpr int kBatch = 8, kWaves = kSumThreads / 64;
+    __shared__ float wsum[kWaves];
     float s = 0.0f;
-    uint64_t i = threadIdx.x;
-    for (; i + 7 * 256 < n; i += 8 * 256) {
-        float v[8];
+    for (uint64_t base = threadIdx.x; base < n; base += (uint64_t)kBatch * kSumThreads) {
+        float v[kBatch];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = x[i + u * 256];
+        for (int u = 0; u < kBatch; ++u) {
+            const uint64_t i = base + (uint64_t)u * kSumThreads;
+            if (i < n) v[u] = x[i];
+        }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
+        for (int u = 0; u < kBatch; ++u)
+            if (base + (uint64_t)u * kSumThreads < n) s += v[u];
     }
-    for (; i < n; i += 256) s += x[i];
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) out[0] = (sign * ((wsum[0] + wsum[1]) + (wsum[2] + wsum[3]))) / div;
+    if (threadIdx.x == 0) {
+        float t = wsum[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) t += wsum[w];
+        out[0] = (sign * t) / div;
+    }
 }
 
 // x / y correctly rounded, for a y shared by many x, from r = 1 / y (IEEE):
@@ -317,11 +331,11 @@ void mse_loss(const float *p, const float *t, size_t n, float *part, float *out,
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t)) & 15) == 0;
     if (blocks && vec) sq_diff_partial_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
     else if (blocks) sq_diff_partial_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
-    ordered_sum_kernel<<<1, 256, 0, s>>>(part, blocks, 1.0f, (float)n, out);
+    ordered_sum_kernel<<<1, kSumThreads, 0, s>>>(part, blocks, 1.0f, (float)n, out);
 }
 
 void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hipStream_t s) {
-    ordered_sum_kernel<<<1, 256, 0, s>>>(x, n, sign, div, out);
+    ordered_sum_kernel<<<1, kSumThreads, 0, s>>>(x, n, sign, div, out);
 }
 
 void mse_backward(const float *p, const float *t, size_t n, const float *grad_loss, float *grad,

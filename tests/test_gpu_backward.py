@@ -182,6 +182,31 @@ def test_cross_entropy(hip, rows, cols):
     assert_close(grad, wg, 1e-4, 1e-4 * 1.5 / rows * 1e-2, f"ce backward {rows}x{cols}")
 
 
+@pytest.mark.parametrize("cols", [1028, 2052, 4100, 8196, 12000, 32768, 32772])
+def test_wide_rows_backward_and_losses(hip, cols):
+    """Widths that take the one-workgroup-per-row kernels (every vectors-per-
+    thread variant) and one past them.  The targets sit in the row's first
+    and last columns and in every thread slot, so l[target] is fetched from
+    each position it can occupy."""
+    g = rng(cols + 3)
+    slots = [4 * 512 * k + 5 for k in range(16) if 4 * 512 * k + 5 < cols]
+    t = np.array([0, cols - 1] + slots, np.float32)
+    rows = len(t)
+    logits = g.normal(0, 3, (rows, cols)).astype(np.float32)
+    tl, tt = hip.tensor(logits), hip.tensor(t)
+    loss = hip.cross_entropy(tl, tt).numpy()[0, 0]
+    want = oracle.cross_entropy(logits, t)[0, 0]
+    assert abs(loss - want) <= 1e-4 * abs(want) + 1e-7, (loss, want)
+    gl = hip.tensor(np.array([1.5], np.float32))
+    grad = hip.cross_entropy_backward(tl, tt, gl).numpy()
+    wg = oracle.cross_entropy_backward(logits, t, 1.5)
+    assert_close(grad, wg, 1e-4, 1e-4 * 1.5 / rows * 1e-2, f"ce backward {rows}x{cols}")
+    y = oracle.softmax(g.normal(0, 2, (3, cols)).astype(np.float32))
+    dy = g.standard_normal((3, cols)).astype(np.float32)
+    got = hip.softmax_backward(hip.tensor(y), hip.tensor(dy)).numpy()
+    softmax_bw_check(got, y, dy, f"softmax backward 3x{cols}")
+
+
 def test_cross_entropy_config3_full(hip):
     g = rng(2)
     logits = g.normal(0, 2, (8192, 4096)).astype(np.float32)

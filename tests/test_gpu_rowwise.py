@@ -37,6 +37,24 @@ def test_layer_norm(hip, shape):
     assert_close(got.numpy(), oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm {shape}")
 
 
+# Rows wider than 1024 columns (width a multiple of 4) take one workgroup of
+# 512 threads per row with P = 1..16 vectors per thread; these widths hit
+# every P, the edges between them and the widths either side of the switch.
+WIDE = [1024, 1028, 2048, 2052, 4100, 8192, 8196, 12000, 16384, 32768, 32772]
+
+
+@pytest.mark.parametrize("cols", WIDE)
+def test_wide_rows(hip, cols):
+    g = rng(cols)
+    x = g.normal(0, 2, (3, cols)).astype(np.float32)
+    assert_close(hip.softmax(hip.tensor(x)).numpy(), oracle.softmax(x), 1e-4, 1e-9,
+                 f"softmax 3x{cols}")
+    gam = g.uniform(0.5, 1.5, cols).astype(np.float32)
+    bet = g.uniform(-0.1, 0.1, cols).astype(np.float32)
+    got = hip.layer_norm(hip.tensor(x), hip.tensor(gam), hip.tensor(bet)).numpy()
+    assert_close(got, oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm 3x{cols}")
+
+
 def test_config3_full(hip):
     """Config 3: [8192, 4096] normal(0, 2), seed 2; gamma U[0.5, 1.5],
     beta U[-0.1, 0.1]."""
