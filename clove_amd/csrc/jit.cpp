@@ -50,15 +50,21 @@ struct Compiled {
 std::unordered_map<std::string, Compiled> g_cache;
 
 // Launch-geometry knobs for tuning sweeps: CLOVE_CHAIN_UNROLL (vectors per
-// thread per iteration, default 4) and CLOVE_CHAIN_BLOCKS_PER_CU (grid cap,
-// default 32).  They change scheduling only, never the result.
+// thread per input per iteration, default 1), CLOVE_CHAIN_BLOCK (threads per
+// block, 64-1024 in steps of 64, default 512) and CLOVE_CHAIN_BLOCKS_PER_CU
+// (grid cap, default 32).  They change scheduling only, never the result.
+// The defaults were the fastest of a sweep with inputs cycled so the
+// last-level cache held none of them (config 2's chain): 512 x 1 gave 77.3%
+// of HBM peak, 256 x 4 74.7%, 256 x 1 76.4%, 512 x 2 76.3%, 512 x 4 71.7%,
+// 1024 x 1 77.3% (but 74.1% on the broadcast chain, against 78.4%).
 int env_int(const char *name, int dflt, int lo, int hi) {
     const char *v = std::getenv(name);
     if (!v || !*v) return dflt;
     const int x = std::atoi(v);
     return x < lo ? lo : (x > hi ? hi : x);
 }
-int chain_unroll() { return env_int("CLOVE_CHAIN_UNROLL", 4, 1, 16); }
+int chain_unroll() { return env_int("CLOVE_CHAIN_UNROLL", 1, 1, 16); }
+int chain_block() { return (env_int("CLOVE_CHAIN_BLOCK", 512, 64, 1024) / 64) * 64; }
 int chain_blocks_per_cu() { return env_int("CLOVE_CHAIN_BLOCKS_PER_CU", 32, 1, 1024); }
 
 const char *op_fn(int opcode) {
@@ -118,11 +124,12 @@ std::string operand_expr(int src) {
 }
 
 std::string generate(const std::vector<ChainOp> &ops, const std::vector<int> &modes, bool wide,
-                     int nout, const std::string &name, int unroll) {
+                     int nout, const std::string &name, int unroll, int block) {
     std::ostringstream s;
     const int nin = (int)modes.size();
     s << "#define CL_NIN " << nin << "\n#define CL_NOUT " << nout << "\n";
     s << "#define CL_KERNEL_NAME " << name << "\n#define CL_UNROLL " << unroll << "\n";
+    s << "#define CL_BLOCK " << block << "\n";
     s << "#include \"ew_device.h\"\n";
     s << "__device__ __forceinline__ void cl_load_all(const cl_chain_args &a, unsigned long long v, cl_f4 *x) {\n";
     for (int k = 0; k < nin; ++k)
@@ -170,7 +177,7 @@ std::string signature(const std::vector<ChainOp> &ops, const std::vector<int> &m
     s << "|m";
     for (int m : modes) s << m;
     s << (wide ? "|w" : "|n");
-    s << "|u" << chain_unroll();
+    s << "|u" << chain_unroll() << "|t" << chain_block();
     return s.str();
 }
 
@@ -303,21 +310,24 @@ void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *
     auto it = g_cache.find(sig);
     if (it == g_cache.end()) {
         const std::string name = kernel_name(ops, modes);
-        Compiled comp = compile(generate(ops, modes, wide, nstore, name, chain_unroll()), name);
+        Compiled comp = compile(
+            generate(ops, modes, wide, nstore, name, chain_unroll(), chain_block()), name);
         it = g_cache.emplace(sig, comp).first;
     }
 
-    // Grid: enough 256-thread blocks to cover the vectors once at the
-    // chain's unroll, capped at a number of blocks per CU (a grid-stride loop
-    // covers the rest).
-    const uint64_t per_block = 256ull * chain_unroll();
+    // Grid: enough blocks to cover the vectors once at the chain's unroll,
+    // capped at a number of blocks per CU (a grid-stride loop covers the
+    // rest).
+    const uint64_t threads = (uint64_t)chain_block();
+    const uint64_t per_block = threads * chain_unroll();
     uint64_t blocks = (args.nvec + per_block - 1) / per_block;
-    if (blocks == 0) blocks = (numel + 255) / 256;
+    if (blocks == 0) blocks = (numel + threads - 1) / threads;
     const uint64_t cap = (uint64_t)c.num_cus * chain_blocks_per_cu();
     if (blocks > cap) blocks = cap;
     if (blocks == 0) blocks = 1;
     void *params[] = {&args};
-    CLOVE_HIP_CHECK(hipModuleLaunchKernel(it->second.fn, (unsigned)blocks, 1, 1, 256, 1, 1, 0,
+    CLOVE_HIP_CHECK(hipModuleLaunchKernel(it->second.fn, (unsigned)blocks, 1, 1, (unsigned)threads,
+                                          1, 1, 0,
                                           c.stream, params, nullptr));
 }
 

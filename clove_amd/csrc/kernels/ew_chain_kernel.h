@@ -9,12 +9,16 @@
 // Each thread streams CL_UNROLL 16-byte vectors per input per iteration
 // (all loads issued before any arithmetic), walking the index space with a
 // grid stride; a scalar loop finishes the elements past the last full vector.
+// CL_BLOCK and CL_UNROLL come from the generator (512 threads, one vector:
+// a block covers 8 KiB of each input, read by eight waves at once).
 #pragma once
 
 #ifndef CL_UNROLL
 #define CL_UNROLL 4
 #endif
+#ifndef CL_BLOCK
 #define CL_BLOCK 256
+#endif
 
 extern "C" __global__ void __launch_bounds__(CL_BLOCK) CL_KERNEL_NAME(cl_chain_args a) {
     const unsigned long long nvec = a.nvec;
