@@ -140,33 +140,44 @@ __global__ void __launch_bounds__(256) bcast_grad_final_kernel(const float *__re
 
 // ---- scalar losses ------------------------------------------------------
 
-// Sum of squared differences over a chunk of CHUNK elements per workgroup,
-// combined in a fixed order: part[block].
-// VEC: 16-byte loads (p and t 16-byte aligned); the chunk's tail past n is
-// read element by element.
-constexpr int kSqChunk = 256 * 64;
+// Sum of squared differences over a chunk of kSqChunk elements per
+// workgroup of kSqThreads threads, combined in a fixed order: part[block].
+// VEC: 16-byte loads (p and t 16-byte aligned), kSqChunk / (4 kSqThreads)
+// vectors of each input per thread, all issued before any arithmetic; a
+// chunk reaching past n is read element by element.  16 KiB of each input
+// per 512-thread workgroup streamed fastest among the shapes measured with
+// inputs the last-level cache does not hold (a 64 KiB chunk per 256 threads
+// read 2-4 points of HBM peak slower).
+constexpr int kSqThreads = 512;
+constexpr int kSqChunk = kSqThreads * 8;
 template <bool VEC>
-__global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float *__restrict__ p,
-                                                              const float *__restrict__ t,
-                                                              uint64_t n,
-                                                              float *__restrict__ part) {
-    __shared__ float wsum[4];
+__global__ void __launch_bounds__(kSqThreads) sq_diff_partial_kernel(const float *__restrict__ p,
+                                                                    const float *__restrict__ t,
+                                                                    uint64_t n,
+                                                                    float *__restrict__ part) {
+    constexpr int kWaves = kSqThreads / 64, kVec = kSqChunk / (4 * kSqThreads);
+    __shared__ float wsum[kWaves];
     const uint64_t base = (uint64_t)blockIdx.x * kSqChunk;
     float s = 0.0f;
     if (VEC && base + kSqChunk <= n) {
         const cl_f4 *p4 = reinterpret_cast<const cl_f4 *>(p + base);
         const cl_f4 *t4 = reinterpret_cast<const cl_f4 *>(t + base);
+        cl_f4 vp[kVec], vt[kVec];
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+            vp[k] = __builtin_nontemporal_load(p4 + k * kSqThreads + threadIdx.x);
+            vt[k] = __builtin_nontemporal_load(t4 + k * kSqThreads + threadIdx.x);
+        }
         cl_f4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-        for (int k = 0; k < kSqChunk / 1024; ++k) {
-            const cl_f4 d = __builtin_nontemporal_load(p4 + k * 256 + threadIdx.x) -
-                            __builtin_nontemporal_load(t4 + k * 256 + threadIdx.x);
+#pragma unroll
+        for (int k = 0; k < kVec; ++k) {
+            const cl_f4 d = vp[k] - vt[k];
             acc += d * d;
         }
         s = hsum4(acc);
     } else {
-        for (int k = 0; k < kSqChunk / 256; ++k) {
-            const uint64_t i = base + (uint64_t)k * 256 + threadIdx.x;
+        for (int k = 0; k < kSqChunk / kSqThreads; ++k) {
+            const uint64_t i = base + (uint64_t)k * kSqThreads + threadIdx.x;
             if (i < n) {
                 const float d = p[i] - t[i];
                 s += d * d;
@@ -176,7 +187,12 @@ __global__ void __launch_bounds__(256) sq_diff_partial_kernel(const float *__res
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = s;
     __syncthreads();
-    if (threadIdx.x == 0) part[blockIdx.x] = (wsum[0] + wsum[1]) + (wsum[2] + wsum[3]);
+    if (threadIdx.x == 0) {
+        float r = wsum[0];
+#pragma unroll
+        for (int w = 1; w < kWaves; ++w) r += wsum[w];
+        part[blockIdx.x] = r;
+    }
 }
 
 // out[0] = (sign * sum of x[0..n)) / div, one workgroup, fixed order.
@@ -228,8 +244,9 @@ __device__ __forceinline__ float div_exact(float x, float y, float r) {
 // MSE backward (backend.rs:2780-2790): grad = 2 * (p - t) * g / n, each
 // step rounded in that order.  VEC: 16-byte streaming loads and stores over
 // the whole vectors (p, t, grad 16-byte aligned), the tail element by element.
+constexpr int kMseBwThreads = 512;
 template <bool VEC>
-__global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restrict__ p,
+__global__ void __launch_bounds__(kMseBwThreads) mse_backward_kernel(const float *__restrict__ p,
                                                            const float *__restrict__ t,
                                                            uint64_t n,
                                                            const float *__restrict__ grad_loss,
@@ -237,14 +254,15 @@ __global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restri
     const float g = grad_loss[0];
     const float nf = (float)n;
     const float rn = 1.0f / nf;
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    const uint64_t stride = (uint64_t)gridDim.x * kMseBwThreads;
     uint64_t tail = 0;
     if (VEC) {
         const uint64_t nv = n / 4;
         const cl_f4 *p4 = reinterpret_cast<const cl_f4 *>(p);
         const cl_f4 *t4 = reinterpret_cast<const cl_f4 *>(t);
         cl_f4 *g4 = reinterpret_cast<cl_f4 *>(grad);
-        for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nv; i += stride) {
+        for (uint64_t i = (uint64_t)blockIdx.x * kMseBwThreads + threadIdx.x; i < nv;
+             i += stride) {
             const cl_f4 d = __builtin_nontemporal_load(p4 + i) - __builtin_nontemporal_load(t4 + i);
             const cl_f4 x = 2.0f * d * g;
             __builtin_nontemporal_store((cl_f4){div_exact(x.x, nf, rn), div_exact(x.y, nf, rn),
@@ -253,7 +271,8 @@ __global__ void __launch_bounds__(256) mse_backward_kernel(const float *__restri
         }
         tail = 4 * nv;
     }
-    for (uint64_t i = tail + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride)
+    for (uint64_t i = tail + (uint64_t)blockIdx.x * kMseBwThreads + threadIdx.x; i < n;
+         i += stride)
         grad[i] = div_exact(2.0f * (p[i] - t[i]) * g, nf, rn);
 }
 
@@ -329,8 +348,10 @@ size_t sq_diff_workspace(size_t n) { return (n + kSqChunk - 1) / kSqChunk; }
 void mse_loss(const float *p, const float *t, size_t n, float *part, float *out, hipStream_t s) {
     const size_t blocks = sq_diff_workspace(n);
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t)) & 15) == 0;
-    if (blocks && vec) sq_diff_partial_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
-    else if (blocks) sq_diff_partial_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, part);
+    if (blocks && vec)
+        sq_diff_partial_kernel<true><<<(unsigned)blocks, kSqThreads, 0, s>>>(p, t, n, part);
+    else if (blocks)
+        sq_diff_partial_kernel<false><<<(unsigned)blocks, kSqThreads, 0, s>>>(p, t, n, part);
     ordered_sum_kernel<<<1, kSumThreads, 0, s>>>(part, blocks, 1.0f, (float)n, out);
 }
 
@@ -343,13 +364,15 @@ void mse_backward(const float *p, const float *t, size_t n, const float *grad_lo
     if (!n) return;
     const bool vec = ((reinterpret_cast<uintptr_t>(p) | reinterpret_cast<uintptr_t>(t) |
                        reinterpret_cast<uintptr_t>(grad)) & 15) == 0;
-    // vectors per thread per pass: a grid of up to 8192 workgroups, the
-    // streaming kernels' shape
-    size_t blocks = ((vec ? n / 4 : n) + 255) / 256;
+    // one vector per thread per pass, 512-thread workgroups (the fused
+    // chains' shape), a grid of up to 8192 workgroups
+    size_t blocks = ((vec ? n / 4 : n) + kMseBwThreads - 1) / kMseBwThreads;
     if (blocks > 8192) blocks = 8192;
     if (blocks == 0) blocks = 1;
-    if (vec) mse_backward_kernel<true><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
-    else mse_backward_kernel<false><<<(unsigned)blocks, 256, 0, s>>>(p, t, n, grad_loss, grad);
+    if (vec)
+        mse_backward_kernel<true><<<(unsigned)blocks, kMseBwThreads, 0, s>>>(p, t, n, grad_loss, grad);
+    else
+        mse_backward_kernel<false><<<(unsigned)blocks, kMseBwThreads, 0, s>>>(p, t, n, grad_loss, grad);
 }
 
 void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s) {
