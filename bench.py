@@ -490,7 +490,7 @@ PART_KERNELS = {
     "cross_entropy_backward": ["cross_entropy_block_kernel<2, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
     "mse_backward": ["mse_backward_kernel<true>"],
-    "rope": ["rope_rows_kernel"],
+    "rope": ["rope_rows_kernel<true>"],
 }
 
 

@@ -307,14 +307,24 @@ __global__ void __launch_bounds__(256) rope_table_kernel(float2 *__restrict__ ta
 
 // backend.rs:2797-2826: x1' = x1 cos - x2 sin, x2' = x1 sin + x2 cos per pair
 // of every whole head; dims past the last whole head are written as 0.
-// One workgroup per row (grid-stride over rows): the row's position and its
-// table row are computed once, each thread then rotates 16-byte vectors
-// (two pairs), issuing up to four vector loads before any arithmetic.
-__global__ void __launch_bounds__(256) rope_rows_kernel(const float *__restrict__ x,
-                                                        float *__restrict__ out, uint64_t rows,
-                                                        int seq, int hidden, int head_dim,
-                                                        int pos_offset, const float2 *tab,
-                                                        int tab_pos0) {
+// One workgroup of kRopeThreads threads per row (grid-stride over rows): the
+// row's position and its table row are computed once, each thread then
+// rotates 16-byte vectors (two pairs), issuing up to kRopeVec vector loads
+// before any arithmetic.  512 threads x 2 vectors (a 4096-float row in one
+// pass) streamed faster than 256 x 4 with inputs the last-level cache does
+// not hold.
+constexpr int kRopeThreads = 512, kRopeVec = 2;
+// HD4 (head_dim % 4 == 0): a vector's two pairs are table entries 2m and
+// 2m + 1 of one row, adjacent and 16-byte aligned, fetched with one 16-byte
+// load issued with the row's loads; the whole-head bound then covers both
+// pairs of a vector alike.
+template <bool HD4>
+__global__ void __launch_bounds__(kRopeThreads) rope_rows_kernel(const float *__restrict__ x,
+                                                                 float *__restrict__ out,
+                                                                 uint64_t rows, int seq,
+                                                                 int hidden, int head_dim,
+                                                                 int pos_offset, const float2 *tab,
+                                                                 int tab_pos0) {
 #pragma clang fp contract(off)
     const int nv = hidden / 4;
     const int pairs = head_dim / 2;
@@ -324,29 +334,41 @@ __global__ void __launch_bounds__(256) rope_rows_kernel(const float *__restrict_
         const float2 *trow = tab + (size_t)p * pairs;
         const float *xr = x + r * (uint64_t)hidden;
         float *orow = out + r * (uint64_t)hidden;
-        for (int v0 = threadIdx.x; v0 < nv; v0 += 4 * 256) {
-            cl_f4 xv[4];
+        for (int v0 = threadIdx.x; v0 < nv; v0 += kRopeVec * kRopeThreads) {
+            cl_f4 xv[kRopeVec], tv[kRopeVec];
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int v = v0 + 256 * u;
-                if (v < nv)
+            for (int u = 0; u < kRopeVec; ++u) {
+                const int v = v0 + kRopeThreads * u;
+                if (v < nv) {
                     xv[u] = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(xr) + v);
+                    if (HD4 && 4 * v < whole)
+                        tv[u] = *reinterpret_cast<const cl_f4 *>(trow + ((4 * v) % head_dim) / 2);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int v = v0 + 256 * u;
+            for (int u = 0; u < kRopeVec; ++u) {
+                const int v = v0 + kRopeThreads * u;
                 if (v >= nv) continue;
                 const int c0 = 4 * v;
                 cl_f4 o = {0.f, 0.f, 0.f, 0.f};
-                if (c0 < whole) {
-                    const float2 t0 = trow[(c0 % head_dim) / 2];
-                    o.x = xv[u].x * t0.x - xv[u].y * t0.y;
-                    o.y = xv[u].x * t0.y + xv[u].y * t0.x;
-                }
-                if (c0 + 2 < whole) {
-                    const float2 t1 = trow[((c0 + 2) % head_dim) / 2];
-                    o.z = xv[u].z * t1.x - xv[u].w * t1.y;
-                    o.w = xv[u].z * t1.y + xv[u].w * t1.x;
+                if (HD4) {
+                    if (c0 < whole) {
+                        o.x = xv[u].x * tv[u].x - xv[u].y * tv[u].y;
+                        o.y = xv[u].x * tv[u].y + xv[u].y * tv[u].x;
+                        o.z = xv[u].z * tv[u].z - xv[u].w * tv[u].w;
+                        o.w = xv[u].z * tv[u].w + xv[u].w * tv[u].z;
+                    }
+                } else {
+                    if (c0 < whole) {
+                        const float2 t0 = trow[(c0 % head_dim) / 2];
+                        o.x = xv[u].x * t0.x - xv[u].y * t0.y;
+                        o.y = xv[u].x * t0.y + xv[u].y * t0.x;
+                    }
+                    if (c0 + 2 < whole) {
+                        const float2 t1 = trow[((c0 + 2) % head_dim) / 2];
+                        o.z = xv[u].z * t1.x - xv[u].w * t1.y;
+                        o.w = xv[u].z * t1.y + xv[u].w * t1.x;
+                    }
                 }
                 __builtin_nontemporal_store(o, reinterpret_cast<cl_f4 *>(orow) + v);
             }
@@ -418,9 +440,12 @@ void rope_apply(const float *x, float *out, size_t rows, int seq, int hidden, in
     // one workgroup per row, at most 64 per CU's worth of rows in flight
     const unsigned grid = (unsigned)(rows < 16384 ? rows : 16384);
     const float2 *t = reinterpret_cast<const float2 *>(tab);
-    if (vec)
-        rope_rows_kernel<<<grid, 256, 0, s>>>(x, out, rows, seq, hidden, head_dim, pos_offset, t,
-                                              tab_pos0);
+    if (vec && head_dim % 4 == 0)
+        rope_rows_kernel<true><<<grid, kRopeThreads, 0, s>>>(x, out, rows, seq, hidden, head_dim,
+                                                             pos_offset, t, tab_pos0);
+    else if (vec)
+        rope_rows_kernel<false><<<grid, kRopeThreads, 0, s>>>(x, out, rows, seq, hidden, head_dim,
+                                                              pos_offset, t, tab_pos0);
     else
         rope_pairs_kernel<<<grid, 256, 0, s>>>(x, out, rows, seq, hidden, head_dim, pos_offset, t,
                                                tab_pos0);

@@ -15,7 +15,12 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("shape,head_dim,pos", [((2, 50, 64), 16, 7), ((10, 128), 128, 0),
-                                                ((3, 5, 20), 8, 3), ((1, 4096, 128), 128, 0)])
+                                                ((3, 5, 20), 8, 3), ((1, 4096, 128), 128, 0),
+                                                # head_dim % 4 != 0 with 16-byte rows (the
+                                                # two-entry table path), and with odd-sized
+                                                # rows (the pair-at-a-time kernel)
+                                                ((3, 7, 12), 6, 5), ((2, 9, 30), 10, 2),
+                                                ((2, 3, 44), 6, 1)])
 def test_rope(hip, shape, head_dim, pos):
     x = rng(sum(shape)).standard_normal(shape).astype(np.float32)
     got = hip.rope(hip.tensor(x), head_dim, pos).numpy()
