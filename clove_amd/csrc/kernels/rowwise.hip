@@ -393,8 +393,10 @@ __global__ void __launch_bounds__(256) cross_entropy_loop_kernel(
 // stay deterministic.  Per element the arithmetic is the wave kernels'.
 // Layer norm keeps one wave per row: with a row per workgroup every row
 // reads gamma and beta (twice the row's bytes) from the L2, and it measured
-// 65-71% (one to four rows per workgroup) against the wave kernel's 75%,
-// which stages them in LDS once per four rows.
+// 65-71% (one to four rows per workgroup, all loaded at once) and 63-69%
+// (4-16 rows walked in order, gamma and beta in registers, the next row
+// prefetched) against the wave kernel's 75%, which stages them in LDS once
+// per four rows.
 constexpr int kBlockThreads = 512;
 constexpr int kBlockWaves = kBlockThreads / 64;
 
