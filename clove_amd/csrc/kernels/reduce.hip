@@ -40,38 +40,61 @@ __global__ void __launch_bounds__(256) bcast_grad_cols_kernel(const float *__res
 }
 
 // The same with four consecutive columns per thread and 16-byte loads
-// (nb % 4 == 0, g 16-byte aligned); each column is still summed in row
-// order.  The row loop is unrolled so sixteen loads are in flight.
-__global__ void __launch_bounds__(256) bcast_grad_cols4_kernel(const float *__restrict__ g,
-                                                               uint64_t n, uint64_t nb,
-                                                               uint64_t rows_per,
-                                                               float *__restrict__ part) {
-    const uint64_t q = (uint64_t)blockIdx.x * 256 + threadIdx.x;  // column quad
+// (nb % 4 == 0, g 16-byte aligned).  A workgroup of 512 threads covers
+// kColQuads column quads (512 columns) of one chunk of rows: thread
+// (q, r) = (tid % kColQuads, tid / kColQuads) sums its quad over rows r,
+// r + kColGroups, ... of the chunk, kColBatch loads at a time, and the
+// kColGroups row groups are then added in group order through LDS (a fixed
+// order: deterministic).  1024 workgroups at 4096 x 4096, each thread's
+// eight loads in flight at once; 256-thread workgroups of 256 columns with
+// sixteen loads per batch gave half the workgroups.
+constexpr int kColThreads = 512, kColQuads = 128, kColGroups = kColThreads / kColQuads;
+constexpr int kColBatch = 8;
+__global__ void __launch_bounds__(kColThreads) bcast_grad_cols4_kernel(const float *__restrict__ g,
+                                                                       uint64_t n, uint64_t nb,
+                                                                       uint64_t rows_per,
+                                                                       float *__restrict__ part) {
+    __shared__ cl_f4 grp_sum[kColGroups - 1][kColQuads];
+    const int ql = threadIdx.x % kColQuads, grp = threadIdx.x / kColQuads;
     const uint64_t nq = nb / 4;
-    if (q >= nq) return;
+    const uint64_t q = (uint64_t)blockIdx.x * kColQuads + ql;
+    const bool live = q < nq;
     const uint64_t r0 = (uint64_t)blockIdx.y * rows_per;
     const uint64_t rows = (n + nb - 1) / nb;
     const uint64_t r1 = r0 + rows_per < rows ? r0 + rows_per : rows;
+    const uint64_t full = n / nb;  // rows wholly inside n
+    const uint64_t r_full = r1 < full ? r1 : full;
     const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(g);
     cl_f4 s = {0.f, 0.f, 0.f, 0.f};
-    uint64_t r = r0;
-    // full rows only in the unrolled part (n % nb == 0 for all but the last)
-    const uint64_t full = n / nb;
-    const uint64_t r_full = r1 < full ? r1 : full;
-    for (; r + 16 <= r_full; r += 16) {
-        cl_f4 v[16];
+    if (live) {
+        uint64_t r = r0 + grp;
+        for (; r + (uint64_t)(kColBatch - 1) * kColGroups < r_full;
+             r += (uint64_t)kColBatch * kColGroups) {
+            cl_f4 v[kColBatch];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) v[u] = __builtin_nontemporal_load(g4 + (r + u) * nq + q);
+            for (int u = 0; u < kColBatch; ++u)
+                v[u] = __builtin_nontemporal_load(g4 + (r + (uint64_t)u * kColGroups) * nq + q);
 #pragma unroll
-        for (int u = 0; u < 16; ++u) s += v[u];
+            for (int u = 0; u < kColBatch; ++u) s += v[u];
+        }
+        for (; r < r1; r += kColGroups) {
+            if (r < full) {
+                s += __builtin_nontemporal_load(g4 + r * nq + q);
+            } else {  // the last, partial row
+                const uint64_t i = r * nb + 4 * q;
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    if (i + c < n) s[c] += g[i + c];
+            }
+        }
     }
-    for (; r < r1; ++r) {
-        const uint64_t i = r * nb + 4 * q;
+    if (grp > 0) grp_sum[grp - 1][ql] = s;
+    __syncthreads();
+    if (grp == 0 && live) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-            if (i + c < n) s[c] += g[i + c];
+        for (int k = 0; k < kColGroups - 1; ++k) s += grp_sum[k][ql];
+        *reinterpret_cast<cl_f4 *>(part + (uint64_t)blockIdx.y * nb + 4 * q) = s;
     }
-    *reinterpret_cast<cl_f4 *>(part + (uint64_t)blockIdx.y * nb + 4 * q) = s;
 }
 
 // nb < 64: T = nb * (256 / nb) threads each own one column, (base + t) % nb,
@@ -328,8 +351,8 @@ void broadcast_grad(const float *g, size_t n, size_t nb, bool negate, float *par
         const size_t rows_per = cols_rows_per(rows);
         chunks = (rows + rows_per - 1) / rows_per;
         if (chunks && nb % 4 == 0 && (reinterpret_cast<uintptr_t>(g) & 15) == 0) {
-            const dim3 grid((unsigned)((nb / 4 + 255) / 256), (unsigned)chunks);
-            bcast_grad_cols4_kernel<<<grid, 256, 0, s>>>(g, n, nb, rows_per, part);
+            const dim3 grid((unsigned)((nb / 4 + kColQuads - 1) / kColQuads), (unsigned)chunks);
+            bcast_grad_cols4_kernel<<<grid, kColThreads, 0, s>>>(g, n, nb, rows_per, part);
         } else if (chunks) {
             const dim3 grid((unsigned)((nb + 255) / 256), (unsigned)chunks);
             bcast_grad_cols_kernel<<<grid, 256, 0, s>>>(g, n, nb, rows_per, part);
