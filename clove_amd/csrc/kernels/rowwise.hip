@@ -250,7 +250,7 @@ __device__ __forceinline__ long target_class(float v) {
 
 // Cross entropy, one wave per row (backend.rs:2661-2680): row value
 // v = (l[t] - max) - ln(sum exp(l - max)); the loss is -sum(v) / rows, which
-// loss_final sums in a fixed order.  Rows at or past `used` (no target)
+// ordered_sum (reduce.hip) adds in a fixed order.  Rows at or past `used` (no target)
 // give 0; a class >= cols raises the error flag and gives 0.
 // MODE 0 writes v to rowv[row].  MODE 1 is the backward (backend.rs:
 // 2686-2712): grad = (exp(l - max) / sum - [j == t]) * g / rows.
