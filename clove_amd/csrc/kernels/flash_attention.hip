@@ -63,9 +63,6 @@ struct AttnArgs {
     int tab_pos0;            // position of rope_tab's first row
 };
 
-__device__ __forceinline__ float fast_exp(float x) {
-    return __builtin_amdgcn_exp2f(x * 1.44269504088896341f);
-}
 
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
@@ -104,6 +101,9 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     const float2 *trow = a.rope_tab && q_ok
                              ? a.rope_tab + (size_t)(query + a.q_pos - a.tab_pos0) * (D / 2)
                              : nullptr;
+    // Scores are kept in base-2 units: q carries scale * log2(e), so a
+    // softmax weight is exp2(s - m) with no multiply per score.
+    const float qscale = a.scale * 1.44269504088896341f;
     cl_f4 qf[kG];
 #pragma unroll
     for (int g = 0; g < kG; ++g) {
@@ -118,7 +118,7 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
             r.w = v.z * t1.y + v.w * t1.x;
             v = r;
         }
-        qf[g] = v * a.scale;
+        qf[g] = v * qscale;
     }
 
     // keys [0, k_end) can be visible to some query of the workgroup
@@ -187,27 +187,19 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
         if (kb < k_wave) {
             const float *K = sK[cur];
             const float *V = sV[cur];
-            // S^T = K . Q^T: s[i] is the score of key kb + 8(i/4) + 4hh + i%4.
-            // Even and odd K-groups go to two accumulators, so consecutive
-            // MFMAs do not wait on each other's results.
-            f16v s, s2;
+            // S^T = K . Q^T: s[i] is the score of key kb + 8(i/4) + 4hh + i%4
+            // (in base-2 units).  One accumulator: splitting the chain over
+            // two measured the same and cost 16 adds per block.
+            f16v s;
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                s[e] = 0.f;
-                s2[e] = 0.f;
-            }
+            for (int e = 0; e < 16; ++e) s[e] = 0.f;
 #pragma unroll
-            for (int g = 0; g < kG; g += 2) {
+            for (int g = 0; g < kG; ++g) {
                 const cl_f4 kf = *reinterpret_cast<const cl_f4 *>(K + l32 * kPK + 8 * g + 4 * hh);
-                const cl_f4 kf2 =
-                    *reinterpret_cast<const cl_f4 *>(K + l32 * kPK + 8 * (g + 1) + 4 * hh);
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
+                for (int t = 0; t < 4; ++t)
                     s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[g][t], s, 0, 0, 0);
-                    s2 = __builtin_amdgcn_mfma_f32_32x32x2f32(kf2[t], qf[g + 1][t], s2, 0, 0, 0);
-                }
             }
-            s += s2;
             // A block the whole wave sees (every key < Sk and, under the causal
             // mask, at or before the wave's first query) skips the mask.
             const int qw0 = q0 + wave * 32;
@@ -230,7 +222,7 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
             // Lazy rescale: the running max m moves only when some query of the
             // wave sees a score more than kSlack above it.  Scores up to
-            // m + kSlack give weights up to e^kSlack, harmless in f32, and the
+            // m + kSlack give weights up to 2^kSlack, harmless in f32, and the
             // numerator O and the denominator lsum share m, so the result is
             // the same; the 16*kJ-multiply rescale of O is skipped on most
             // blocks.  (m = -inf, no visible key yet, always updates.)
@@ -238,7 +230,7 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
             const bool grow = __any(mloc > m + kSlack);
             if (grow) {
                 const float m_new = fmaxf(m, mloc);
-                const float alpha = m_new == -INFINITY ? 1.0f : fast_exp(m - m_new);
+                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
                 lsum *= alpha;
 #pragma unroll
                 for (int j = 0; j < kJ; ++j)
@@ -246,10 +238,14 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
                     for (int e = 0; e < 16; ++e) o[j][e] *= alpha;
                 m = m_new;
             }
+            // exp2(-inf) is 0, so masked scores need no test; only a lane
+            // with no visible key yet (m = -inf, every score of the block
+            // -inf) takes 0 as its max so that -inf - m is not NaN.
+            const float mz = m == -INFINITY ? 0.0f : m;
             float ps = 0.0f;
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                s[i] = s[i] == -INFINITY ? 0.0f : fast_exp(s[i] - m);
+                s[i] = __builtin_amdgcn_exp2f(s[i] - mz);
                 ps += s[i];
             }
             ps += __shfl_xor(ps, 32, 64);
