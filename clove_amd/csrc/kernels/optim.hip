@@ -49,19 +49,24 @@ __device__ __forceinline__ void adamw_elem(float &w, float g, float &m, float &v
     w -= h.lr * m_hat / (sqrtf(v_hat) + h.eps);
 }
 
-__global__ void __launch_bounds__(256) adamw_kernel(AdamWArgs a) {
+// 512-thread workgroups (83.9% of HBM peak at 4096 x 4096 against 83.0% for
+// 256).  w, m and v are read and written back with ordinary loads and stores:
+// non-temporal ones for these read-modify-write arrays measured 75.5%; the
+// gradient, read once, streams non-temporally.
+constexpr int kAdamWThreads = 512;
+__global__ void __launch_bounds__(kAdamWThreads) adamw_kernel(AdamWArgs a) {
     const int t = blockIdx.y;
     const uint64_t n = a.n[t];
     float *__restrict__ w = a.w[t];
     const float *__restrict__ g = a.g[t];
     float *__restrict__ m = a.m[t];
     float *__restrict__ v = a.v[t];
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    const uint64_t stride = (uint64_t)gridDim.x * kAdamWThreads;
     // 16-byte vectors when all four arrays are aligned; the rest element-wise
     const bool vec = ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(g) |
                        reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
     const uint64_t nvec = vec ? n / 4 : 0;
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nvec; i += stride) {
+    for (uint64_t i = (uint64_t)blockIdx.x * kAdamWThreads + threadIdx.x; i < nvec; i += stride) {
         cl_f4 wv = reinterpret_cast<cl_f4 *>(w)[i];
         const cl_f4 gv = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(g) + i);
         cl_f4 mv = reinterpret_cast<cl_f4 *>(m)[i];
@@ -78,7 +83,8 @@ __global__ void __launch_bounds__(256) adamw_kernel(AdamWArgs a) {
         reinterpret_cast<cl_f4 *>(m)[i] = mv;
         reinterpret_cast<cl_f4 *>(v)[i] = vv;
     }
-    for (uint64_t i = 4 * nvec + (uint64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) {
+    for (uint64_t i = 4 * nvec + (uint64_t)blockIdx.x * kAdamWThreads + threadIdx.x; i < n;
+         i += stride) {
         float wc = w[i], mc = m[i], vc = v[i];
         adamw_elem(wc, g[i], mc, vc, a.h);
         w[i] = wc;
@@ -107,11 +113,11 @@ void adamw_step(float *const *w, const float *const *g, float *const *m, float *
         if (!most) continue;
         // enough workgroups for the largest tensor (4 elements per thread per
         // pass), capped at 16 per CU and tensor: the loop strides the rest
-        uint64_t blocks = (most / 4 + 255) / 256;
+        uint64_t blocks = (most / 4 + kAdamWThreads - 1) / kAdamWThreads;
         const uint64_t cap = (uint64_t)num_cus * 16 / (uint64_t)c;
         if (blocks > cap) blocks = cap > 0 ? cap : 1;
         if (blocks < 1) blocks = 1;
-        adamw_kernel<<<dim3((unsigned)blocks, (unsigned)c), 256, 0, s>>>(a);
+        adamw_kernel<<<dim3((unsigned)blocks, (unsigned)c), kAdamWThreads, 0, s>>>(a);
     }
 }
 
