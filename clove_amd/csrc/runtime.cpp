@@ -20,8 +20,14 @@ Context g_ctx;
 bool g_ready = false;
 
 // Free blocks by capacity.  Capacities are size classes, so a request only
-// reuses a block of its own class.
-std::multimap<size_t, void *> g_free;
+// reuses a block of its own class.  Created once and never destroyed: tensors
+// held by other translation units' statics (the RoPE table cache) are
+// released by their destructors at process exit, in an order the language
+// leaves open, and must still find a live map to return their blocks to.
+std::multimap<size_t, void *> &free_blocks() {
+    static auto *m = new std::multimap<size_t, void *>();
+    return *m;
+}
 size_t g_reserved = 0;
 
 std::vector<hipEvent_t> g_events;
@@ -35,8 +41,8 @@ const std::string &last_error() { return g_last_error; }
 void fail(int code, const std::string &msg) { throw Error{code, msg}; }
 
 std::recursive_mutex &api_mutex() {
-    static std::recursive_mutex m;
-    return m;
+    static auto *m = new std::recursive_mutex();  // never destroyed (see free_blocks)
+    return *m;
 }
 
 Context &ctx() {
@@ -76,10 +82,10 @@ static size_t size_class(size_t bytes) {
 void *dev_alloc(size_t bytes, size_t *capacity) {
     ctx();  // fails before clove_hip_init
     const size_t cap = size_class(bytes);
-    auto it = g_free.find(cap);
-    if (it != g_free.end()) {
+    auto it = free_blocks().find(cap);
+    if (it != free_blocks().end()) {
         void *p = it->second;
-        g_free.erase(it);
+        free_blocks().erase(it);
         *capacity = cap;
         return p;
     }
@@ -102,18 +108,18 @@ void *dev_alloc(size_t bytes, size_t *capacity) {
 
 void dev_free(void *p, size_t capacity) {
     if (!p) return;
-    g_free.emplace(capacity, p);
+    free_blocks().emplace(capacity, p);
 }
 
 void dev_empty_cache() {
-    if (g_free.empty()) return;
+    if (free_blocks().empty()) return;
     // Blocks may still be referenced by enqueued kernels.
     (void)hipStreamSynchronize(g_ctx.stream);
-    for (auto &kv : g_free) {
+    for (auto &kv : free_blocks()) {
         (void)hipFree(kv.second);
         g_reserved -= kv.first;
     }
-    g_free.clear();
+    free_blocks().clear();
 }
 
 size_t dev_reserved() { return g_reserved; }

@@ -114,3 +114,26 @@ def test_attention_rope_equals_rope_then_attention(hip, B, S, Sk, H, D, flags, q
     qr, kr = hip.rope(t(q), D, q_pos), hip.rope(t(k), D, k_pos)
     split = hip.flash_attention(qr, kr, t(v), H, q_pos, k_pos, flags & ~2).numpy()
     assert np.array_equal(fused, split)
+
+
+def test_exit_without_shutdown_is_clean(hip):
+    """A process that uses the RoPE table cache and exits without
+    clove_hip_shutdown: the cache's tensors are released by static
+    destructors at exit, after (or before) the allocator's own statics;
+    the allocator state is never destroyed, so the exit is clean in any
+    order of destruction."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    code = (
+        "import sys; sys.path.insert(0, %r)\n"
+        "import numpy as np, clove_amd as ca\n"
+        "ca.init(0)\n"
+        "x = ca.tensor(np.ones((2, 64, 256), np.float32))\n"
+        "y = ca.flash_attention(x, x, x, 2)\n"
+        "z = ca.rope(x, 128, 5)\n"
+        "ca.synchronize()\n"
+        "print('ok', flush=True)\n" % root)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.returncode, r.stdout, r.stderr[-2000:])
