@@ -9,6 +9,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 
 #include "common.hpp"
 #include "kernels/launch.hpp"
@@ -88,7 +89,15 @@ TensorNode HipBackend::softmax_backward(const TensorNode &y_, const TensorNode &
 
 // backend.rs:1314-1360: grad_a = grad_out . b^T (a's shape, m = prod of a's
 // leading dims), grad_b = a^T . grad_out ([k, n]).  Each product is the MFMA
-// GEMM on a transposed copy of the other operand.
+// GEMM; where its plan allows (interior tiles of the 128x128 / 128x256
+// configurations) the GEMM reads the transposed operand directly
+// (k::gemm_f32_transposed), else it runs on a transposed copy.  Both give the
+// same bits.  CLOVE_GEMM_TRANSPOSED=0 forces the copies (tests).
+static bool transposed_loads_enabled() {
+    const char *v = std::getenv("CLOVE_GEMM_TRANSPOSED");
+    return !(v && v[0] == '0');
+}
+
 void HipBackend::matmul_backward(const TensorNode &a_, const TensorNode &b_, const TensorNode &g_,
                                  TensorNode *grad_a, TensorNode *grad_b) {
     const Tensor &a = need(a_, "a");
@@ -110,20 +119,28 @@ void HipBackend::matmul_backward(const TensorNode &a_, const TensorNode &b_, con
     hipStream_t s = ctx().stream;
     Tensor gv;
     view2d(g, m, n, &gv);
-    if (grad_a) {
+    const bool direct = transposed_loads_enabled();
+    const int cus = ctx().num_cus;
+    if (grad_a) {  // [m, n] . ([kk, n])^T
         TensorNode da = new_tensor(a.shape, CLOVE_HIP_F32);
-        TensorNode bt = new_tensor({n, kk}, CLOVE_HIP_F32);
-        k::transpose(b.f32(), bt->f32(), kk, n, s);
         Tensor dav;
         view2d(*da, m, kk, &dav);
-        matmul_into(gv, *bt, dav);
+        const k::GemmPlan p = k::gemm_plan((int)m, (int)kk, (int)n, cus, -1);
+        if (!(direct && k::gemm_f32_transposed(p, g.f32(), b.f32(), da->f32(), false, true, s))) {
+            TensorNode bt = new_tensor({n, kk}, CLOVE_HIP_F32);
+            k::transpose(b.f32(), bt->f32(), kk, n, s);
+            matmul_into(gv, *bt, dav);
+        }
         *grad_a = da;
     }
-    if (grad_b) {
+    if (grad_b) {  // ([m, kk])^T . [m, n]
         TensorNode db = new_tensor({kk, n}, CLOVE_HIP_F32);
-        TensorNode at = new_tensor({kk, m}, CLOVE_HIP_F32);
-        k::transpose(a.f32(), at->f32(), m, kk, s);
-        matmul_into(*at, gv, *db);
+        const k::GemmPlan p = k::gemm_plan((int)kk, (int)n, (int)m, cus, -1);
+        if (!(direct && k::gemm_f32_transposed(p, a.f32(), g.f32(), db->f32(), true, false, s))) {
+            TensorNode at = new_tensor({kk, m}, CLOVE_HIP_F32);
+            k::transpose(a.f32(), at->f32(), m, kk, s);
+            matmul_into(*at, gv, *db);
+        }
         *grad_b = db;
     }
 }

@@ -111,13 +111,28 @@ struct GemmCfg {
 // Loads one slab of A (rows m0.., cols k0..) and B (rows k0.., cols n0..)
 // into registers.  EDGE enables bounds checks; VEC selects 16-byte loads
 // (only legal when K % 4 == 0 and N % 4 == 0).
-template <class C, int BK, int BN, bool EDGE, bool VEC>
+// TA / TB (interior tiles only): A holds the [K, M] matrix whose transpose
+// is the product's A, or B the [N, K] matrix whose transpose is its B.  A
+// thread then loads four consecutive m (or k) of one k (or n) row, with k
+// (or the k quad) the fastest index over the threads, and store_slab writes
+// the four values to the same LDS places the plain layout would use, so the
+// product is the same bit for bit as transposing first.
+template <class C, int BM, int BK, int BN, bool EDGE, bool VEC, bool TA, bool TB>
 __device__ __forceinline__ void load_slab(const float *__restrict__ A, const float *__restrict__ B,
                                           int M, int N, int K, int m0, int n0, int k0, f4 *ra,
                                           f4 *rb) {
     const int tid = threadIdx.x;
+    static_assert(!(TA || TB) || (!EDGE && VEC), "transposed loads are interior-only");
+    if constexpr (TA) {
 #pragma unroll
-    for (int i = 0; i < C::kLoadsA; ++i) {
+        for (int i = 0; i < C::kLoadsA; ++i) {
+            const int idx = tid + i * C::kThreads;
+            const int k = idx % BK, mq = idx / BK;
+            ra[i] = *reinterpret_cast<const f4 *>(A + (size_t)(k0 + k) * M + m0 + 4 * mq);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (TA ? 0 : C::kLoadsA); ++i) {
         const int idx = tid + i * C::kThreads;
         const int r = idx / (BK / 4), kq = idx % (BK / 4);
         const int gm = m0 + r, gk = k0 + 4 * kq;
@@ -135,8 +150,16 @@ __device__ __forceinline__ void load_slab(const float *__restrict__ A, const flo
             ra[i] = v;
         }
     }
+    if constexpr (TB) {
 #pragma unroll
-    for (int i = 0; i < C::kLoadsB; ++i) {
+        for (int i = 0; i < C::kLoadsB; ++i) {
+            const int idx = tid + i * C::kThreads;
+            const int kq = idx % (BK / 4), n = idx / (BK / 4);
+            rb[i] = *reinterpret_cast<const f4 *>(B + (size_t)(n0 + n) * K + k0 + 4 * kq);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < (TB ? 0 : C::kLoadsB); ++i) {
         const int idx = tid + i * C::kThreads;
         const int r = idx / (BN / 4), nq = idx % (BN / 4);
         const int gk = k0 + r, gn = n0 + 4 * nq;
@@ -156,24 +179,37 @@ __device__ __forceinline__ void load_slab(const float *__restrict__ A, const flo
     }
 }
 
-template <class C, int BK, int BN>
+template <class C, int BK, int BN, bool TA = false, bool TB = false>
 __device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, const f4 *rb) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < C::kLoadsA; ++i) {
         const int idx = tid + i * C::kThreads;
-        const int r = idx / (BK / 4), kq = idx % (BK / 4);
-        *reinterpret_cast<f4 *>(sA + r * C::kPitchA + 4 * kq) = ra[i];
+        if constexpr (TA) {  // four m of one k: column k of rows 4mq .. 4mq+3
+            const int k = idx % BK, mq = idx / BK;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sA[(4 * mq + c) * C::kPitchA + k] = ra[i][c];
+        } else {
+            const int r = idx / (BK / 4), kq = idx % (BK / 4);
+            *reinterpret_cast<f4 *>(sA + r * C::kPitchA + 4 * kq) = ra[i];
+        }
     }
 #pragma unroll
     for (int i = 0; i < C::kLoadsB; ++i) {
         const int idx = tid + i * C::kThreads;
-        const int r = idx / (BN / 4), nq = idx % (BN / 4);
-        *reinterpret_cast<f4 *>(sB + r * C::kPitchB + 4 * nq) = rb[i];
+        if constexpr (TB) {  // four k of one n: rows 4kq .. 4kq+3 of column n
+            const int kq = idx % (BK / 4), n = idx / (BK / 4);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sB[(4 * kq + c) * C::kPitchB + n] = rb[i][c];
+        } else {
+            const int r = idx / (BN / 4), nq = idx % (BN / 4);
+            *reinterpret_cast<f4 *>(sB + r * C::kPitchB + 4 * nq) = rb[i];
+        }
     }
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC, bool EPI>
+template <int BM, int BN, int BK, int WM, int WN, bool EDGE, bool VEC, bool EPI, bool TA = false,
+          bool TB = false>
 __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     using Cfg = GemmCfg<BM, BN, BK, WM, WN>;
     __shared__ __attribute__((aligned(16))) float smem[2 * (Cfg::kSizeA + Cfg::kSizeB)];
@@ -207,8 +243,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     f4 ra[Cfg::kLoadsA], rb[Cfg::kLoadsB];
     const int slabs = (k_len + BK - 1) / BK;
 
-    load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, k_begin, ra, rb);
-    store_slab<Cfg, BK, BN>(smem, smem + Cfg::kSizeA, ra, rb);
+    load_slab<Cfg, BM, BK, BN, EDGE, VEC, TA, TB>(A, B, M, N, K, m0, n0, k_begin, ra, rb);
+    store_slab<Cfg, BK, BN, TA, TB>(smem, smem + Cfg::kSizeA, ra, rb);
     __syncthreads();
 
     for (int s = 0; s < slabs; ++s) {
@@ -216,7 +252,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
         float *sB = sA + Cfg::kSizeA;
         const bool more = s + 1 < slabs;
         if (more)
-            load_slab<Cfg, BK, BN, EDGE, VEC>(A, B, M, N, K, m0, n0, k_begin + (s + 1) * BK, ra, rb);
+            load_slab<Cfg, BM, BK, BN, EDGE, VEC, TA, TB>(A, B, M, N, K, m0, n0,
+                                                          k_begin + (s + 1) * BK, ra, rb);
 
 #pragma unroll
         for (int gk = 0; gk < BK / 8; ++gk) {
@@ -243,7 +280,7 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 
         if (more) {
             float *nA = smem + ((s + 1) & 1) * (Cfg::kSizeA + Cfg::kSizeB);
-            store_slab<Cfg, BK, BN>(nA, nA + Cfg::kSizeA, ra, rb);
+            store_slab<Cfg, BK, BN, TA, TB>(nA, nA + Cfg::kSizeA, ra, rb);
         }
         __syncthreads();
     }
@@ -918,6 +955,33 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
     case 8: gemm_small_grouped_kernel<8><<<(unsigned)start, 512, 0, s>>>(ga); break;
     default: gemm_small_grouped_kernel<16><<<(unsigned)start, 1024, 0, s>>>(ga); break;
     }
+}
+
+bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
+                         bool tb, hipStream_t s) {
+    if (ta == tb) return false;  // exactly one operand read transposed (the matmul backward)
+    if (p.small || p.skinny || p.splits != 1 || !p.interior || p.K <= 0) return false;
+    if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) return false;
+    if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128) return false;
+    const GemmArgs g{A, B, C, nullptr, p.M, p.N, p.K, p.tiles_n, p.k_per_split, 1, GemmEpilogue{},
+                     p.tiles, (p.tiles + 7) / 8};
+    const dim3 grid((unsigned)(g.per_xcd * 8), 1u);
+    if (p.cfg == CFG_128x256) {
+        if (ta)
+            gemm_f32_mfma_kernel<128, 256, 16, 64, 128, false, true, false, true, false>
+                <<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_mfma_kernel<128, 256, 16, 64, 128, false, true, false, false, true>
+                <<<grid, 256, 0, s>>>(g);
+    } else {
+        if (ta)
+            gemm_f32_mfma_kernel<128, 128, 16, 64, 64, false, true, false, true, false>
+                <<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_mfma_kernel<128, 128, 16, 64, 64, false, true, false, false, true>
+                <<<grid, 256, 0, s>>>(g);
+    }
+    return true;
 }
 
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,

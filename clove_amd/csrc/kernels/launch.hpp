@@ -131,6 +131,14 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
                    int force_skinny_splits = 0);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
+// C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the
+// [N, K] matrix), read transposed inside the tiled kernel's slab loads: the
+// same bits as transposing first.  Launches nothing and returns false unless
+// exactly one of ta, tb is set and p is an interior, unsplit 128x128 or
+// 128x256 tiled plan with 16-byte aligned operands; the caller then
+// transposes explicitly.
+bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
+                         bool tb, hipStream_t s);
 
 // paged_attention.hip
 struct PagedArgs {
