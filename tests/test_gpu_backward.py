@@ -161,8 +161,9 @@ def test_matmul_backward_transposed_loads_match_copies(hip, monkeypatch, m, k, n
                                   (1 << 24, 1), (5, 8), (64 * 300 + 5, 64), (63 * 1000, 63),
                                   (65 * 777, 65), (784 * 128, 128), (640, 10), (0, 3),
                                   # a partial block of column quads and a partial last row;
-                                  # more than 16384 x 32 rows (chunks of more than 32 rows)
-                                  (4100 * 70 + 13, 4100), (530000 * 64 + 3, 64)])
+                                  # more than 16384 x 64 rows (chunks of more than 64 rows)
+                                  (4100 * 70 + 13, 4100), (530000 * 64 + 3, 64),
+                                  (1100000 * 64 + 3, 64)])
 def test_broadcast_grad_exact(hip, n, nb):
     g = rng(n % 1000 + nb)
     go = g.integers(-8, 9, n).astype(np.float32)
