@@ -38,7 +38,7 @@ F32, I32 = 0, 1
 OP = dict(
     INPUT=0, MATMUL=1, ADD=2, SUB=3, MUL=4, SCALAR_MUL=5, FLATTEN=6, RELU=7, GELU=8,
     SIN=9, COS=10, SOFTMAX=11, LAYER_NORM=12, DROPOUT=13, RELU_GRAD=14, GELU_GRAD=15,
-    CAST=16, SIGMOID=17, TANH=18, PAGED_ATTENTION=19,
+    CAST=16, SIGMOID=17, TANH=18, PAGED_ATTENTION=19, ROPE=20,
 )
 
 
@@ -127,6 +127,7 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_graph_free": (None, [vp]),
         "clove_hip_graph_input": (C.c_int, [vp, C.c_char_p]),
         "clove_hip_graph_op": (C.c_int, [vp, C.c_int, C.POINTER(C.c_int), C.c_int, f]),
+        "clove_hip_graph_rope": (C.c_int, [vp, C.c_int, sz, sz]),
         "clove_hip_compile": (vp, [vp, C.POINTER(C.c_int), C.c_int]),
         "clove_hip_model_free": (None, [vp]),
         "clove_hip_execute": (C.c_int, [vp, C.POINTER(vp), C.c_int, C.POINTER(C.c_int64),
@@ -558,6 +559,13 @@ class Graph:
     def op(self, name: str, *deps: int, param: float = 0.0) -> int:
         arr = (C.c_int * max(1, len(deps)))(*deps)
         rc = lib().clove_hip_graph_op(self._h, OP[name.upper()], arr, len(deps), param)
+        if rc < 0:
+            raise CloveError(-rc, last_error())
+        return rc
+
+    def rope(self, x: int, head_dim: int, pos_offset: int = 0) -> int:
+        """RoPE(pos_offset, head_dim) over node x (lazy.rs:475-480)."""
+        rc = lib().clove_hip_graph_rope(self._h, x, pos_offset, head_dim)
         if rc < 0:
             raise CloveError(-rc, last_error())
         return rc

@@ -85,16 +85,19 @@ TensorNode rope_table_for(int pos0, int npos, int head_dim, int *tab_pos0) {
 }
 
 // lazy.rs:1621-1690 (the FlashAttention pattern) and :4821-4909 (its
-// kernel): q [B, S, H*D], k and v [B, Sk, H*D].  flags: causal mask on
-// absolute positions (t + k_pos > s + q_pos masked) and RoPE on q and k (k
-// in one pass before the kernel, q inside it).  scale <= 0 means 1/sqrt(D),
-// the reference's.
-TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,
-                                       const TensorNode &v_, int num_heads, int q_pos, int k_pos,
-                                       int flags, float scale) {
-    const Tensor &q = need(q_, "q");
-    const Tensor &k = need(k_, "k");
-    const Tensor &v = need(v_, "v");
+// kernel): q [B, S, H*D], k and v [B, Sk, H*D].  flags: causal mask and
+// RoPE on q and k (k in one pass before the kernel, q inside it) at
+// positions s + q_pos and t + k_pos.  The mask hides key t from query s when
+// t + mask_k > s + mask_q: the eager entry masks on absolute positions
+// (mask_q = q_pos, mask_k = k_pos); the planner's fused step masks on row
+// indices as the reference kernel does (lazy.rs:4882: key_idx > row).
+// scale <= 0 means 1/sqrt(D), the reference's.
+void HipBackend::flash_attention_into(const Tensor &q, const Tensor &k, const Tensor &v,
+                                      int num_heads, int q_pos, int k_pos, int mask_q,
+                                      int mask_k, int flags, float scale, Tensor &out) {
+    CLOVE_REQUIRE(q.dtype == CLOVE_HIP_F32 && k.dtype == CLOVE_HIP_F32 &&
+                      v.dtype == CLOVE_HIP_F32 && out.dtype == CLOVE_HIP_F32,
+                  CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be f32 tensors");
     size_t B, S, X, Bk, Sk, Xk, Bv, Sv, Xv;
     bsx(q, "q", &B, &S, &X);
     bsx(k, "k", &Bk, &Sk, &Xk);
@@ -109,10 +112,11 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
                   "flash_attention: head_dim " + std::to_string(D) + " (64 and 128 have kernels)");
     CLOVE_REQUIRE((flags & ~(CLOVE_ATTN_CAUSAL | CLOVE_ATTN_ROPE)) == 0, CLOVE_HIP_ERR_INVALID,
                   "flash_attention: unknown flag");
-    CLOVE_REQUIRE(q_pos >= 0 && k_pos >= 0, CLOVE_HIP_ERR_INVALID,
-                  "flash_attention: positions must be >= 0");
+    CLOVE_REQUIRE(q_pos >= 0 && k_pos >= 0 && mask_q >= 0 && mask_k >= 0,
+                  CLOVE_HIP_ERR_INVALID, "flash_attention: positions must be >= 0");
     CLOVE_REQUIRE(B * S < (1ull << 31) && B * Sk < (1ull << 31) &&
-                      (size_t)q_pos + S < (1ull << 30) && (size_t)k_pos + Sk < (1ull << 30),
+                      (size_t)q_pos + S < (1ull << 30) && (size_t)k_pos + Sk < (1ull << 30) &&
+                      (size_t)mask_q + S < (1ull << 30) && (size_t)mask_k + Sk < (1ull << 30),
                   CLOVE_HIP_ERR_SHAPE, "flash_attention: too many tokens");
     // the kernel addresses one batch's K or V rows with 32-bit byte offsets
     CLOVE_REQUIRE(Sk * X * 4 < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
@@ -120,9 +124,11 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
     // one 256-thread workgroup per (batch, head, block of 128 queries)
     CLOVE_REQUIRE(B * (size_t)num_heads * ((S + 127) / 128) * 256 < (1ull << 32),
                   CLOVE_HIP_ERR_SHAPE, "flash_attention: too many query blocks for one grid");
-    CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data),
+    CLOVE_REQUIRE(out.numel >= q.numel, CLOVE_HIP_ERR_SHAPE, "flash_attention: output too small");
+    CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data) &&
+                      aligned16(out.data),
                   CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned");
-    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
+    if (q.numel == 0) return;
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
     hipStream_t s = ctx().stream;
     const float *kp = k.f32();
@@ -138,15 +144,29 @@ TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k
         k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), t0, s);
         kp = kr->f32();
     }
-    k::attention_prefill(q.f32(), kp, v.f32(), out->f32(), (int)B, (int)S, (int)Sk, num_heads, D,
-                         q_pos, k_pos, (flags & CLOVE_ATTN_CAUSAL) != 0, sc,
-                         tab ? tab->f32() : nullptr, t0, s);
+    // The kernel reads query s's table row at s + (its q_pos) - (its
+    // tab_pos0); passing the mask offset as its q_pos and shifting the table
+    // origin by the difference keeps that row at s + q_pos.
+    k::attention_prefill(q.f32(), kp, v.f32(), out.f32(), (int)B, (int)S, (int)Sk, num_heads, D,
+                         mask_q, mask_k, (flags & CLOVE_ATTN_CAUSAL) != 0, sc,
+                         tab ? tab->f32() : nullptr, t0 - (q_pos - mask_q), s);
+}
+
+TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,
+                                       const TensorNode &v_, int num_heads, int q_pos, int k_pos,
+                                       int flags, float scale) {
+    const Tensor &q = need(q_, "q");
+    const Tensor &k = need(k_, "k");
+    const Tensor &v = need(v_, "v");
+    TensorNode out = new_tensor(q.shape, CLOVE_HIP_F32);
+    flash_attention_into(q, k, v, num_heads, q_pos, k_pos, q_pos, k_pos, flags, scale, *out);
     return out;
 }
 
 // backend.rs:2797-2826: x [B, S, hidden] or [S, hidden].
-TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head_dim) {
-    const Tensor &x = need(x_, "x");
+void HipBackend::rope_into(const Tensor &x, size_t pos_offset, size_t head_dim, Tensor &out) {
+    CLOVE_REQUIRE(x.dtype == CLOVE_HIP_F32 && out.dtype == CLOVE_HIP_F32, CLOVE_HIP_ERR_INVALID,
+                  "rope: x must be an f32 tensor");
     size_t B, S, X;
     bsx(x, "x", &B, &S, &X);
     CLOVE_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, CLOVE_HIP_ERR_SHAPE,
@@ -154,12 +174,18 @@ TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head
     CLOVE_REQUIRE(X % 2 == 0, CLOVE_HIP_ERR_SHAPE, "rope: the hidden size must be even");
     CLOVE_REQUIRE(pos_offset + S < (1ull << 30) && X < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
                   "rope: positions or hidden size exceed 2^30");
-    TensorNode out = new_tensor(x.shape, CLOVE_HIP_F32);
-    if (x.numel == 0) return out;
+    CLOVE_REQUIRE(out.numel >= x.numel, CLOVE_HIP_ERR_SHAPE, "rope: output too small");
+    if (x.numel == 0) return;
     int t0 = 0;
     TensorNode tab = rope_table_for((int)pos_offset, (int)S, (int)head_dim, &t0);
-    k::rope_apply(x.f32(), out->f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
+    k::rope_apply(x.f32(), out.f32(), B * S, (int)S, (int)X, (int)head_dim, (int)pos_offset,
                   tab->f32(), t0, ctx().stream);
+}
+
+TensorNode HipBackend::rope(const TensorNode &x_, size_t pos_offset, size_t head_dim) {
+    const Tensor &x = need(x_, "x");
+    TensorNode out = new_tensor(x.shape, CLOVE_HIP_F32);
+    rope_into(x, pos_offset, head_dim, *out);
     return out;
 }
 

@@ -425,6 +425,9 @@ int clove_hip_fused_chain(const clove_hip_chain_op *ops, int n_ops, const CTenso
             chain[i].store = ops[i].store != 0 || i + 1 == n_ops;
             chain[i].param = ops[i].param;
         }
+        // The structure is checked before anything follows an operand, so
+        // the walk below only ever steps to earlier ops and ends at an input.
+        clove::validate_chain(chain, (size_t)n_inputs);
         std::vector<const Tensor *> ins(n_inputs);
         for (int k = 0; k < n_inputs; ++k) ins[k] = &deref(inputs[k], "input");
         // Index space: the numel of the last op, which (as in the tracer,
@@ -471,6 +474,17 @@ int clove_hip_graph_op(clove_hip_graph *g, int opcode, const int *deps, int n_de
         if (!g) clove::fail(CLOVE_HIP_ERR_INVALID, "graph is NULL");
         if (n_deps < 0 || (n_deps > 0 && !deps)) clove::fail(CLOVE_HIP_ERR_INVALID, "bad operand list");
         id = g->g.add_op(opcode, std::vector<int>(deps, deps + n_deps), param);
+    });
+    return rc == CLOVE_HIP_OK ? id : -rc;
+}
+
+int clove_hip_graph_rope(clove_hip_graph *g, int x, size_t pos_offset, size_t head_dim) {
+    int id = -1;
+    const int rc = guarded([&] {
+        if (!g) clove::fail(CLOVE_HIP_ERR_INVALID, "graph is NULL");
+        if (pos_offset >= (1u << 30) || head_dim > 256)
+            clove::fail(CLOVE_HIP_ERR_INVALID, "RoPE: pos_offset or head_dim out of range");
+        id = g->g.add_rope(x, (int64_t)pos_offset, (int64_t)head_dim);
     });
     return rc == CLOVE_HIP_OK ? id : -rc;
 }

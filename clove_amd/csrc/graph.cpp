@@ -37,6 +37,8 @@
 
 #include "common.hpp"
 #include "graph.hpp"
+#include "kernels/ew_abi.h"
+#include "kernels/launch.hpp"
 #include "runtime.hpp"
 
 namespace clove {
@@ -175,6 +177,7 @@ const char *op_name(int op) {
     case CLOVE_OP_SIGMOID: return "Sigmoid";
     case CLOVE_OP_TANH: return "Tanh";
     case CLOVE_OP_PAGED_ATTENTION: return "PagedAttention";
+    case CLOVE_OP_ROPE: return "RoPE";
     default: return "?";
     }
 }
@@ -243,9 +246,30 @@ int Graph::add_op(int op, const std::vector<int> &deps, float param) {
     } else if (op == CLOVE_OP_PAGED_ATTENTION) {  // lazy.rs:860-886: q's shape
         want(6);
         n.shape = nodes[deps[0]].shape;
+    } else if (op == CLOVE_OP_ROPE) {
+        fail(CLOVE_HIP_ERR_INVALID, "RoPE takes two integer parameters: use clove_hip_graph_rope");
     } else {
         fail(CLOVE_HIP_ERR_INVALID, "opcode " + std::to_string(op) + " is not on the hot path");
     }
+    nodes.push_back(n);
+    return n.id;
+}
+
+// lazy.rs:475-480: RoPE(pos_offset, head_dim) keeps its operand's shape.
+int Graph::add_rope(int x, int64_t pos_offset, int64_t head_dim) {
+    CLOVE_REQUIRE(x >= 0 && x < (int)nodes.size(), CLOVE_HIP_ERR_INVALID,
+                  "RoPE: operand " + std::to_string(x) + " does not exist");
+    CLOVE_REQUIRE(head_dim >= 2 && head_dim % 2 == 0 && head_dim <= 256, CLOVE_HIP_ERR_SHAPE,
+                  "RoPE: head_dim must be even and at most 256");
+    CLOVE_REQUIRE(pos_offset >= 0 && pos_offset < (1 << 30), CLOVE_HIP_ERR_INVALID,
+                  "RoPE: pos_offset must be in [0, 2^30)");
+    Node n;
+    n.id = (int)nodes.size();
+    n.op = CLOVE_OP_ROPE;
+    n.deps = {x};
+    n.shape = nodes[x].shape;
+    n.pos_offset = pos_offset;
+    n.head_dim = head_dim;
     nodes.push_back(n);
     return n.id;
 }
@@ -273,8 +297,12 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
     std::vector<int> alias(nodes.size());
     for (size_t i = 0; i < nodes.size(); ++i) alias[i] = (int)i;
     std::set<int> out_set(outs.begin(), outs.end());
+    // Nodes whose first operand was a folded x * 1.0: the attention pattern
+    // below reads that as a softmax scale of 1.
+    std::set<int> unit_scaled_lhs;
     for (auto &n : nodes) {
         if (!alive[n.id]) continue;
+        if (!n.deps.empty() && alias[n.deps[0]] != n.deps[0]) unit_scaled_lhs.insert(n.id);
         for (int &d : n.deps) d = alias[d];
         if (n.op == CLOVE_OP_SCALAR_MUL && !n.deps.empty() &&
             std::fabs(n.param - 1.0f) < 1.1920929e-7f && !out_set.count(n.id)) {
@@ -291,6 +319,70 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
     for (const Node &n : nodes)
         if (alive[n.id])
             for (int d : n.deps) users[d].push_back(n.id);
+
+    // `sole(id)`: the only consumer of `id`, or -1 when it has several, none,
+    // or is a requested output.
+    auto sole = [&](int id) {
+        return (!out_set.count(id) && users[id].size() == 1) ? users[id][0] : -1;
+    };
+    std::set<int> absorbed;  // nodes folded into another step
+
+    // 2b. The FlashAttention pattern (lazy.rs:1621-1690):
+    //   MatMul(Softmax(MatMul([ScalarMul(s)](RoPE(q)), RoPE(k))), v)
+    // becomes one ATTENTION step over the un-rotated q and k and v, with the
+    // contract of the reference's fused kernel (lazy.rs:4821-4909): one token
+    // per row, keys after the query's row masked, q and k rotated at the
+    // RoPE nodes' positions, head_dim from the RoPE nodes (here heads =
+    // hidden / head_dim; the reference kernel takes one head).  The softmax
+    // scale is the ScalarMul's factor (a folded x * 1.0 counts as a factor of
+    // 1), 1/sqrt(head_dim) without one (the
+    // reference kernel always uses 1/sqrt(head_dim) and drops the
+    // ScalarMul, which is the same thing in MultiHeadAttention::forward,
+    // nn/attention.rs:62-67).  Both RoPE nodes must be present with one
+    // head_dim the kernel supports, q must be 2-d, and the inner MatMul and
+    // the Softmax must feed only the pattern; otherwise the nodes are planned
+    // one by one.  A RoPE or ScalarMul node that other nodes also read keeps
+    // its own step; the fused step still starts from the un-rotated inputs.
+    std::map<int, Step> attention_at;  // outer MatMul id -> its ATTENTION step
+    for (const Node &outer : nodes) {
+        if (!alive[outer.id] || outer.op != CLOVE_OP_MATMUL) continue;
+        const int sm = outer.deps[0], v = outer.deps[1];
+        if (nodes[sm].op != CLOVE_OP_SOFTMAX || sole(sm) != outer.id) continue;
+        const int inner = nodes[sm].deps[0];
+        if (nodes[inner].op != CLOVE_OP_MATMUL || sole(inner) != sm) continue;
+        int qq = nodes[inner].deps[0];
+        const int kk = nodes[inner].deps[1];
+        float scale = unit_scaled_lhs.count(inner) ? 1.0f : 0.0f;
+        int smul = -1;
+        if (nodes[qq].op == CLOVE_OP_SCALAR_MUL) {
+            scale = nodes[qq].param;
+            smul = qq;
+            qq = nodes[qq].deps[0];
+        }
+        if (nodes[qq].op != CLOVE_OP_ROPE || nodes[kk].op != CLOVE_OP_ROPE || qq == kk) continue;
+        const int64_t hd = nodes[qq].head_dim;
+        if (nodes[kk].head_dim != hd || !k::attention_supported((int)hd)) continue;
+        const int q = nodes[qq].deps[0], kx = nodes[kk].deps[0];
+        if (nodes[q].shape.size() != 2 || nodes[kx].shape.size() != 2 ||
+            nodes[v].shape.size() != 2)
+            continue;
+        if (smul >= 0 && !(scale > 0.f)) continue;  // the kernel needs a positive scale
+        Step st;
+        st.kind = Step::ATTENTION;
+        st.in = {q, kx, v};
+        st.out = {outer.id};
+        st.q_pos = nodes[qq].pos_offset;
+        st.k_pos = nodes[kk].pos_offset;
+        st.head_dim = hd;
+        st.scale = scale;
+        attention_at[outer.id] = st;
+        absorbed.insert(sm);
+        absorbed.insert(inner);
+        const int after_q = smul >= 0 ? smul : inner;
+        if (smul >= 0 && sole(smul) == inner) absorbed.insert(smul);
+        if (sole(qq) == after_q) absorbed.insert(qq);
+        if (sole(kk) == inner) absorbed.insert(kk);
+    }
 
     // 3. planning
     std::vector<int> group;
@@ -331,13 +423,36 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
         steps.push_back(st);
         group.clear();
     };
-    std::set<int> absorbed;  // nodes folded into a GEMM epilogue
+    // Whether `group` plus node `id` stays within what one chain launch
+    // takes (run_chain: CL_MAX_IN distinct outside inputs, CL_MAX_OUT stored
+    // values).  A member is stored when it is requested or read outside the
+    // group, and the last member always is, exactly as flush() decides.
+    auto fits_with = [&](int id) {
+        std::set<int> members(group.begin(), group.end());
+        members.insert(id);
+        std::set<int> outside;
+        int stores = 0;
+        for (int m : members) {
+            for (int d : nodes[m].deps)
+                if (!members.count(d)) outside.insert(d);
+            bool escapes = out_set.count(m) > 0 || m == id;
+            for (int u : users[m])
+                if (!members.count(u)) escapes = true;
+            stores += escapes;
+        }
+        return (int)outside.size() <= CL_MAX_IN && stores <= CL_MAX_OUT;
+    };
     for (const Node &n : nodes) {
         if (!alive[n.id] || n.op == CLOVE_OP_INPUT || absorbed.count(n.id)) continue;
+        if (attention_at.count(n.id)) {
+            flush();
+            steps.push_back(attention_at[n.id]);
+            continue;
+        }
         if (ew_arity(n.op) > 0) {
             if (!group.empty() &&
                 (shape_key(nodes[group.back()].shape) != shape_key(n.shape) ||
-                 (int)group.size() >= 32))
+                 (int)group.size() >= 32 || !fits_with(n.id)))
                 flush();
             group.push_back(n.id);
             continue;
@@ -348,15 +463,17 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
         case CLOVE_OP_MATMUL: st.kind = Step::MATMUL; break;
         case CLOVE_OP_SOFTMAX: st.kind = Step::SOFTMAX; break;
         case CLOVE_OP_LAYER_NORM: st.kind = Step::LAYER_NORM; break;
+        case CLOVE_OP_ROPE:
+            st.kind = Step::ROPE;
+            st.q_pos = n.pos_offset;
+            st.head_dim = n.head_dim;
+            break;
         default: st.kind = Step::PAGED; break;
         }
         st.in = n.deps;
         st.out = {n.id};
         if (n.op == CLOVE_OP_MATMUL) {
-            // Epilogue fusion.  `sole` is the only consumer of `id`, or -1.
-            auto sole = [&](int id) {
-                return (!out_set.count(id) && users[id].size() == 1) ? users[id][0] : -1;
-            };
+            // Epilogue fusion.
             int tail = n.id;
             const int add = sole(n.id);
             if (add >= 0 && nodes[add].op == CLOVE_OP_ADD && nodes[add].deps[0] == n.id &&
@@ -444,7 +561,10 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
                 vbuf[o] = num_vbufs++;
             }
         }
-        for (int d : steps[i].in) {
+        // each buffer is released once, however many operands of the step
+        // read it (MatMul(a, a), attention with q and k from one node)
+        std::set<int> read(steps[i].in.begin(), steps[i].in.end());
+        for (int d : read) {
             auto it = vbuf.find(d);
             if (it != vbuf.end() && last_use[d] == (int)i && !out_set.count(d))
                 free_list.push_back(it->second);
@@ -477,6 +597,11 @@ std::string Model::describe() const {
             break;
         case Step::SOFTMAX: s << "Softmax"; break;
         case Step::LAYER_NORM: s << "LayerNorm"; break;
+        case Step::ROPE: s << "RoPE(" << st.q_pos << "," << st.head_dim << ")"; break;
+        case Step::ATTENTION:
+            s << "FlashAttention(q_pos=" << st.q_pos << ",k_pos=" << st.k_pos
+              << ",head_dim=" << st.head_dim << ",causal)";
+            break;
         default: s << "PagedAttention"; break;
         }
         s << " in=(";
@@ -594,6 +719,23 @@ std::vector<TensorNode> Model::execute(const std::vector<TensorNode> &in, const 
             HipBackend::layer_norm_into(*arg(st.in[0]), *arg(st.in[1]), *arg(st.in[2]),
                                         *view_of(st.out[0]));
             break;
+        case Step::ROPE:
+            HipBackend::rope_into(*arg(st.in[0]), (size_t)st.q_pos, (size_t)st.head_dim,
+                                  *view_of(st.out[0]));
+            break;
+        case Step::ATTENTION: {
+            const Tensor *q = arg(st.in[0]);
+            const int heads = (int)(q->shape.back() / (size_t)st.head_dim);
+            CLOVE_REQUIRE(heads >= 1 && q->shape.back() % (size_t)st.head_dim == 0,
+                          CLOVE_HIP_ERR_SHAPE,
+                          "attention: the hidden size " + std::to_string(q->shape.back()) +
+                              " is not a multiple of head_dim " + std::to_string(st.head_dim));
+            HipBackend::flash_attention_into(*q, *arg(st.in[1]), *arg(st.in[2]), heads,
+                                             (int)st.q_pos, (int)st.k_pos, 0, 0,
+                                             CLOVE_ATTN_CAUSAL | CLOVE_ATTN_ROPE, st.scale,
+                                             *view_of(st.out[0]));
+            break;
+        }
         case Step::PAGED: {
             const Tensor *q = arg(st.in[0]);
             const int D = (int)arg(st.in[3])->shape.back();

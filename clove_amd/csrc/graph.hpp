@@ -34,6 +34,7 @@ struct Node {
     std::vector<SymPtr> shape;
     std::vector<int> deps;
     float param = 0.f;
+    int64_t pos_offset = 0, head_dim = 0;  // RoPE(pos_offset, head_dim) only
 };
 
 // ComputeGraph (backend.rs:149-160), held explicitly instead of in a
@@ -43,11 +44,12 @@ struct Graph {
     std::vector<int> input_order;
     int add_input(const std::string &spec);
     int add_op(int op, const std::vector<int> &deps, float param);
+    int add_rope(int x, int64_t pos_offset, int64_t head_dim);
 };
 
 // Step (lazy.rs:1158-1376), hot-path kinds only.
 struct Step {
-    enum Kind { FUSED, MATMUL, SOFTMAX, LAYER_NORM, PAGED, MATMUL_GROUP };
+    enum Kind { FUSED, MATMUL, SOFTMAX, LAYER_NORM, PAGED, MATMUL_GROUP, ROPE, ATTENTION };
     Kind kind = FUSED;
     std::vector<int> in;    // node ids read (each once)
     std::vector<int> out;   // node ids written
@@ -57,6 +59,12 @@ struct Step {
                                  // 3 row softmax); a third input, when present, is the
                                  // fused bias
     std::vector<Step> members;   // MATMUL_GROUP only: independent MATMUL steps
+    // ROPE: rotation of in[0] at pos_offset q_pos with head_dim.
+    // ATTENTION (in = q, k, v): causal attention on row indices with q
+    // rotated at q_pos and k at k_pos (head_dim-wide heads), softmax scale
+    // `scale` (<= 0: 1/sqrt(head_dim)).
+    int64_t q_pos = 0, k_pos = 0, head_dim = 0;
+    float scale = 0.f;
 };
 
 // CompiledModel (lazy.rs:2545-2555).

@@ -237,13 +237,11 @@ int ew_arity(int opcode) {
     }
 }
 
-void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *> &inputs,
-               const std::vector<Tensor *> &outs, size_t numel) {
-    Context &c = ctx();
+int validate_chain(const std::vector<ChainOp> &ops, size_t n_inputs) {
     CLOVE_REQUIRE(!ops.empty(), CLOVE_HIP_ERR_INVALID, "empty chain");
     CLOVE_REQUIRE((int)ops.size() <= CL_MAX_OPS, CLOVE_HIP_ERR_INVALID,
                   "chain longer than " + std::to_string(CL_MAX_OPS) + " ops");
-    CLOVE_REQUIRE((int)inputs.size() <= CL_MAX_IN && !inputs.empty(), CLOVE_HIP_ERR_INVALID,
+    CLOVE_REQUIRE(n_inputs <= (size_t)CL_MAX_IN && n_inputs > 0, CLOVE_HIP_ERR_INVALID,
                   "a chain takes 1.." + std::to_string(CL_MAX_IN) + " inputs");
     int nstore = 0;
     for (size_t i = 0; i < ops.size(); ++i) {
@@ -253,14 +251,27 @@ void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *
                       "opcode " + std::to_string(op.opcode) + " is not elementwise");
         const int srcs[2] = {op.src0, op.src1};
         for (int j = 0; j < ar; ++j) {
-            const int s = srcs[j];
-            CLOVE_REQUIRE(s < (int)i && -s - 1 < (int)inputs.size(), CLOVE_HIP_ERR_INVALID,
+            // 64-bit, so that -(src + 1) of INT_MIN does not overflow
+            const int64_t s = srcs[j];
+            const bool earlier_op = s >= 0 && s < (int64_t)i;
+            const bool input = s < 0 && -s - 1 < (int64_t)n_inputs;
+            CLOVE_REQUIRE(earlier_op || input, CLOVE_HIP_ERR_INVALID,
                           "op " + std::to_string(i) + " operand " + std::to_string(s) +
                               " is neither an earlier op nor an input");
         }
         if (op.store || i + 1 == ops.size()) ++nstore;
     }
-    CLOVE_REQUIRE(nstore == (int)outs.size() && nstore <= CL_MAX_OUT, CLOVE_HIP_ERR_INVALID,
+    CLOVE_REQUIRE(nstore <= CL_MAX_OUT, CLOVE_HIP_ERR_INVALID,
+                  "chain stores " + std::to_string(nstore) + " values; at most " +
+                      std::to_string(CL_MAX_OUT) + " are allowed");
+    return nstore;
+}
+
+void run_chain(const std::vector<ChainOp> &ops, const std::vector<const Tensor *> &inputs,
+               const std::vector<Tensor *> &outs, size_t numel) {
+    Context &c = ctx();
+    const int nstore = validate_chain(ops, inputs.size());
+    CLOVE_REQUIRE(nstore == (int)outs.size(), CLOVE_HIP_ERR_INVALID,
                   "chain stores " + std::to_string(nstore) + " values but " +
                       std::to_string(outs.size()) + " outputs were given");
     if (numel == 0) return;

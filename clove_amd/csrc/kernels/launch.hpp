@@ -140,6 +140,14 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
 bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
                          bool tb, hipStream_t s);
 
+// Bits of the device error word (runtime.cpp) that the next synchronising
+// call reports: kernels OR them in when they meet a bad index.
+enum : int32_t {
+    kErrPagedRange = 1,  // a block-table entry outside the pool / a context past the table
+    kErrClassRange = 2,  // a cross-entropy target >= the number of classes
+    kErrIndexValue = 4,  // an f32 index tensor held a value that is not an integer in [0, 2^24)
+};
+
 // paged_attention.hip
 struct PagedArgs {
     const float *q;        // [B, H, D]
@@ -169,8 +177,23 @@ void paged_append(float *k_cache, float *v_cache, const float *k_new, const floa
                   const int32_t *block_tables, const int32_t *context_lens, int num_seqs,
                   int max_blocks, int block_size, int64_t num_blocks, int row_floats,
                   int32_t *err_flag, hipStream_t s);
+// Slots bt[b][t/bs]*bs + t%bs, -1 past ctx_b; a negative entry, or one
+// whose slots do not fit in int32, gives -1 and sets kErrPagedRange.
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,
-                 int num_seqs, int max_blocks, int block_size, int max_ctx, hipStream_t s);
+                 int num_seqs, int max_blocks, int block_size, int max_ctx, int32_t *err_flag,
+                 hipStream_t s);
+// Block tables / context lengths that arrive as f32 (Clove builds every
+// tensor from a Vec<f32>, backend.rs:176), converted in one launch.  A value
+// is taken when it is an integer in [0, 2^24), where f32 holds every integer
+// exactly; otherwise it becomes -1.  A bad context length always sets
+// kErrIndexValue; a bad table entry only when its sequence's context reaches
+// it (entry j of sequence b is used when j * block_size < ctx_b), so padding
+// past a sequence's blocks is never an error, as it is never read.
+//   bt_f  f32 [B, max_blocks] or null (the table is int32 already)
+//   cl_f  f32 [B] or null, in which case cl_i (int32 [B]) gives the lengths
+void paged_index_from_f32(const float *bt_f, int32_t *bt_out, const float *cl_f,
+                          const int32_t *cl_i, int32_t *cl_out, int num_seqs, int max_blocks,
+                          int block_size, int32_t *err_flag, hipStream_t s);
 
 }  // namespace k
 }  // namespace clove

@@ -66,16 +66,11 @@ namespace k {
 
 namespace {
 
-// Physical slot of logical token t of a sequence whose table row is `bt`.
-__device__ __forceinline__ int64_t paged_slot(const int32_t *bt, int t, int bs) {
-    return (int64_t)bt[t / bs] * bs + t % bs;
-}
-
 __device__ __forceinline__ int clamp_ctx(const PagedArgs &a, int b, bool report) {
     int ctx = a.context_lens[b];
     const int cap = a.max_blocks * a.block_size;
     if (ctx < 0 || ctx > cap) {
-        if (report) atomicOr(a.err_flag, 1);
+        if (report) atomicOr(a.err_flag, kErrPagedRange);
         ctx = ctx < 0 ? 0 : cap;
     }
     return ctx;
@@ -336,7 +331,7 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
         for (int lb = lb_first; lb < full_end; ++lb) {
             const int64_t blk = bt[lb];
             if (blk < 0 || blk >= nb) {
-                if (lane == 0) atomicOr(a.err_flag, 1);
+                if (lane == 0) atomicOr(a.err_flag, kErrPagedRange);
                 continue;
             }
             BlockRegs<D, BS> r;
@@ -347,7 +342,7 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
     if (tail_checked) {
         const int64_t blk = bt[lb_last];
         if (blk < 0 || blk >= nb) {
-            if (lane == 0) atomicOr(a.err_flag, 1);
+            if (lane == 0) atomicOr(a.err_flag, kErrPagedRange);
         } else {
             const size_t off = (size_t)blk * BS * row_stride + lane_off;
             fold_block<D, BS, true>(a, a.k_cache + off, a.v_cache + off, row_stride, lb_last * BS,
@@ -433,12 +428,12 @@ __global__ void __launch_bounds__(256) paged_append_kernel(float *__restrict__ k
     const int ctx = cl[b];
     if (ctx <= 0) return;
     if (ctx > max_blocks * bs) {
-        if (threadIdx.x == 0) atomicOr(err_flag, 1);
+        if (threadIdx.x == 0) atomicOr(err_flag, kErrPagedRange);
         return;
     }
     const int64_t blk = bt[(size_t)b * max_blocks + (ctx - 1) / bs];
     if (blk < 0 || blk >= num_blocks) {
-        if (threadIdx.x == 0) atomicOr(err_flag, 1);
+        if (threadIdx.x == 0) atomicOr(err_flag, kErrPagedRange);
         return;
     }
     const size_t dst = ((size_t)blk * bs + (ctx - 1) % bs) * row_floats;
@@ -453,15 +448,55 @@ __global__ void __launch_bounds__(256) paged_slots_kernel(const int32_t *__restr
                                                           const int32_t *__restrict__ cl,
                                                           int32_t *__restrict__ slots,
                                                           int num_seqs, int max_blocks, int bs,
-                                                          int max_ctx) {
+                                                          int max_ctx, int32_t *err_flag) {
     const int64_t total = (int64_t)num_seqs * max_ctx;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total;
          i += (int64_t)gridDim.x * 256) {
         const int b = (int)(i / max_ctx), t = (int)(i % max_ctx);
         const int ctx = cl[b];
-        slots[i] = (t < ctx && t < max_blocks * bs)
-                       ? (int32_t)paged_slot(bt + (size_t)b * max_blocks, t, bs)
-                       : -1;
+        int32_t slot = -1;
+        if (t < ctx && t < max_blocks * bs) {
+            const int32_t e = bt[(size_t)b * max_blocks + t / bs];
+            // every slot of block e must be a non-negative int32
+            if (e >= 0 && (int64_t)e * bs + bs <= (int64_t)INT32_MAX)
+                slot = e * bs + t % bs;
+            else
+                atomicOr(err_flag, kErrPagedRange);
+        }
+        slots[i] = slot;
+    }
+}
+
+// An f32 index value: v when v is an integer in [0, 2^24) (f32 represents
+// all of them exactly, so the comparison with its truncation and the
+// conversion are exact), else -1.
+__device__ __forceinline__ int32_t index_value(float v) {
+    return (v >= 0.0f && v < 16777216.0f && v == truncf(v)) ? (int32_t)v : -1;
+}
+
+__global__ void __launch_bounds__(256) paged_index_kernel(const float *__restrict__ bt_f,
+                                                          int32_t *__restrict__ bt_out,
+                                                          const float *__restrict__ cl_f,
+                                                          const int32_t *__restrict__ cl_i,
+                                                          int32_t *__restrict__ cl_out,
+                                                          int num_seqs, int max_blocks, int bs,
+                                                          int32_t *err_flag) {
+    const int64_t n_bt = bt_f ? (int64_t)num_seqs * max_blocks : 0;
+    const int64_t n_cl = cl_f ? num_seqs : 0;
+    const int64_t stride = (int64_t)gridDim.x * 256;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n_cl + n_bt; i += stride) {
+        if (i < n_cl) {
+            const int32_t c = index_value(cl_f[i]);
+            if (c < 0) atomicOr(err_flag, kErrIndexValue);
+            cl_out[i] = c;
+            continue;
+        }
+        const int64_t e = i - n_cl;
+        const int b = (int)(e / max_blocks), j = (int)(e % max_blocks);
+        const int32_t ctx = cl_f ? index_value(cl_f[b]) : cl_i[b];
+        const int32_t v = index_value(bt_f[e]);
+        if (v < 0 && ctx > 0 && (int64_t)j * bs < (int64_t)ctx) atomicOr(err_flag, kErrIndexValue);
+        bt_out[e] = v;
     }
 }
 
@@ -533,13 +568,28 @@ void paged_append(float *k_cache, float *v_cache, const float *k_new, const floa
 }
 
 void paged_slots(const int32_t *block_tables, const int32_t *context_lens, int32_t *slots,
-                 int num_seqs, int max_blocks, int block_size, int max_ctx, hipStream_t s) {
+                 int num_seqs, int max_blocks, int block_size, int max_ctx, int32_t *err_flag,
+                 hipStream_t s) {
     const int64_t total = (int64_t)num_seqs * max_ctx;
     if (total <= 0) return;
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     paged_slots_kernel<<<(unsigned)blocks, 256, 0, s>>>(block_tables, context_lens, slots,
-                                                        num_seqs, max_blocks, block_size, max_ctx);
+                                                        num_seqs, max_blocks, block_size, max_ctx,
+                                                        err_flag);
+}
+
+void paged_index_from_f32(const float *bt_f, int32_t *bt_out, const float *cl_f,
+                          const int32_t *cl_i, int32_t *cl_out, int num_seqs, int max_blocks,
+                          int block_size, int32_t *err_flag, hipStream_t s) {
+    const int64_t total =
+        (bt_f ? (int64_t)num_seqs * max_blocks : 0) + (cl_f ? (int64_t)num_seqs : 0);
+    if (total <= 0) return;
+    int64_t blocks = (total + 255) / 256;
+    if (blocks > 4096) blocks = 4096;
+    paged_index_kernel<<<(unsigned)blocks, 256, 0, s>>>(bt_f, bt_out, cl_f, cl_i, cl_out,
+                                                        num_seqs, max_blocks, block_size,
+                                                        err_flag);
 }
 
 }  // namespace k

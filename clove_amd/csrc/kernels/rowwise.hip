@@ -277,7 +277,7 @@ __global__ void __launch_bounds__(256) cross_entropy_wave_kernel(
     if (row < used) {
         t = target_class(targets[row]);
         if (t >= cols) {
-            if (lane == 0) *err_flag = 1;
+            if (lane == 0) atomicOr(err_flag, kErrClassRange);
             t = -1;
         }
     }
@@ -349,7 +349,7 @@ __global__ void __launch_bounds__(256) cross_entropy_loop_kernel(
     if (row < used) {
         t = target_class(targets[row]);
         if (t >= cols) {
-            if (lane == 0) *err_flag = 1;
+            if (lane == 0) atomicOr(err_flag, kErrClassRange);
             t = -1;
         }
     }
@@ -513,7 +513,7 @@ __global__ void __launch_bounds__(kBlockThreads) cross_entropy_block_kernel(
     if (row < used) {
         t = target_class(targets[row]);
         if (t >= cols) {
-            if (threadIdx.x == 0) *err_flag = 1;
+            if (threadIdx.x == 0) atomicOr(err_flag, kErrClassRange);
             t = -1;
         }
     }

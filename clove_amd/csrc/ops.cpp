@@ -31,6 +31,42 @@ void need_f32(const Tensor &t, const char *what) {
                   std::string(what) + " must be an f32 tensor");
 }
 
+// The int32 views of a block table and a context-length tensor.  Clove
+// builds every tensor from a Vec<f32> (backend.rs:176, ffi.rs:71-87), so its
+// paged_attention receives both as f32 tensors (backend.rs:249-256,
+// nn.rs:528-546); int32 tensors are used as they are.  f32 ones are
+// converted on the device into temporaries, in one launch: an integer value
+// in [0, 2^24) is taken as is, anything else becomes -1 and, for a context
+// length or a table entry the context reaches, is reported as
+// CLOVE_HIP_ERR_RANGE by the next synchronising call (a -1 entry lies outside
+// the pool and its tokens are skipped; a -1 context length counts as 0).
+// Entries past a sequence's blocks are never read, so their values do not
+// matter, as with int32 tables.
+struct IndexPair {
+    const int32_t *bt = nullptr, *cl = nullptr;
+    TensorNode bt_tmp, cl_tmp;
+};
+
+IndexPair index_pair(const Tensor &bt, const Tensor &cl, int block_size) {
+    auto ok = [](const Tensor &t) { return t.dtype == CLOVE_HIP_I32 || t.dtype == CLOVE_HIP_F32; };
+    CLOVE_REQUIRE(ok(bt) && ok(cl), CLOVE_HIP_ERR_INVALID,
+                  "block_tables and context_lens must be int32 or f32 tensors");
+    CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == cl.numel && bt.shape[1] < (1ull << 31),
+                  CLOVE_HIP_ERR_SHAPE,
+                  "block_tables must be [num_seqs, max_blocks] with num_seqs = numel(context_lens)");
+    IndexPair p;
+    if (bt.dtype == CLOVE_HIP_F32) p.bt_tmp = new_tensor(bt.shape, CLOVE_HIP_I32);
+    if (cl.dtype == CLOVE_HIP_F32) p.cl_tmp = new_tensor(cl.shape, CLOVE_HIP_I32);
+    if (p.bt_tmp || p.cl_tmp)
+        k::paged_index_from_f32(p.bt_tmp ? bt.f32() : nullptr, p.bt_tmp ? p.bt_tmp->i32() : nullptr,
+                                p.cl_tmp ? cl.f32() : nullptr, p.cl_tmp ? nullptr : cl.i32(),
+                                p.cl_tmp ? p.cl_tmp->i32() : nullptr, (int)cl.numel,
+                                (int)bt.shape[1], block_size, device_error_flag(), ctx().stream);
+    p.bt = p.bt_tmp ? p.bt_tmp->i32() : bt.i32();
+    p.cl = p.cl_tmp ? p.cl_tmp->i32() : cl.i32();
+    return p;
+}
+
 }  // namespace
 
 TensorNode HipBackend::new_cpu(const float *data, const std::vector<size_t> &shape) {
@@ -266,8 +302,9 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
                                       float scale, Tensor &out) {
     need_f32(q, "q");
     need_f32(kv, "kv_cache");
-    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
-                  "block_tables and context_lens must be int32 tensors");
+    CLOVE_REQUIRE((bt.dtype == CLOVE_HIP_I32 || bt.dtype == CLOVE_HIP_F32) &&
+                      (cl.dtype == CLOVE_HIP_I32 || cl.dtype == CLOVE_HIP_F32),
+                  CLOVE_HIP_ERR_INVALID, "block_tables and context_lens must be int32 or f32 tensors");
     CLOVE_REQUIRE(kv.shape.size() == 5 && kv.shape[0] == 2, CLOVE_HIP_ERR_SHAPE,
                   "kv_cache must be [2, num_blocks, block_size, heads, head_dim], got " +
                       shape_str(kv.shape));
@@ -295,6 +332,7 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
                   "context capacity exceeds 2^31 tokens");
     if (B == 0) return;
     Context &c = ctx();
+    const IndexPair idx = index_pair(bt, cl, (int)bs);
 
     k::PagedArgs a{};
     a.q = q.f32();
@@ -302,8 +340,8 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
     a.v_new = vn ? vn->f32() : nullptr;
     a.k_cache = kv.f32();
     a.v_cache = kv.f32() + nb * bs * H * D;
-    a.block_tables = bt.i32();
-    a.context_lens = cl.i32();
+    a.block_tables = idx.bt;
+    a.context_lens = idx.cl;
     a.out = out.f32();
     a.err_flag = device_error_flag();
     a.num_blocks = (int64_t)nb;
@@ -323,8 +361,8 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
         a.partials = work->f32();
     }
     k::paged_attention(a, c.stream);
-    // `work` returns to the allocator here; later users of the block are
-    // ordered after these kernels on the same stream.
+    // `work` and the index temporaries return to the allocator here; later
+    // users of those blocks are ordered after these kernels on the same stream.
 }
 
 TensorNode HipBackend::paged_attention(const TensorNode &q_, const TensorNode &k_,
@@ -341,16 +379,18 @@ TensorNode HipBackend::paged_gather_indices(const TensorNode &bt_, const TensorN
                                             int block_size, int max_ctx) {
     const Tensor &bt = need(bt_, "block_tables");
     const Tensor &cl = need(cl_, "context_lens");
-    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
-                  "block_tables and context_lens must be int32 tensors");
     CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == cl.numel, CLOVE_HIP_ERR_SHAPE,
                   "block_tables must be [num_seqs, max_blocks]");
     CLOVE_REQUIRE(block_size > 0 && max_ctx >= 0, CLOVE_HIP_ERR_INVALID,
                   "block_size must be > 0 and max_ctx >= 0");
+    CLOVE_REQUIRE(bt.shape[1] * (size_t)block_size < (1ull << 31) &&
+                      cl.numel * (size_t)max_ctx < (1ull << 40),
+                  CLOVE_HIP_ERR_SHAPE, "gather indices: sizes exceed the index range");
     const size_t B = cl.numel;
+    const IndexPair idx = index_pair(bt, cl, block_size);
     TensorNode out = new_tensor({B, (size_t)max_ctx}, CLOVE_HIP_I32);
-    k::paged_slots(bt.i32(), cl.i32(), out->i32(), (int)B, (int)bt.shape[1], block_size, max_ctx,
-                   ctx().stream);
+    k::paged_slots(idx.bt, idx.cl, out->i32(), (int)B, (int)bt.shape[1], block_size, max_ctx,
+                   device_error_flag(), ctx().stream);
     return out;
 }
 
@@ -376,8 +416,9 @@ void HipBackend::paged_kv_append(const Tensor &kv, const Tensor &k, const Tensor
     need_f32(kv, "kv_cache");
     need_f32(k, "k");
     need_f32(v, "v");
-    CLOVE_REQUIRE(bt.dtype == CLOVE_HIP_I32 && cl.dtype == CLOVE_HIP_I32, CLOVE_HIP_ERR_INVALID,
-                  "block_tables and context_lens must be int32 tensors");
+    CLOVE_REQUIRE((bt.dtype == CLOVE_HIP_I32 || bt.dtype == CLOVE_HIP_F32) &&
+                      (cl.dtype == CLOVE_HIP_I32 || cl.dtype == CLOVE_HIP_F32),
+                  CLOVE_HIP_ERR_INVALID, "block_tables and context_lens must be int32 or f32 tensors");
     CLOVE_REQUIRE(kv.shape.size() == 5 && kv.shape[0] == 2, CLOVE_HIP_ERR_SHAPE,
                   "kv_cache must be [2, num_blocks, block_size, heads, head_dim], got " +
                       shape_str(kv.shape));
@@ -394,7 +435,8 @@ void HipBackend::paged_kv_append(const Tensor &kv, const Tensor &k, const Tensor
     CLOVE_REQUIRE(bt.shape[1] * bs < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
                   "context capacity exceeds 2^31 tokens");
     if (B == 0) return;
-    k::paged_append(kv.f32(), kv.f32() + nb * bs * row, k.f32(), v.f32(), bt.i32(), cl.i32(),
+    const IndexPair idx = index_pair(bt, cl, (int)bs);
+    k::paged_append(kv.f32(), kv.f32() + nb * bs * row, k.f32(), v.f32(), idx.bt, idx.cl,
                     (int)B, (int)bt.shape[1], (int)bs, (int64_t)nb, (int)row, device_error_flag(),
                     ctx().stream);
 }

@@ -207,10 +207,17 @@ void synchronize() {
     CLOVE_HIP_CHECK(hipMemcpy(&flag, g_err_flag, 4, hipMemcpyDeviceToHost));
     if (flag) {
         CLOVE_HIP_CHECK(hipMemset(g_err_flag, 0, 4));
-        fail(CLOVE_HIP_ERR_RANGE,
-             "an earlier call met an index out of range: a block-table entry outside the KV "
-             "pool (those tokens were skipped) or a cross-entropy target >= the number of "
-             "classes (that row counted 0)");
+        std::string msg = "an earlier call met an index out of range:";
+        if (flag & k::kErrPagedRange)
+            msg += " a block-table entry outside the KV pool or a context length past the "
+                   "table (those tokens were skipped);";
+        if (flag & k::kErrClassRange)
+            msg += " a cross-entropy target >= the number of classes (that row counted 0);";
+        if (flag & k::kErrIndexValue)
+            msg += " an f32 block_tables/context_lens value that is not an integer in "
+                   "[0, 2^24) (read as -1: its tokens were skipped);";
+        msg.pop_back();
+        fail(CLOVE_HIP_ERR_RANGE, msg);
     }
 }
 

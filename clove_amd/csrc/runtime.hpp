@@ -41,6 +41,12 @@ struct ChainOp {
 // is not elementwise.
 int ew_arity(int opcode);
 
+// Checks a chain's structure: 1..CL_MAX_OPS elementwise ops, 1..CL_MAX_IN
+// inputs, every operand an earlier op or an existing input, at most
+// CL_MAX_OUT stored values (the last op always is).  Returns the number of
+// stored values; fails with CLOVE_HIP_ERR_INVALID otherwise.
+int validate_chain(const std::vector<ChainOp> &ops, size_t n_inputs);
+
 // Evaluates `ops` over the index space [0, numel) and writes the stored ops
 // into `outs` (one pre-allocated f32 tensor of at least numel elements per
 // stored op, in op order).
@@ -101,6 +107,12 @@ struct HipBackend {
                                       const TensorNode &v, int num_heads, int q_pos, int k_pos,
                                       int flags, float scale);
     static TensorNode rope(const TensorNode &x, size_t pos_offset, size_t head_dim);
+    static void rope_into(const Tensor &x, size_t pos_offset, size_t head_dim, Tensor &out);
+    // RoPE at (q_pos, k_pos); key t is hidden from query s when causal and
+    // t + mask_k > s + mask_q.
+    static void flash_attention_into(const Tensor &q, const Tensor &k, const Tensor &v,
+                                     int num_heads, int q_pos, int k_pos, int mask_q, int mask_k,
+                                     int flags, float scale, Tensor &out);
     // optim.rs:375-395: one AdamW step in place on every (w, g, m, v).
     struct AdamWParams {
         float lr, beta1, beta2, eps, weight_decay, loss_scale, clip;

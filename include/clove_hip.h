@@ -69,7 +69,9 @@ enum clove_hip_opcode {
     CLOVE_OP_CAST = 16,        /* identity on f32 data, lazy.rs:1808-1814 */
     CLOVE_OP_SIGMOID = 17,
     CLOVE_OP_TANH = 18,
-    CLOVE_OP_PAGED_ATTENTION = 19 /* deps: q, k, v, kv_cache, block_tables, context_lens */
+    CLOVE_OP_PAGED_ATTENTION = 19, /* deps: q, k, v, kv_cache, block_tables, context_lens */
+    CLOVE_OP_ROPE = 20         /* RoPE(pos_offset, head_dim), backend.rs:111; deps: x.
+                                  Added with clove_hip_graph_rope (two integer parameters) */
 };
 
 /* ---------------------------------------------------------------------- */
@@ -299,6 +301,17 @@ int clove_hip_graph_input(clove_hip_graph *g, const char *shape);
 /* Adds an op node over earlier node ids; the output shape follows the op's
  * rule.  Returns the node id or a negative status. */
 int clove_hip_graph_op(clove_hip_graph *g, int opcode, const int *deps, int n_deps, float param);
+/* Adds RoPE(pos_offset, head_dim) over node x: the LazyBackend trace of
+ * rope (lazy.rs:475-480, Opcode::RoPE at backend.rs:111); x's shape.  On its
+ * own it runs as clove_hip_rope does.  The planner fuses
+ *   MatMul(Softmax(MatMul([ScalarMul(s)](RoPE(q, pq, D)), RoPE(k, pk, D))), v)
+ * into one attention step (the FlashAttention pattern, lazy.rs:1621-1690,
+ * with the contract of its kernel, lazy.rs:4821-4909): q [S, H*D] and k, v
+ * [Sk, H*D] hold one token per row, H = hidden / D heads, q rotated at
+ * s + pq and k at t + pk, keys t > s masked (on row indices, as the
+ * reference kernel does), softmax scale s (1/sqrt(D) without a ScalarMul).
+ * Returns the node id or a negative status. */
+int clove_hip_graph_rope(clove_hip_graph *g, int x, size_t pos_offset, size_t head_dim);
 /* Dead-code elimination, constant folding, fusion planning, liveness-based
  * buffer assignment and kernel compilation for the given outputs. */
 clove_hip_model *clove_hip_compile(clove_hip_graph *g, const int *outputs, int n_outputs);

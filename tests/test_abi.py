@@ -203,3 +203,178 @@ def test_symbolic_shapes_parse_and_reject():
         g.op("matmul", 0)             # wrong operand count
     with pytest.raises(ca.CloveError):
         g.op("add", 0, 99)            # unknown node
+
+
+# ---------------------------------------------------------------------------
+# fused-chain structure checks (before any operand is followed), CPU only
+# ---------------------------------------------------------------------------
+
+def _chain_status(ops, n_inputs=1):
+    lib = ca.lib()
+    arr = (ca.ChainOp * len(ops))()
+    for i, (name, s0, s1) in enumerate(ops):
+        arr[i] = ca.ChainOp(ca.OP[name.upper()], s0, s1, 0, 0.0)
+    ins = (C.c_void_p * n_inputs)()          # NULL handles: structure is checked first
+    outs = (C.c_void_p * len(ops))()
+    return lib.clove_hip_fused_chain(arr, len(ops), ins, n_inputs, outs), ca.last_error()
+
+
+@pytest.mark.parametrize("ops", [
+    [("relu", 0, 0)],                 # its own value: would loop forever
+    [("relu", 5, 0)],                 # a later op
+    [("relu", -3, 0)],                # input 2 of 1
+    [("relu", -1, 0), ("add", 0, 1)],  # the second operand names the op itself
+    [("relu", -2147483648, 0)],       # INT_MIN: -(src + 1) must not overflow
+])
+def test_fused_chain_rejects_bad_operands(ops):
+    rc, msg = _chain_status(ops)
+    assert rc == -ca.ERR_INVALID
+    assert "neither an earlier op nor an input" in msg
+
+
+def test_fused_chain_checks_structure_before_handles():
+    # a well-formed chain gets as far as the (NULL) input handle
+    rc, msg = _chain_status([("relu", -1, 0), ("add", 0, -1)])
+    assert rc == -ca.ERR_INVALID and "input is NULL" in msg
+    rc, msg = _chain_status([("softmax", -1, 0)])
+    assert rc == -ca.ERR_INVALID and "not elementwise" in msg
+
+
+# ---------------------------------------------------------------------------
+# planner: chain launch limits, RoPE and the FlashAttention pattern
+# ---------------------------------------------------------------------------
+
+def _step_io(model):
+    """(name, ins, outs) per step from describe()."""
+    out = []
+    for line in model.describe().strip().splitlines()[:-1]:
+        name = line.split(" ")[0]
+        ins = line[line.index("in=(") + 4:line.index(")", line.index("in=("))]
+        outs = line[line.index("out=(") + 5:line.rindex(")")]
+        out.append((name, [int(x) for x in ins.split(",") if x],
+                    [int(x) for x in outs.split(",") if x]))
+    return out
+
+
+def test_plan_splits_chains_at_sixteen_inputs():
+    # a sum of 20 inputs: one chain would need 20 inputs, run_chain takes 16
+    g = ca.Graph()
+    xs = [g.input("64,64") for _ in range(20)]
+    acc = xs[0]
+    for x in xs[1:]:
+        acc = g.op("add", acc, x)
+    m = g.compile([acc])
+    io = _step_io(m)
+    assert len(io) == 2 and all(n.startswith("Fused") for n, _, _ in io)
+    assert all(len(ins) <= 16 and len(outs) <= 16 for _, ins, outs in io)
+    # the first chain's last value feeds the second chain
+    assert io[0][2][-1] in io[1][1]
+
+
+def test_plan_splits_chains_at_sixteen_stores():
+    # a 20-op chain whose every value is requested: at most 16 stores per launch
+    g = ca.Graph()
+    x = g.input("128")
+    vals, v = [], x
+    for i in range(20):
+        v = g.op("sin" if i % 2 else "cos", v)
+        vals.append(v)
+    m = g.compile(vals)
+    io = _step_io(m)
+    assert len(io) == 2
+    assert all(len(outs) <= 16 for _, _, outs in io)
+    stored = [o for _, _, outs in io for o in outs]
+    assert sorted(stored) == sorted(vals)
+
+
+def attention_graph(S=64, X=128, D=64, q_pos=3, k_pos=5, scale=True, sk=None):
+    g = ca.Graph()
+    q = g.input(f"{S},{X}")
+    k = g.input(f"{sk or S},{X}")
+    v = g.input(f"{sk or S},{X}")
+    qr = g.rope(q, D, q_pos)
+    kr = g.rope(k, D, k_pos)
+    qs = g.op("scalar_mul", qr, param=1.0 / np.sqrt(D)) if scale else qr
+    y = g.op("matmul", g.op("softmax", g.op("matmul", qs, kr)), v)
+    return g, (q, k, v, qr, kr, qs), y
+
+
+def test_plan_flash_attention_pattern():
+    # lazy.rs:1621-1690: MatMul(Softmax(MatMul(ScalarMul(RoPE q), RoPE k)), v)
+    # is one step reading the un-rotated q, k and v
+    g, (q, k, v, *_), y = attention_graph()
+    m = g.compile([y])
+    io = _step_io(m)
+    assert [n for n, _, _ in io] == ["FlashAttention(q_pos=3,k_pos=5,head_dim=64,causal)"]
+    assert io[0][1] == [q, k, v] and io[0][2] == [y]
+    # without the ScalarMul (the reference's kernel scales by 1/sqrt(D) anyway)
+    g, (q, k, v, *_), y = attention_graph(scale=False)
+    assert _step_io(g.compile([y]))[0][1] == [q, k, v]
+
+
+def test_plan_flash_attention_non_matches():
+    # no RoPE on k: planned op by op
+    g = ca.Graph()
+    q, k, v = g.input("64,128"), g.input("128,64"), g.input("64,128")
+    y = g.op("matmul", g.op("softmax", g.op("matmul", g.rope(q, 64), k)), v)
+    assert steps(g.compile([y])) == ["RoPE(0,64)", "MatMul+Softmax", "MatMul"]
+    # head_dim without an attention kernel (32)
+    g, _, y = attention_graph(D=32)
+    assert "FlashAttention" not in g.compile([y]).describe()
+    # the scores are requested too: they must be materialised
+    g, _, y = attention_graph()
+    scores = y - 1
+    assert "FlashAttention" not in g.compile([y, scores]).describe()
+    # different head dims on q and k
+    g = ca.Graph()
+    q, k, v = g.input("64,128"), g.input("64,128"), g.input("64,128")
+    y = g.op("matmul", g.op("softmax", g.op("matmul", g.rope(q, 64), g.rope(k, 128))), v)
+    assert "FlashAttention" not in g.compile([y]).describe()
+
+
+def test_plan_flash_attention_keeps_shared_nodes():
+    # the rotated k is also an output: its RoPE keeps a step of its own, and
+    # the fused step still reads the un-rotated k
+    g, (q, k, v, qr, kr, qs), y = attention_graph()
+    m = g.compile([y, kr])
+    io = _step_io(m)
+    names = [n for n, _, _ in io]
+    assert names[0] == "RoPE(5,64)" and names[1].startswith("FlashAttention")
+    assert io[1][1] == [q, k, v]
+
+
+def test_plan_flash_attention_same_input_for_q_and_k():
+    # self-attention on one tensor: q and k are the same node; its buffer is
+    # released once (a duplicate release would hand one buffer to two values)
+    g = ca.Graph()
+    x, v = g.input("64,128"), g.input("64,128")
+    y = g.op("matmul", g.op("softmax", g.op("matmul", g.rope(x, 64, 2), g.rope(x, 64, 2))), v)
+    z = g.op("relu", y)
+    m = g.compile([z])
+    assert steps(m)[0].startswith("FlashAttention") and steps(m)[1] == "Fused[ReLU]"
+
+
+def test_plan_matmul_of_a_node_with_itself():
+    # MatMul(a, a) reads a twice: a's buffer is released once, so the two
+    # values planned after it get different buffers
+    g = ca.Graph()
+    x = g.input("16,16")
+    a = g.op("relu", x)
+    p = g.op("matmul", a, a)
+    s1 = g.op("sin", p)
+    s2 = g.op("cos", p)
+    y = g.op("matmul", s1, s2)
+    m = g.compile([y])
+    assert "vbufs=3" in m.describe(), m.describe()
+
+
+def test_graph_rope_rejects_bad_parameters():
+    g = ca.Graph()
+    x = g.input("4,8")
+    for hd in (0, 3, 258):
+        with pytest.raises(ca.CloveError):
+            g.rope(x, hd)
+    with pytest.raises(ca.CloveError):
+        g.rope(99, 8)
+    with pytest.raises(ca.CloveError):
+        g.op("rope", x)          # two integer parameters: only through graph_rope

@@ -284,3 +284,124 @@ def test_horizontal_matmul_group(hip):
             assert_close(got, w_, 1e-4, 1e-7, "softmax head member")
         else:
             assert_close(got, w_, 2e-3, 1e-4 * float(np.abs(w_).max()), f"member {i}")
+
+
+# ---------------------------------------------------------------------------
+# chains past one launch's limits (16 inputs, 16 stored values)
+# ---------------------------------------------------------------------------
+
+def test_sum_of_twenty_inputs(hip):
+    g = hip.Graph()
+    xs = rng(40).standard_normal((20, 64, 96)).astype(np.float32)
+    ids = [g.input("64,96") for _ in range(20)]
+    acc = ids[0]
+    for i in ids[1:]:
+        acc = g.op("add", acc, i)
+    m = g.compile([acc])
+    assert m.num_steps == 2
+    (got,) = m.execute([hip.tensor(x) for x in xs])
+    want = xs[0]
+    for x in xs[1:]:
+        want = oracle.add(want, x)      # the same sequential f32 order
+    assert np.array_equal(got.numpy(), want)
+
+
+def test_twenty_requested_values_of_one_chain(hip):
+    g = hip.Graph()
+    x = rng(41).standard_normal((33, 17)).astype(np.float32)
+    xi = g.input("33,17")
+    ids, v = [], xi
+    for i in range(20):
+        v = g.op("sin" if i % 2 else "cos", v)
+        ids.append(v)
+    m = g.compile(ids)
+    outs = m.execute([hip.tensor(x)])
+    want = x
+    for i, o in enumerate(outs):
+        want = oracle.sin(want) if i % 2 else oracle.cos(want)
+        assert_close(o.numpy(), want, 1e-5, 1e-6, f"value {i}")
+
+
+# ---------------------------------------------------------------------------
+# the FlashAttention pattern (lazy.rs:1621-1690) as one planned step
+# ---------------------------------------------------------------------------
+
+def attention_plan(hip, S, Sk, X, D, q_pos, k_pos, scale):
+    g = hip.Graph()
+    q, k, v = g.input(f"{S},{X}"), g.input(f"{Sk},{X}"), g.input(f"{Sk},{X}")
+    qr, kr = g.rope(q, D, q_pos), g.rope(k, D, k_pos)
+    qs = g.op("scalar_mul", qr, param=scale) if scale else qr
+    y = g.op("matmul", g.op("softmax", g.op("matmul", qs, kr)), v)
+    m = g.compile([y])
+    assert m.num_steps == 1 and m.describe().startswith("FlashAttention"), m.describe()
+    return m
+
+
+def attention_want(q, k, v, D, q_pos, k_pos, scale, rows=None):
+    """The reference kernel's contract (lazy.rs:4821-4909): q and k rotated
+    at their RoPE positions, keys after the query's row masked."""
+    qr, kr = oracle.rope(q, D, q_pos), oracle.rope(k, D, k_pos)
+    return oracle.attention(qr, kr, v, q.shape[-1] // D, 0, 0, oracle.ATTN_CAUSAL,
+                            scale or None, rows=rows)
+
+
+@pytest.mark.parametrize("S,Sk,X,D,q_pos,k_pos,scale", [
+    (64, 64, 64, 64, 0, 0, 0.125),        # one head, MultiHeadAttention's scale
+    (130, 130, 256, 128, 3, 3, None),     # two heads, no ScalarMul: 1/sqrt(D)
+    (100, 100, 192, 64, 5, 17, 0.2),      # different rotation positions, own scale
+    (33, 70, 128, 64, 0, 9, 1.0),         # more keys than queries
+])
+def test_graph_flash_attention(hip, S, Sk, X, D, q_pos, k_pos, scale):
+    g = rng(S * 3 + Sk + X + D)
+    q = g.standard_normal((S, X)).astype(np.float32)
+    k = g.standard_normal((Sk, X)).astype(np.float32)
+    v = g.standard_normal((Sk, X)).astype(np.float32)
+    m = attention_plan(hip, S, Sk, X, D, q_pos, k_pos, scale)
+    (got,) = m.execute([hip.tensor(a) for a in (q, k, v)])
+    want = attention_want(q, k, v, D, q_pos, k_pos, scale)
+    assert_close(got.numpy(), want, 2e-3, 1e-5, f"attention plan S={S} Sk={Sk} X={X} D={D}")
+
+
+def test_graph_flash_attention_equals_eager_bits(hip):
+    """With equal positions the index mask is the position mask, so the
+    planned step and the eager entry give the same bits."""
+    g = rng(77)
+    q, k, v = (g.standard_normal((257, 256)).astype(np.float32) for _ in range(3))
+    m = attention_plan(hip, 257, 257, 256, 128, 11, 11, None)
+    t = hip.tensor
+    (got,) = m.execute([t(q), t(k), t(v)])
+    eager = hip.flash_attention(t(q), t(k), t(v), 2, 11, 11, hip.ATTN_CAUSAL | hip.ATTN_ROPE)
+    assert np.array_equal(got.numpy(), eager.numpy())
+
+
+def test_graph_flash_attention_4096_sampled(hip):
+    """S = 4096, hidden 4096 = 32 heads of 128: sampled query rows of every
+    head against the oracle."""
+    g = rng(78)
+    S, X, D = 4096, 4096, 128
+    q, k, v = (g.standard_normal((S, X)).astype(np.float32) for _ in range(3))
+    m = attention_plan(hip, S, S, X, D, 0, 0, float(1 / np.sqrt(np.float32(D))))
+    (got,) = m.execute([hip.tensor(a) for a in (q, k, v)])
+    got = got.numpy()
+    for lo, hi in ((0, 2), (127, 130), (2047, 2049), (4094, 4096)):
+        want = attention_want(q, k, v, D, 0, 0, float(1 / np.sqrt(np.float32(D))),
+                              rows=(lo, hi))
+        assert_close(got[lo:hi], want[lo:hi], 2e-3, 1e-5, f"rows {lo}..{hi}")
+
+
+def test_graph_attention_non_match_runs_op_by_op(hip):
+    """Without RoPE on k the nodes run one by one with the matmul rule (k is
+    [D, Sk], the keys transposed), the graph's literal meaning."""
+    g = rng(79)
+    q = g.standard_normal((64, 128)).astype(np.float32)
+    kt = g.standard_normal((128, 64)).astype(np.float32)
+    v = g.standard_normal((64, 128)).astype(np.float32)
+    gr = hip.Graph()
+    qi, ki, vi = gr.input("64,128"), gr.input("128,64"), gr.input("64,128")
+    y = gr.op("matmul", gr.op("softmax", gr.op("matmul", gr.rope(qi, 64, 2), ki)), vi)
+    m = gr.compile([y])
+    assert "FlashAttention" not in m.describe()
+    (got,) = m.execute([hip.tensor(a) for a in (q, kt, v)])
+    scores = oracle.softmax(oracle.matmul(oracle.rope(q, 64, 2), kt))
+    want = oracle.matmul(scores, v)
+    assert_close(got.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "op by op")

@@ -50,22 +50,19 @@ def test_matmul_identity_is_exact(hip):
 
 def test_config4_full(hip):
     """Config 4: C = A.B at M=N=K=4096 and the skinny M=32 case, A and B
-    normal(0, 1/sqrt(K)), seed 3.  The oracle checks sampled row blocks of
-    the square product (it is a sequential CPU kernel) and all of the
-    skinny one."""
+    normal(0, 1/sqrt(K)), seed 3.  Every element of both products is checked
+    against the oracle (rayon_matmul restated: a few seconds on the host's
+    cores for the square one), and the square one also against float64."""
     g = rng(3)
     K = 4096
     a = g.normal(0, 1 / np.sqrt(K), (4096, K)).astype(np.float32)
     b = g.normal(0, 1 / np.sqrt(K), (K, 4096)).astype(np.float32)
     tb = hip.tensor(b)
     got = hip.matmul(hip.tensor(a), tb).numpy()
-    for r0 in (0, 2048 + 64, 4096 - 32):
-        want = oracle.matmul(a, b, rows=(r0, r0 + 32))[r0:r0 + 32]
-        check(got[r0:r0 + 32], want, f"4096^3 rows {r0}..")
-    # every element against a float64 product, with a K-scaled bound
-    sub = slice(0, 4096, 97)
-    ref64 = a[sub].astype(np.float64) @ b.astype(np.float64)
-    assert np.max(np.abs(got[sub] - ref64)) < 1e-5
+    check(got, oracle.matmul(a, b), "4096^3")
+    # float64 with a bound of a few ulps of the K-term sum's scale
+    ref64 = a.astype(np.float64) @ b.astype(np.float64)
+    assert np.max(np.abs(got - ref64)) < 1e-5
     a32 = a[:32].copy()
     check(hip.matmul(hip.tensor(a32), tb).numpy(), oracle.matmul(a32, b), "skinny 32x4096x4096")
 

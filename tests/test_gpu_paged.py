@@ -111,31 +111,72 @@ def test_shape_errors(hip):
         run(hip, q[:, :64], None, None, kv, bt, cl)
 
 
-def test_config5_full(hip):
+@pytest.fixture(scope="module")
+def config5(hip):
     """Config 5: B=32, H=32, D=128, block 16, ctx ~ U[512, 4096], tables from
     a seeded permutation of a 16,384-block pool, Q/K/V normal(0,1), seed 4,
-    scale 1/sqrt(128).  The 8 GiB pool is filled on the device; the oracle
-    checks four whole sequences (all heads) on a compact copy of the blocks
-    they use, and every output is checked against the f64 evaluation for
-    finiteness and scale."""
+    scale 1/sqrt(128).  The 8 GiB pool is filled on the device."""
     P = workloads.PAGED
     B, H, D, bs, nb = P["num_seqs"], P["num_heads"], P["head_dim"], P["block_size"], P["pool_blocks"]
     ctx, bt = workloads.paged_layout(4)
     kv = hip.empty((2, nb, bs, H, D)).fill_normal(4)
     q = rng(4).standard_normal((B, H * D), dtype=np.float32)
-    tq, tbt, tcl = hip.tensor(q), hip.tensor(bt), hip.tensor(ctx)
-    out = hip.paged_attention(tq, None, None, kv, tbt, tcl).numpy()
-    assert np.all(np.isfinite(out))
-    plane = nb * bs * H * D
-    blk = bs * H * D
+    out = hip.paged_attention(hip.tensor(q), None, None, kv, hip.tensor(bt),
+                              hip.tensor(ctx)).numpy()
+    yield dict(B=B, H=H, D=D, bs=bs, nb=nb, ctx=ctx, bt=bt, kv=kv, q=q, out=out)
+    kv.free()
+
+
+def test_config5_full(hip, config5):
+    """Every sequence of config 5 (all heads) against the oracle, in batches
+    of 8 sequences on compact copies of the blocks they use (the gather reads
+    the same rows, so this equals the full pool)."""
+    c = config5
+    B, H, D, bs, nb, kv = c["B"], c["H"], c["D"], c["bs"], c["nb"], c["kv"]
+    plane, blk = nb * bs * H * D, bs * H * D
 
     def read_block(p, b):
         return kv.read(p * plane + b * blk, blk).reshape(bs, H, D)
 
-    seqs = [int(np.argmin(ctx)), int(np.argmax(ctx)), 7, 19]
-    pool, sbt, scl = workloads.compact_pool(read_block, bt, ctx, seqs, bs)
-    want = oracle.paged_attention(q[seqs], None, None, pool, sbt, scl).reshape(len(seqs), H * D)
-    assert_close(out[seqs], want, RTOL, ATOL, "config5 sampled sequences")
+    assert np.all(np.isfinite(c["out"]))
+    for lo in range(0, B, 8):
+        seqs = list(range(lo, min(B, lo + 8)))
+        pool, sbt, scl = workloads.compact_pool(read_block, c["bt"], c["ctx"], seqs, bs)
+        want = oracle.paged_attention(c["q"][seqs], None, None, pool, sbt, scl)
+        assert_close(c["out"][seqs], want.reshape(len(seqs), H * D), RTOL, ATOL,
+                     f"config5 sequences {seqs[0]}..{seqs[-1]}")
+
+
+def test_config5_gather_indices_bit_exact(hip, config5):
+    """The slots of every token of the config-5 tables, bit for bit against
+    the integer closed form (lazy.rs:5262-5270)."""
+    c = config5
+    tbt, tcl = hip.tensor(c["bt"]), hip.tensor(c["ctx"])
+    max_ctx = int(c["ctx"].max())
+    got = hip.paged_gather_indices(tbt, tcl, c["bs"], max_ctx).numpy()
+    want = oracle.paged_slots(c["bt"], c["ctx"], c["bs"], max_ctx)
+    assert np.array_equal(got, want)
+    # every slot lies in the pool, and the used slots are distinct
+    used = got[got >= 0]
+    assert used.max() < c["nb"] * c["bs"] and np.unique(used).size == used.size
+
+
+def test_config5_f32_tables_equal_int32_tables(hip, config5):
+    """Clove builds every tensor from a Vec<f32> (backend.rs:176), so
+    nn::PagedAttention passes its block tables and context lengths as f32
+    tensors (nn.rs:528-546).  At config 5 they give the int32 result bit for
+    bit; the -1 padding past each sequence's blocks is never read, so it is
+    no error."""
+    c = config5
+    f32 = lambda a: hip.tensor(np.asarray(a, np.float32), dtype=np.float32)
+    out = hip.paged_attention(hip.tensor(c["q"]), None, None, c["kv"], f32(c["bt"]),
+                              f32(c["ctx"])).numpy()
+    hip.synchronize()  # no index was reported
+    assert np.array_equal(out, c["out"])
+    got = hip.paged_gather_indices(f32(c["bt"]), f32(c["ctx"]), c["bs"],
+                                   int(c["ctx"].max())).numpy()
+    assert np.array_equal(got, oracle.paged_slots(c["bt"], c["ctx"], c["bs"],
+                                                  int(c["ctx"].max())))
 
 
 def test_kv_append_then_cached_decode_equals_new_token_decode(hip):
@@ -162,3 +203,75 @@ def test_kv_append_skips_empty_and_reports_bad_entries(hip):
     with pytest.raises(hip.CloveError) as e:
         hip.synchronize()
     assert e.value.code == hip.ERR_RANGE
+
+
+def f32t(hip, a):
+    return hip.tensor(np.asarray(a, np.float32), dtype=np.float32)
+
+
+@pytest.mark.parametrize("where,value", [
+    ("table", 3.5), ("table", -1.0), ("table", float(1 << 24)), ("table", float("nan")),
+    ("ctx", 2.5), ("ctx", -1.0), ("ctx", float("inf")),
+])
+def test_f32_index_values_must_be_integers(hip, where, value):
+    """A used table entry or a context length that is not an integer in
+    [0, 2^24) is reported as CLOVE_HIP_ERR_RANGE by the next synchronising
+    call; that sequence's bad tokens are skipped and the others are exact."""
+    q, kn, vn, kv, bt, cl = make(12, 2, 2, 64, 16, 20, 4, [40, 40])
+    btf, clf = bt.astype(np.float32), cl.astype(np.float32)
+    if where == "table":
+        btf[1, 1] = value
+    else:
+        clf[1] = value
+    out = hip.paged_attention(hip.tensor(q), None, None, hip.tensor(kv), f32t(hip, btf),
+                              f32t(hip, clf))
+    with pytest.raises(hip.CloveError) as e:
+        hip.synchronize()
+    assert e.value.code == hip.ERR_RANGE and "f32 block_tables/context_lens" in str(e.value)
+    want = oracle.paged_attention(q[:1], None, None, kv, bt[:1], cl[:1]).reshape(1, 128)
+    assert_close(out.numpy()[:1], want, RTOL, ATOL, "unaffected sequence")
+    hip.synchronize()
+
+
+def test_f32_unused_table_entries_are_not_checked(hip):
+    q, kn, vn, kv, bt, cl = make(13, 2, 2, 64, 16, 20, 4, [17, 40])
+    btf = bt.astype(np.float32)
+    btf[0, 2:] = [0.5, -3.0]          # sequence 0 uses blocks 0 and 1 only
+    got = hip.paged_attention(hip.tensor(q), None, None, hip.tensor(kv), f32t(hip, btf),
+                              f32t(hip, cl)).numpy()
+    hip.synchronize()
+    want = run(hip, q, None, None, kv, bt, cl)
+    assert np.array_equal(got, want)
+
+
+def test_f32_tables_in_kv_append_and_graph(hip):
+    """The append and the lazy graph's PagedAttention step take f32 tables
+    too, with the int32 results."""
+    q, kn, vn, kv, bt, cl = make(14, 4, 4, 128, 16, 200, 32, [1, 16, 17, 300])
+    t = hip.tensor
+    tkv = t(kv)
+    hip.paged_kv_append(tkv, t(kn), t(vn), f32t(hip, bt), f32t(hip, cl))
+    assert np.array_equal(tkv.numpy(), oracle.paged_kv_append(kv, kn, vn, bt, cl))
+    g = hip.Graph()
+    ids = [g.input(s) for s in ("4,512", "4,512", "4,512", "2,200,16,4,128", "4,32", "4")]
+    y = g.op("paged_attention", *ids)
+    m = g.compile([y])
+    got = m.execute([t(q), t(kn), t(vn), t(kv), f32t(hip, bt), f32t(hip, cl)])[0].numpy()
+    want = run(hip, q, kn, vn, kv, bt, cl)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("entry", [-5, (1 << 31) - 1, (1 << 28)])
+def test_gather_indices_bad_entries_give_minus_one(hip, entry):
+    """A negative entry, or one whose slots overflow int32, gives -1 (never a
+    wrapped or negative slot) and CLOVE_HIP_ERR_RANGE at the next sync."""
+    bt = np.array([[3, entry], [4, 5]], np.int32)
+    cl = np.array([20, 20], np.int32)
+    out = hip.paged_gather_indices(hip.tensor(bt), hip.tensor(cl), 16, 20)
+    with pytest.raises(hip.CloveError) as e:
+        hip.synchronize()
+    assert e.value.code == hip.ERR_RANGE
+    got = out.numpy()
+    assert np.array_equal(got[0, :16], 48 + np.arange(16))
+    assert np.all(got[0, 16:] == -1)
+    assert np.array_equal(got[1], oracle.paged_slots(bt[1:], cl[1:], 16, 20)[0])
