@@ -106,6 +106,9 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_paged_attention": (vp, [vp, vp, vp, vp, vp, vp]),
         "clove_hip_paged_attention_scaled": (vp, [vp, vp, vp, vp, vp, vp, f]),
         "clove_hip_paged_gather_indices": (vp, [vp, vp, C.c_int, C.c_int]),
+        "clove_hip_paged_attention_noalloc": (C.c_int, [vp, vp, vp, vp, C.c_int64, C.c_int,
+                                                        C.c_int, C.c_int, vp, C.c_int, vp,
+                                                        C.c_int, f, vp]),
         "clove_hip_paged_kv_append": (C.c_int, [vp, vp, vp, vp, vp]),
         "clove_hip_relu_backward": (vp, [vp, vp]),
         "clove_hip_gelu_backward": (vp, [vp, vp]),

@@ -285,6 +285,18 @@ CTensor clove_hip_paged_attention_scaled(CTensor q, CTensor k, CTensor v, CTenso
     });
 }
 
+int clove_hip_paged_attention_noalloc(const float *q, const float *k, const float *v,
+                                      const float *kv_cache, int64_t num_blocks, int block_size,
+                                      int num_heads, int head_dim, const int32_t *block_tables,
+                                      int max_blocks, const int32_t *context_lens, int num_seqs,
+                                      float scale, float *out) {
+    return guarded([&] {
+        HipBackend::paged_attention_noalloc({q, k, v, kv_cache, num_blocks, block_size, num_heads,
+                                             head_dim, block_tables, max_blocks, context_lens,
+                                             num_seqs, scale, out});
+    });
+}
+
 CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
                                   CTensor block_tables, CTensor context_lens) {
     return guarded_tensor([&] {

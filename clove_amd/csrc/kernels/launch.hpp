@@ -165,6 +165,12 @@ struct PagedArgs {
     int part_tokens;       // tokens per partition (multiple of block_size)
     float scale;
 };
+// The allocation-free decode's partition workspace: a static device array
+// of this many floats (16 MiB) in paged_attention.hip.  paged_scratch_address
+// returns its address on the current device (call it with each device
+// current once; the address differs per device).
+constexpr size_t kPagedScratchFloats = size_t(4) << 20;
+hipError_t paged_scratch_address(float **ptr);
 // Workspace floats needed for a given shape (0 when one partition suffices).
 size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max_ctx,
                               int part_tokens);

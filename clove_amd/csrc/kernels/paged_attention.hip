@@ -500,7 +500,22 @@ __global__ void __launch_bounds__(256) paged_index_kernel(const float *__restric
     }
 }
 
+// Partition workspace of the allocation-free decode entry
+// (clove_hip_paged_attention_noalloc): one array per GPU, alive until the
+// process ends.  Host code never names it in a launch or a copy: it takes
+// the device address once per device (paged_scratch_address) and passes that.
+// Every partial a launch's merge reads is written by the same launch's
+// partition kernel first, so nothing in it needs clearing.
+static __device__ __align__(256) float scratch[kPagedScratchFloats];
+
 }  // namespace
+
+hipError_t paged_scratch_address(float **ptr) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    *ptr = e == hipSuccess ? static_cast<float *>(p) : nullptr;
+    return e;
+}
 
 bool paged_supported(int head_dim, int block_size) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&

@@ -297,6 +297,44 @@ TensorNode HipBackend::matmul(const TensorNode &a_, const TensorNode &b_) {
 
 // ---- paged attention -----------------------------------------------------------
 
+// Checks the sizes and alignment both decode entries share and fills the
+// kernel arguments (without the workspace); *ws receives the workspace floats
+// the launch needs (0 when every context fits one partition).
+static k::PagedArgs paged_args(const HipBackend::PagedRaw &r, size_t *ws) {
+    const int64_t B = r.num_seqs, H = r.num_heads, D = r.head_dim, bs = r.block_size;
+    CLOVE_REQUIRE((int64_t)r.max_blocks * bs < (1ll << 31) && r.num_blocks * bs < (1ll << 31),
+                  CLOVE_HIP_ERR_SHAPE, "context capacity exceeds 2^31 tokens");
+    // grid: (head groups, partitions, sequences)
+    CLOVE_REQUIRE(B < 65536, CLOVE_HIP_ERR_SHAPE, "at most 65535 sequences per launch");
+    auto aligned = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    CLOVE_REQUIRE(aligned(r.q) && aligned(r.k_new) && aligned(r.v_new) && aligned(r.kv_cache) &&
+                      aligned(r.out),
+                  CLOVE_HIP_ERR_INVALID, "q, k, v, kv_cache and out must be 16-byte aligned");
+    k::PagedArgs a{};
+    a.q = r.q;
+    a.k_new = r.k_new;
+    a.v_new = r.v_new;
+    a.k_cache = r.kv_cache;
+    a.v_cache = r.kv_cache + (size_t)r.num_blocks * bs * H * D;
+    a.block_tables = r.block_tables;
+    a.context_lens = r.context_lens;
+    a.out = r.out;
+    a.err_flag = device_error_flag();
+    a.num_blocks = r.num_blocks;
+    a.num_seqs = (int)B;
+    a.num_heads = (int)H;
+    a.head_dim = (int)D;
+    a.block_size = (int)bs;
+    a.max_blocks = r.max_blocks;
+    const int cap = (int)(r.max_blocks * bs);
+    a.part_tokens = k::paged_part_tokens((int)B, (int)H, cap, (int)bs, ctx().num_cus);
+    a.max_parts = std::max(1, (cap + a.part_tokens - 1) / a.part_tokens);
+    CLOVE_REQUIRE(a.max_parts < 65536, CLOVE_HIP_ERR_SHAPE, "too many context partitions");
+    a.scale = r.scale;
+    *ws = k::paged_workspace_floats((int)B, (int)H, (int)D, cap, a.part_tokens);
+    return a;
+}
+
 void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const Tensor *vn,
                                       const Tensor &kv, const Tensor &bt, const Tensor &cl,
                                       float scale, Tensor &out) {
@@ -328,41 +366,48 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
                       "k and v must have q's number of elements");
     }
     CLOVE_REQUIRE(out.numel >= q.numel, CLOVE_HIP_ERR_SHAPE, "output too small");
-    CLOVE_REQUIRE(max_blocks * bs < (1ull << 31) && nb * bs < (1ull << 31), CLOVE_HIP_ERR_SHAPE,
-                  "context capacity exceeds 2^31 tokens");
     if (B == 0) return;
-    Context &c = ctx();
     const IndexPair idx = index_pair(bt, cl, (int)bs);
-
-    k::PagedArgs a{};
-    a.q = q.f32();
-    a.k_new = kn ? kn->f32() : nullptr;
-    a.v_new = vn ? vn->f32() : nullptr;
-    a.k_cache = kv.f32();
-    a.v_cache = kv.f32() + nb * bs * H * D;
-    a.block_tables = idx.bt;
-    a.context_lens = idx.cl;
-    a.out = out.f32();
-    a.err_flag = device_error_flag();
-    a.num_blocks = (int64_t)nb;
-    a.num_seqs = (int)B;
-    a.num_heads = (int)H;
-    a.head_dim = (int)D;
-    a.block_size = (int)bs;
-    a.max_blocks = (int)max_blocks;
-    const int cap = (int)(max_blocks * bs);
-    a.part_tokens = k::paged_part_tokens((int)B, (int)H, cap, (int)bs, c.num_cus);
-    a.max_parts = std::max(1, (cap + a.part_tokens - 1) / a.part_tokens);
-    a.scale = scale;
-    const size_t ws = k::paged_workspace_floats((int)B, (int)H, (int)D, cap, a.part_tokens);
+    size_t ws = 0;
+    k::PagedArgs a = paged_args({q.f32(), kn ? kn->f32() : nullptr, vn ? vn->f32() : nullptr,
+                                 kv.f32(), (int64_t)nb, (int)bs, (int)H, (int)D, idx.bt,
+                                 (int)max_blocks, idx.cl, (int)B, scale, out.f32()},
+                                &ws);
     TensorNode work;
     if (ws) {
         work = new_tensor({ws}, CLOVE_HIP_F32);
         a.partials = work->f32();
     }
-    k::paged_attention(a, c.stream);
+    k::paged_attention(a, ctx().stream);
     // `work` and the index temporaries return to the allocator here; later
     // users of those blocks are ordered after these kernels on the same stream.
+}
+
+// The allocation-free form: the caller's device memory, int32 indices, and
+// the partition workspace in this device's static scratch array.  Nothing
+// is allocated and nothing needs clearing (every partial the merge reads is
+// written by the same launch).  Launches on one GPU that overlap (different
+// streams) share the array and race.
+void HipBackend::paged_attention_noalloc(const PagedRaw &r) {
+    CLOVE_REQUIRE(r.num_seqs >= 0 && r.num_heads >= 1 && r.max_blocks >= 1 && r.num_blocks >= 1,
+                  CLOVE_HIP_ERR_SHAPE,
+                  "num_seqs >= 0, num_heads >= 1, max_blocks >= 1 and num_blocks >= 1 are required");
+    CLOVE_REQUIRE(k::paged_supported(r.head_dim, r.block_size), CLOVE_HIP_ERR_SHAPE,
+                  "paged attention supports head_dim 64/128/256 and block_size 8/16/32, got " +
+                      std::to_string(r.head_dim) + "/" + std::to_string(r.block_size));
+    CLOVE_REQUIRE((r.k_new == nullptr) == (r.v_new == nullptr), CLOVE_HIP_ERR_INVALID,
+                  "pass both k and v, or neither");
+    if (r.num_seqs == 0) return;
+    CLOVE_REQUIRE(r.q && r.kv_cache && r.block_tables && r.context_lens && r.out,
+                  CLOVE_HIP_ERR_INVALID, "q, kv_cache, block_tables, context_lens and out are required");
+    size_t ws = 0;
+    k::PagedArgs a = paged_args(r, &ws);
+    CLOVE_REQUIRE(ws <= k::kPagedScratchFloats, CLOVE_HIP_ERR_SHAPE,
+                  "the decode needs a " + std::to_string(ws * 4) +
+                      "-byte partition workspace; the allocation-free entry has " +
+                      std::to_string(k::kPagedScratchFloats * 4) + " bytes of scratch");
+    if (ws) a.partials = paged_scratch();
+    k::paged_attention(a, ctx().stream);
 }
 
 TensorNode HipBackend::paged_attention(const TensorNode &q_, const TensorNode &k_,

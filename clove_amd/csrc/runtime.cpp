@@ -33,6 +33,11 @@ size_t g_reserved = 0;
 std::vector<hipEvent_t> g_events;
 
 int32_t *g_err_flag = nullptr;  // device word set by kernels that saw bad indices
+
+// Device address of the paged decode's static scratch array, per device
+// ordinal (each GPU holds its own copy of the array at its own address).
+constexpr int kMaxDevices = 64;
+float *g_paged_scratch[kMaxDevices] = {};
 }  // namespace
 
 void set_last_error(const std::string &msg) { g_last_error = msg; }
@@ -158,6 +163,14 @@ void init(int device) {
                   "device ordinal " + std::to_string(device) + " out of range (" +
                       std::to_string(count) + " devices)");
     CLOVE_HIP_CHECK(hipSetDevice(device));
+    CLOVE_REQUIRE(device < kMaxDevices, CLOVE_HIP_ERR_INVALID, "device ordinal too large");
+    if (!g_paged_scratch[device]) {
+        // with `device` current: the address of this GPU's copy
+        float *p = nullptr;
+        CLOVE_HIP_CHECK(k::paged_scratch_address(&p));
+        CLOVE_REQUIRE(p != nullptr, CLOVE_HIP_ERR_HIP, "no address for the paged scratch array");
+        g_paged_scratch[device] = p;
+    }
     hipDeviceProp_t prop;
     CLOVE_HIP_CHECK(hipGetDeviceProperties(&prop, device));
     std::string arch = prop.gcnArchName;
@@ -198,6 +211,8 @@ int32_t *device_error_flag() {
     ctx();
     return g_err_flag;
 }
+
+float *paged_scratch() { return g_paged_scratch[ctx().device]; }
 
 
 void synchronize() {

@@ -16,6 +16,9 @@ void shutdown();
 void synchronize();
 void set_stream(void *s);
 int32_t *device_error_flag();
+// The current device's address of the paged decode's static scratch array
+// (k::kPagedScratchFloats floats), taken at init.
+float *paged_scratch();
 
 void upload(Tensor &t, const void *src, size_t offset, size_t count);
 void download(const Tensor &t, void *dst, size_t offset, size_t count);
@@ -82,6 +85,20 @@ struct HipBackend {
                                       const TensorNode &v, const TensorNode &kv_cache,
                                       const TensorNode &block_tables,
                                       const TensorNode &context_lens, float scale);
+    // Paged decode on caller-owned device memory with the partition
+    // workspace in the static scratch array: no device allocation.
+    struct PagedRaw {
+        const float *q, *k_new, *v_new, *kv_cache;
+        int64_t num_blocks;
+        int block_size, num_heads, head_dim;
+        const int32_t *block_tables;
+        int max_blocks;
+        const int32_t *context_lens;
+        int num_seqs;
+        float scale;
+        float *out;
+    };
+    static void paged_attention_noalloc(const PagedRaw &r);
     static void paged_kv_append(const Tensor &kv_cache, const Tensor &k, const Tensor &v,
                                 const Tensor &block_tables, const Tensor &context_lens);
     static TensorNode paged_gather_indices(const TensorNode &block_tables,

@@ -171,6 +171,27 @@ CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_ca
 CTensor clove_hip_paged_attention_scaled(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
                                          CTensor block_tables, CTensor context_lens,
                                          float scale);
+/* Allocation-free paged decode.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Computes what
+ * clove_hip_paged_attention_scaled computes, with the same kernels, on
+ * caller-owned device memory given as plain pointers:
+ *   q, out       f32 [num_seqs, num_heads*head_dim]
+ *   k, v         f32 [num_seqs, num_heads*head_dim] new token, or both NULL
+ *   kv_cache     f32 [2, num_blocks, block_size, num_heads, head_dim]
+ *   block_tables int32 [num_seqs, max_blocks]; context_lens int32 [num_seqs]
+ * all 16-byte aligned; scale is used as given.  The partition workspace
+ * (num_seqs*num_heads*partitions*(head_dim+2) floats when a context spans
+ * more than one partition) lives in a static 16 MiB device array per GPU;
+ * a shape needing more fails with CLOVE_HIP_ERR_SHAPE before any launch.
+ * Nothing is allocated.  Calls on one GPU that overlap (on different
+ * streams) share that array and race; calls on the library's one stream are
+ * ordered.  Index errors are reported as by the other paged entries. */
+int clove_hip_paged_attention_noalloc(const float *q, const float *k, const float *v,
+                                      const float *kv_cache, int64_t num_blocks, int block_size,
+                                      int num_heads, int head_dim, const int32_t *block_tables,
+                                      int max_blocks, const int32_t *context_lens, int num_seqs,
+                                      float scale, float *out);
 /* KV-cache append: writes each sequence's new-token k[b] and v[b] (f32
  * [B, H*D]) into planes 0 and 1 of kv_cache at the slot of token ctx_b - 1,
  * bt[b][(ctx_b-1)/bs]*bs + (ctx_b-1)%bs.  Sequences with ctx_b <= 0 are
