@@ -25,7 +25,9 @@ Rank 0 prints ONE JSON line on stdout:
                MLP plan (us per forward) and the backward passes and losses
                (GB/s; the matmul backward in TFLOP/s), attention prefill
                (TFLOP/s) and RoPE (GB/s), each with its roofline fraction and
-               a sampled CPU baseline; an HBM-bound part's `traffic` is the
+               a CPU baseline over the full workload (the attention prefill's
+               on sampled query rows: the full one is ~20 s of host time),
+               with the host CPU model; an HBM-bound part's `traffic` is the
                measured bytes per step of its kernels from the same summary.
 Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
 exits with a message.
@@ -113,6 +115,25 @@ def cpu_time(fn, reps=3):
     return float(np.median(best))
 
 
+def cpu_model():
+    """The host CPU's model name from /proc/cpuinfo (the baseline's hardware)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_record(oracle, value, unit, sample):
+    """A cpu_baseline object: the oracle (a restatement of Clove's Rayon
+    kernels, kind "port") on `oracle.threads()` host threads."""
+    return {"value": value, "unit": unit, "cores": oracle.threads(), "kind": "port",
+            "cpu_model": cpu_model(), "sample": sample}
+
+
 def roofline(bound, achieved, peak, unit, traffic=None):
     return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic}
@@ -161,15 +182,13 @@ def bench_rows(ca, oracle, args, out):
                 "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         if not args.no_cpu:
             def leg(name=name, part=part, nbytes=nbytes):
-                rows = 1024  # sample: 1/8 of the rows
-                xs = x.read(0, rows * 4096).reshape(rows, 4096)
+                xs = x.numpy()
                 gh, bh = gam.numpy(), bet.numpy()
                 fn = (lambda: oracle.softmax(xs)) if name == "softmax" else \
                     (lambda: oracle.layer_norm(xs, gh, bh))
-                t = cpu_time(fn) * (8192 / rows)
-                part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                        "cores": oracle.threads(), "kind": "port",
-                                        "sample": f"{rows} of 8192 rows, scaled"}
+                t = cpu_time(fn)
+                part["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
+                                                  "full [8192, 4096] workload, median of 3")
             defer(leg)
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), {per.mean() * 1e3:.1f} us")
@@ -188,24 +207,16 @@ def bench_matmul(ca, oracle, args, out):
             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
     if not args.no_cpu:
         def leg():
-            rows = 128
-            ah = a.read(0, rows * K).reshape(rows, K)
-            bh = b.numpy()
-            # rayon_matmul transposes B once, then computes rows; time both
-            # and scale only the row part to 4096 rows.
-            t_t = cpu_time(lambda: oracle.matmul(ah, bh, rows=(0, 0)), reps=1)
-            t_s = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
-            t = t_t + max(t_s - t_t, 0.0) * (4096 / rows)
-            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": f"{rows} of 4096 output rows plus the B "
-                                              "transpose, row time scaled to 4096"}
+            ah, bh = a.numpy(), b.numpy()
+            t = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
+            part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
+                                              "full 4096^3 product (B transpose included), "
+                                              "one run")
             ah32 = a32.numpy()
-            t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=1)
-            out["matmul_skinny_32"]["cpu_baseline"] = {
-                "value": round(2.0 * 32 * K * 4096 / t / 1e12, 5), "unit": "TFLOP/s",
-                "cores": oracle.threads(), "kind": "port",
-                "sample": "full 32x4096x4096 product (B transpose included)"}
+            t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=3)
+            out["matmul_skinny_32"]["cpu_baseline"] = cpu_record(
+                oracle, round(2.0 * 32 * K * 4096 / t / 1e12, 5), "TFLOP/s",
+                "full 32x4096x4096 product (B transpose included), median of 3")
         defer(leg)
     out["matmul_4096"] = part
     log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
@@ -244,18 +255,18 @@ def bench_paged(ca, oracle, args, out):
             "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if not args.no_cpu:
         def leg():
-            seqs = [0, 1, 2, 3]
+            seqs = list(range(B))
             plane, blk = nb * bs * H * D, bs * H * D
+            # the blocks the 32 sequences use, renumbered: the same rows the
+            # decode reads from the full pool
             pool, sbt, scl = workloads.compact_pool(
                 lambda p, b: kv.read(p * plane + b * blk, blk).reshape(bs, H, D), bt, ctx, seqs,
                 bs)
-            qh = q.numpy()[seqs]
+            qh = q.numpy()
             t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl))
-            t_full = t * ctx.sum() / scl.sum()
-            part["cpu_baseline"] = {"value": round(B / t_full, 2), "unit": "tokens/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": "4 of 32 sequences (all heads), scaled by context "
-                                              "tokens"}
+            part["cpu_baseline"] = cpu_record(oracle, round(B / t, 2), "tokens/s",
+                                              "full config 5 decode (32 sequences, all heads) "
+                                              "on the blocks it reads, median of 3")
         defer(leg)
     out["paged_decode"] = part
     log(f"paged decode: {B / sec:.0f} tokens/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM), "
@@ -279,8 +290,8 @@ def bench_mlp(ca, oracle, args, out):
     if not args.no_cpu:
         def leg():
             t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5)
-            part["cpu_baseline"] = {"value": round(t * 1e6, 1), "unit": "us/forward",
-                                    "cores": oracle.threads(), "kind": "port", "sample": "full"}
+            part["cpu_baseline"] = cpu_record(oracle, round(t * 1e6, 1), "us/forward",
+                                              "full config 1 forward, median of 5")
         defer(leg)
     out["mlp_forward"] = part
     log(f"mlp plan: {wall * 1e3:.1f} us/forward wall, {per.mean() * 1e3:.1f} us GPU")
@@ -346,9 +357,9 @@ def bench_backward(ca, oracle, args, out):
             wh, gh = w.numpy(), gw.numpy()
             zh = np.zeros(N, np.float32)
             t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1))
-            part["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": "full 16.7M-element parameter, one step"}
+            part["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
+                                              "full 16.7M-element parameter, one step, "
+                                              "median of 3")
         defer(leg)
     out["adamw_4096x4096"] = part
     log(f"adamw 4096x4096: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
@@ -379,15 +390,10 @@ def bench_backward(ca, oracle, args, out):
             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
     if oracle is not None:
         def leg(part=part):
-            rows = 16
             ah, bh, dch = a.numpy(), b.numpy(), dc.numpy()
-            t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch, da_rows=(0, rows),
-                                                        db_rows=(0, rows)), reps=1)
-            t *= 4096 / rows
-            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": f"{rows} of 4096 rows of grad_a and of grad_b, "
-                                              "scaled"}
+            t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch), reps=1)
+            part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
+                                              "full grad_a and grad_b at 4096^3, one run")
         defer(leg)
     out["matmul_backward_4096"] = part
     log(f"matmul backward 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA "
@@ -395,18 +401,17 @@ def bench_backward(ca, oracle, args, out):
 
 
 def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
-    rows = 1024  # row-sampled cases: 1/8 of the 8192 rows, scaled
     if name in ("softmax_backward", "cross_entropy", "cross_entropy_backward"):
-        th = targets.numpy()[:rows]
+        th = targets.numpy()
         if name == "softmax_backward":
-            ys, dys = y.read(0, rows * 4096).reshape(rows, 4096), dy.read(0, rows * 4096).reshape(rows, 4096)
+            ys, dys = y.numpy(), dy.numpy()
             fn = lambda: oracle.softmax_backward(ys, dys)
         else:
-            xs = x.read(0, rows * 4096).reshape(rows, 4096)
+            xs = x.numpy()
             fn = (lambda: oracle.cross_entropy(xs, th)) if name == "cross_entropy" else \
                 (lambda: oracle.cross_entropy_backward(xs, th, 1.0))
-        t = cpu_time(fn) * (8192 / rows)
-        sample = f"{rows} of 8192 rows, scaled"
+        t = cpu_time(fn)
+        sample = "full [8192, 4096] workload, median of 3"
     else:
         ah, bh = a.numpy(), b.numpy()
         fn = {"gelu_backward": lambda: oracle.gelu_backward(ah, bh),
@@ -414,9 +419,8 @@ def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
               "mse": lambda: oracle.mse(ah, bh),
               "mse_backward": lambda: oracle.mse_backward(ah, bh, 1.0)}[name]
         t = cpu_time(fn)
-        sample = "full workload"
-    return {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "cores": oracle.threads(),
-            "kind": "port", "sample": sample}
+        sample = "full [4096, 4096] workload, median of 3"
+    return cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s", sample)
 
 
 def bench_attention(ca, oracle, args, out):
@@ -444,10 +448,10 @@ def bench_attention(ca, oracle, args, out):
                                    reps=1)
             t_rows = max(t_rows - len(rows) * t_rope, 0.0)
             t = t_rope + t_rows * S / len(rows)
-            part["cpu_baseline"] = {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s",
-                                    "cores": oracle.threads(), "kind": "port",
-                                    "sample": f"{len(rows)} of {S} query rows (all heads) plus "
-                                              "the full RoPE of q and k, row time scaled"}
+            part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
+                                              f"{len(rows)} of {S} query rows (all heads) plus "
+                                              "the full RoPE of q and k, row time scaled (the "
+                                              "full prefill is about 20 s of host time)")
         defer(leg)
     out["flash_attention_4096"] = part
     log(f"attention prefill S=4096 H=32 D=128 causal+rope: {tf:.1f} TFLOP/s "
@@ -463,12 +467,10 @@ def bench_attention(ca, oracle, args, out):
                    "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if oracle is not None:
         def leg2():
-            rows = 512
-            xs = x.read(0, rows * H * D).reshape(1, rows, H * D)
-            t = cpu_time(lambda: oracle.rope(xs, D), reps=1) * S / rows
-            out["rope"]["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                           "cores": oracle.threads(), "kind": "port",
-                                           "sample": f"{rows} of {S} positions, scaled"}
+            xs = x.numpy()
+            t = cpu_time(lambda: oracle.rope(xs, D))
+            out["rope"]["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
+                                                     f"full [{S}, {H * D}] workload, median of 3")
         defer(leg2)
     log(f"rope [4096, 4096]: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), {per.mean() * 1e3:.1f} us")
 
@@ -573,10 +575,9 @@ def main():
         def leg():
             host = [ins[i].numpy() for i in range(4)]
             t = cpu_time(cpu_chain(oracle, host))
-            result["cpu_baseline"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s",
-                                      "cores": oracle.threads(), "kind": "port",
-                                      "sample": "full config 2 workload, 4 unfused passes "
-                                                "(Clove's eager CPU path), median of 3"}
+            result["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
+                                                "full config 2 workload, 4 unfused passes "
+                                                "(Clove's eager CPU path), median of 3")
         defer(leg)
 
     out = {}

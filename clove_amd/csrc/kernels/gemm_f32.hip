@@ -551,6 +551,190 @@ __global__ void __launch_bounds__(64 * W) gemm_skinny_kernel(GemmArgs g) {
     for (int j = 0; j < kPer; ++j) part[idx + j] = sum[j];
 }
 
+// Strip path: M <= 32 with B of 4 MiB or more, in ONE launch with no
+// workspace (the 32 x 4096 x 4096 decode-style product).  Every workgroup
+// produces final outputs over the whole K, since a reduction across
+// workgroups needs a device-scope fence per workgroup, which costs far more
+// than the product on this part (+36 us at this shape, measured), or a second
+// launch.  With 256 workgroups each one owns 512 outputs; a tile of 16 rows
+// x 32 columns keeps its L1 fill (16 + 32 rows of K) near the minimum and
+// reads B in whole 128-byte lines.  The two 16-row halves of a 32-column
+// strip are neighbouring workgroups on one XCD, so the second reads B's
+// lines from that XCD's L2: HBM sees B once.
+//  * v_mfma_f32_16x16x4_f32 (lane l supplies A[l%16][l/16] and
+//    B[l/16][l%16]; D[4(l/16) + i][l%16] in element i), two 16x16 blocks:
+//    lane (l16, q) loads B[k][n0 + 2 l16 .. +1] in one 8-byte load straight
+//    into operand registers, block 0 takes the even column, block 1 the odd
+//    one.  kStripDepth groups of 32 k are in flight.
+//  * K is split over the 4 waves (one per SIMD); a wave walks its range in
+//    chunks of 64 k (two groups).  A goes through LDS: each wave keeps a ring
+//    of kStripRing chunks (16 rows x 64 k, 4 KiB) filled by buffer->LDS DMA
+//    (no registers) that many chunks ahead, each DMA lane moving 16
+//    contiguous bytes of one row, and reads its MFMA operands from there.
+//    Within a chunk, 16-byte slot s of row r holds k-piece s ^ r, so the 16
+//    rows a read touches fall in different banks.  A group's LDS reads start
+//    after its first B register has arrived: loads complete in order, and
+//    the DMA of its chunk was issued before that B load.
+//  * Each strip starts its waves' chunk walks at a different offset
+//    (strip * 3 mod chunks): the workgroups of an XCD then read different k
+//    ranges of A at any moment instead of the same lines.
+//  * Measured at 32 x 4096 x 4096 (cold B): A read into registers from L2,
+//    16.1-17 us; A through the LDS ring, 13.1-13.8 us; a plain read of B
+//    alone, 10.2 us; the split-K skinny kernel plus its reduce, 17.3-17.8 us.
+//  * The 4 partial tiles meet in LDS and are summed in wave order, so the
+//    result is deterministic; the epilogue applies at the store.
+// A kernel variant per chunks-per-wave count NCH (the walk is unrolled: a
+// loop back-edge makes the compiler's load waits conservative).  Needs
+// K % 4 == 0, N % 2 == 0, a 16-byte aligned A and A, B under 2 GiB (the
+// plan checks them); rows past M and k past K read as zeros (a DMA lane
+// past the end of A writes zeros to LDS).
+constexpr int kStripWaves = 4;
+constexpr int kStripDepth = 2;   // B groups in flight
+constexpr int kStripRing = 6;    // A chunks in flight per wave
+constexpr int kStripRot = 3;
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+// FULL: K is exactly the walk (kStripWaves * 64 * NCH): no k masking, the
+// row and chunk steps ride in the uniform scalar offsets.  Otherwise every
+// load's offset is formed per lane and k past K is sent past the end of its
+// buffer.
+template <int NCH, bool EPI, bool FULL>
+__global__ void __launch_bounds__(64 * kStripWaves) gemm_strip_kernel(GemmArgs g) {
+    constexpr int W = kStripWaves, D = kStripDepth;
+    constexpr int R = NCH < kStripRing ? NCH : kStripRing;
+    constexpr int G2 = 2 * NCH;          // groups of 32 k per wave
+    constexpr int CH = 16 * 64;          // floats per chunk
+    constexpr int kPitch = 33;
+    static_assert(R == NCH || D < 2 * R - 1, "a chunk's DMA must precede its first B group");
+    __shared__ __attribute__((aligned(16))) float ring[W * R * CH];
+    const int M = g.M, N = g.N, K = g.K;
+    const int L = blockIdx.x;
+    const int V = (L % 8) * g.per_xcd + L / 8;
+    if (V >= g.tiles) return;
+    const int halves = g.tiles / g.tiles_n;
+    const int strip = V / halves, mh = V % halves;
+    const int n0 = strip * 32, m0 = mh * 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int l16 = lane & 15, q = lane >> 4;
+    const int kb = wave * (64 * NCH);
+    float *myring = ring + wave * R * CH;
+    // past the end of A and B (each under 2 GiB); plus any in-range offset it
+    // stays below 2^32, so it never wraps back into the buffer
+    constexpr uint32_t kOutside = 0x80000000u;
+    const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, (uint32_t)((size_t)K * N * 4));
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 4));
+    const int col = n0 + 2 * l16;
+    const bool col_ok = col < N;  // N is even: col + 1 < N too
+    const uint32_t boff = col_ok ? ((uint32_t)(kb + 8 * q) * (uint32_t)N + (uint32_t)col) * 4u
+                                 : kOutside;
+    const uint32_t row_bytes = (uint32_t)N * 4u;
+    // DMA lane mapping: instruction j, lane l -> chunk row 4j + l/16, slot
+    // l%16, holding k-piece slot ^ row.  Rows >= M start at or past M * K * 4,
+    // the end of A.
+    uint32_t adma[4];
+    int akp[4];  // this lane's k offset within a chunk, per instruction
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 4 * j + (lane >> 4), slot = lane & 15;
+        akp[j] = 4 * (slot ^ row);
+        adma[j] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(kb + akp[j])) * 4u;
+    }
+    const int rot = (strip * kStripRot) % NCH;
+    auto dma = [&](int c0) {  // chunk c0 of the walk into its ring slot
+        const int c = (c0 + rot) % NCH;
+        float *dst = myring + (c0 % R) * CH;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (FULL) {
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + 256 * j), 16,
+                                                         (int)adma[j], 256 * c, 0, 0);
+            } else {
+                // past K a row would run on into the next one
+                const uint32_t o = kb + 64 * c + akp[j] < K ? adma[j] + 256u * c : kOutside;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(dst + 256 * j), 16, (int)o,
+                                                         0, 0, 0);
+            }
+        }
+    };
+    typedef unsigned u2 __attribute__((ext_vector_type(2)));
+    float bq[D][8][2];
+    auto loadb = [&](int g0, int d) {  // group g0 of the walk
+        const int gi = 2 * (((g0 >> 1) + rot) % NCH) + (g0 & 1);
+        const int k0 = kb + 32 * gi + 8 * q;  // this lane's first k of the group
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            u2 v;
+            if (FULL) {
+                v = __builtin_amdgcn_raw_buffer_load_b64(
+                    rb, (int)boff, (int)((uint32_t)(32 * gi + t) * row_bytes), 0);
+            } else {
+                const uint32_t o = (col_ok && k0 + t < K)
+                                       ? boff + (uint32_t)(32 * gi + t) * row_bytes
+                                       : kOutside;
+                v = __builtin_amdgcn_raw_buffer_load_b64(rb, (int)o, 0, 0);
+            }
+            bq[d][t][0] = __uint_as_float(v.x);
+            bq[d][t][1] = __uint_as_float(v.y);
+        }
+    };
+    f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    auto mma = [&](int g0, int d) {
+        // wait for this group's first B load: everything issued before it,
+        // including the DMA of its A chunk, has completed
+        asm volatile("" ::"v"(bq[d][0][0]) : "memory");
+        const float *src = myring + ((g0 >> 1) % R) * CH + l16 * 64;
+        f4 a[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            // lane (l16, q) covers k = 32 sg + 8q + 4h + (0..3) of the chunk
+            const int piece = 8 * (g0 & 1) + 2 * q + h;
+            a[h] = *reinterpret_cast<const f4 *>(src + 4 * (piece ^ l16));
+        }
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t / 4][t % 4], bq[d][t][0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t / 4][t % 4], bq[d][t][1], acc1, 0, 0, 0);
+        }
+    };
+    // chunk 0 first (the first B groups' waits cover it), then B, then the
+    // rest of the ring
+    dma(0);
+#pragma unroll
+    for (int d = 0; d < D && d < G2; ++d) loadb(d, d);
+#pragma unroll
+    for (int c = 1; c < R; ++c) dma(c);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int gi = 0; gi < G2; ++gi) {
+        mma(gi, gi % D);
+        if (gi + D < G2) loadb(gi + D, gi % D);
+        // the slot of chunk gi/2 is free once both its groups are multiplied
+        if ((gi & 1) && gi / 2 + R < NCH) dma(gi / 2 + R);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();  // every wave is done with its ring: reuse it for the sums
+    // lane holds rows 4q + j: block 0 at column 2 l16, block 1 at 2 l16 + 1
+    float *red = ring;
+    float *mine = red + wave * 16 * kPitch;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        mine[(4 * q + j) * kPitch + 2 * l16] = acc0[j];
+        mine[(4 * q + j) * kPitch + 2 * l16 + 1] = acc1[j];
+    }
+    __syncthreads();
+    // 512 outputs over 256 threads, each summed in wave order
+    for (int o = threadIdx.x; o < 16 * 32; o += 64 * W) {
+        const int r = o / 32, c = o % 32;
+        float sum = red[r * kPitch + c];
+#pragma unroll
+        for (int w = 1; w < W; ++w) sum += red[w * 16 * kPitch + r * kPitch + c];
+        const int gr = m0 + r, gc = n0 + c;
+        if (gr < M && gc < N)
+            g.C[(size_t)gr * N + gc] = EPI ? epilogue(g.epi, sum, gr, gc, N) : sum;
+    }
+}
+
 // Small path: products whose tiles of 16*MB x 16 fit the chip in one wave
 // of workgroups and whose K is at most 1024 (the MLP layers, decode-sized
 // projections).  Every tile of C gets one workgroup of W waves that
@@ -794,6 +978,29 @@ void launch_skinny(const GemmPlan &p, const GemmArgs &g, dim3 grid, hipStream_t 
     else launch_skinny_w<2, 1, 8>(p, g, grid, s);
 }
 
+template <int NCH>
+void launch_strip_g(const GemmArgs &g, hipStream_t s) {
+    const bool epi = g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE;
+    const bool full = g.K == kStripWaves * 64 * NCH;
+    const unsigned grid = (unsigned)(8 * g.per_xcd);
+    if (epi && full) gemm_strip_kernel<NCH, true, true><<<grid, 64 * kStripWaves, 0, s>>>(g);
+    else if (epi) gemm_strip_kernel<NCH, true, false><<<grid, 64 * kStripWaves, 0, s>>>(g);
+    else if (full) gemm_strip_kernel<NCH, false, true><<<grid, 64 * kStripWaves, 0, s>>>(g);
+    else gemm_strip_kernel<NCH, false, false><<<grid, 64 * kStripWaves, 0, s>>>(g);
+}
+
+void launch_strip(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
+    switch (p.k_per_wave / 64) {
+    case 1: launch_strip_g<1>(g, s); break;
+    case 2: launch_strip_g<2>(g, s); break;
+    case 4: launch_strip_g<4>(g, s); break;
+    case 8: launch_strip_g<8>(g, s); break;
+    case 16: launch_strip_g<16>(g, s); break;
+    case 32: launch_strip_g<32>(g, s); break;
+    default: launch_strip_g<64>(g, s); break;
+    }
+}
+
 template <int W, int MB, int NBATCH>
 void launch_small_b(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
     const bool epi = g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE;
@@ -821,7 +1028,8 @@ void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
 }  // namespace
 
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned,
-                   bool force_skinny, int force_skinny_nb, int force_skinny_splits) {
+                   bool force_skinny, int force_skinny_nb, int force_skinny_splits,
+                   bool force_strip) {
     GemmPlan p{};
     p.M = M;
     p.N = N;
@@ -871,6 +1079,27 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     }
     const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned &&
                           b_bytes < (1ull << 31) && force_cfg < 0;
+    // Strip path (one launch, no workspace): M <= 32, even N, B of 4 MiB or
+    // more, enough 16 x 32 tiles for every CU, and K within the longest
+    // unrolled walk (4 waves x 64 chunks of 64 k).
+    {
+        const int halves = (M + 15) / 16, strips = (N + 31) / 32;
+        if (eligible && !force_skinny && M <= 32 && N % 2 == 0 && K <= kStripWaves * 64 * 64 &&
+            (force_strip ||
+             (b_bytes >= (4ull << 20) && (int64_t)halves * strips >= num_cus))) {
+            p.strip = true;
+            p.tiles_n = strips;
+            p.tiles = halves * strips;
+            int nch = 1;
+            while (nch < 64 && kStripWaves * 64 * nch < K) nch *= 2;
+            p.k_per_wave = 64 * nch;
+            p.waves = kStripWaves;
+            p.splits = 1;
+            p.ws_floats = 0;
+            p.vec = true;
+            return p;
+        }
+    }
     if (eligible && (force_skinny || b_bytes >= (4ull << 20))) {
         p.skinny = true;
         p.mb = M <= 32 ? 1 : 2;
@@ -966,7 +1195,7 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
                          bool tb, hipStream_t s) {
     if (ta == tb) return false;  // exactly one operand read transposed (the matmul backward)
-    if (p.small || p.skinny || p.splits != 1 || !p.interior || p.K <= 0) return false;
+    if (p.small || p.skinny || p.strip || p.splits != 1 || !p.interior || p.K <= 0) return false;
     if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) return false;
     if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128) return false;
     const GemmArgs g{A, B, C, nullptr, p.M, p.N, p.K, p.tiles_n, p.k_per_split, 1, GemmEpilogue{},
@@ -1008,6 +1237,10 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
                p.tiles, (p.tiles + 7) / 8};
     if (p.small) {
         launch_small(p, g, s);
+        return;
+    }
+    if (p.strip) {
+        launch_strip(p, g, s);
         return;
     }
     if (p.skinny) {

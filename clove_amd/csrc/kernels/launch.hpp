@@ -100,6 +100,10 @@ struct GemmPlan {
     // Small path: one workgroup of `waves` waves per 16 x 16 tile of C, K
     // split inside the workgroup (k_per_split k per wave); no workspace.
     bool small;
+    // Strip path (M <= 32): one workgroup per 16-row half of a 32-column
+    // strip over the whole K (k_per_wave k per wave, `waves` waves); one
+    // launch, no workspace.  tiles_n = strips, tiles = halves * strips.
+    bool strip;
 };
 // Optional epilogue fused into the GEMM store: bias add with Clove's
 // broadcast rule (bias read at flat index % bias_n) and an activation.
@@ -124,11 +128,12 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 // 16-byte aligned (the skinny path needs it).  force_cfg >= 0 overrides the
 // configuration and turns the skinny path off; force_skinny takes the skinny
 // path wherever it is legal, with force_skinny_nb (1, 2, 4) /
-// force_skinny_splits > 0 overriding its plan (tuning and tests).  Every
-// plan computes the same product.
+// force_skinny_splits > 0 overriding its plan; force_strip takes the strip
+// path wherever it is legal (M <= 32, even N, K % 4 == 0, K <= 16384; tuning
+// and tests).  Every plan computes the same product.
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned = true,
                    bool force_skinny = false, int force_skinny_nb = 0,
-                   int force_skinny_splits = 0);
+                   int force_skinny_splits = 0, bool force_strip = false);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
 // C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the

@@ -184,11 +184,16 @@ static void matmul_dims(const Tensor &a, const Tensor &b, size_t *m, size_t *k, 
 // CLOVE_GEMM_CFG selects a tile configuration by index and turns the
 // skinny path off; CLOVE_GEMM_SKINNY="nb,splits" forces the skinny path where
 // it is legal (M <= 64, K % 4 == 0) and sets its column blocks per wave and
-// K splits (0 keeps the default).  Both are for tuning sweeps only: every plan computes the same
-// product.
+// K splits (0 keeps the default); CLOVE_GEMM_STRIP=1 forces the strip path
+// where it is legal (M <= 32, even N).  All are for tuning sweeps and tests
+// only: every plan computes the same product.
 static int gemm_cfg_override() {
     const char *v = std::getenv("CLOVE_GEMM_CFG");
     return (v && *v) ? std::atoi(v) : -1;
+}
+static bool gemm_strip_override() {
+    const char *v = std::getenv("CLOVE_GEMM_STRIP");
+    return v && *v && std::atoi(v) != 0;
 }
 static bool gemm_skinny_override(int *nb, int *splits) {
     *nb = 0;
@@ -222,7 +227,7 @@ static k::GemmPlan prepare_matmul(const Tensor &a, const Tensor &b, const Tensor
     const bool sk_force = gemm_skinny_override(&sk_nb, &sk_splits);
     const bool a_aligned = (reinterpret_cast<uintptr_t>(a.data) & 15) == 0;
     return k::gemm_plan((int)m, (int)n, (int)kk, ctx().num_cus, gemm_cfg_override(), a_aligned,
-                        sk_force, sk_nb, sk_splits);
+                        sk_force, sk_nb, sk_splits, gemm_strip_override());
 }
 
 // A product the grouped small kernel can take: the small path, and for a

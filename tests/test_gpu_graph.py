@@ -187,6 +187,28 @@ def test_skinny_epilogue(hip, monkeypatch, plan, m, k, n, bias_n, act):
     assert_close(fused.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "skinny epilogue")
 
 
+@pytest.mark.parametrize("m,k,n,bias_n,act", [(32, 4096, 512, 3, "gelu"), (20, 300, 66, 66, "relu"),
+                                               (32, 4096, 4096, 4096, "relu")])
+def test_strip_epilogue(hip, monkeypatch, m, k, n, bias_n, act):
+    """The fused epilogue on the strip path (applied at its store), equal to
+    the eager composition's bits and to the oracle's composition."""
+    monkeypatch.setenv("CLOVE_GEMM_STRIP", "1")
+    gg = rng(7 * m + n + k)
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, bias_n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},{k}"), g.input(f"{k},{n}"), g.input(f"{bias_n}")
+    y = g.op(act, g.op("add", g.op("matmul", x, wi), bi))
+    model = g.compile([y])
+    ta, tw, tb = hip.tensor(a), hip.tensor(w), hip.tensor(b)
+    (fused,) = model.execute([ta, tw, tb])
+    eager = getattr(hip, act)(hip.add(hip.matmul(ta, tw), tb))
+    assert np.array_equal(fused.numpy(), eager.numpy())
+    want = getattr(oracle, act)(oracle.add(oracle.matmul(a, w), b))
+    assert_close(fused.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "strip epilogue")
+
+
 @pytest.mark.parametrize("m,k,n,bias_n", [(64, 128, 10, 10), (37, 64, 16, 1), (5, 8, 3, 0),
                                            (64, 128, 17, 17), (64, 2048, 10, 10),
                                            (300, 96, 12, 12)])

@@ -67,6 +67,28 @@ def test_config4_full(hip):
     check(hip.matmul(hip.tensor(a32), tb).numpy(), oracle.matmul(a32, b), "skinny 32x4096x4096")
 
 
+# The strip path (M <= 32, even N, K % 4 == 0): one launch, a workgroup per
+# 16-row half of a 32-column strip over the whole K.  The plan picks it when
+# B >= 4 MiB and the strips fill the chip (32 x 4096 x 4096: config 4's
+# skinny case); CLOVE_GEMM_STRIP forces it on the edge shapes here: K equal
+# to the unrolled walk (256, 4096, 16384) or not (k past K masked), partial
+# strips (N % 32 != 0), one or two row halves, partial halves.
+@pytest.mark.parametrize("m,k,n", [(1, 4, 2), (5, 12, 34), (16, 256, 64), (17, 300, 96),
+                                   (31, 2052, 130), (32, 4096, 512), (32, 256, 2),
+                                   (20, 16384, 64), (32, 4104, 94), (9, 8188, 4098),
+                                   (32, 1024, 4096)])
+def test_strip_shapes(hip, monkeypatch, m, k, n):
+    monkeypatch.setenv("CLOVE_GEMM_STRIP", "1")
+    g = rng(m * 13 + k * 3 + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, oracle.matmul(a, b), f"strip {m}x{k}x{n}")
+    # deterministic: the same plan gives the same bits
+    assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
+
+
 # The skinny path (M <= 64, K % 4 == 0, 16-byte aligned A): 32*nb columns
 # per workgroup, a K split over the workgroup's waves and across workgroups.
 # The plan picks it for B >= 4 MiB; CLOVE_GEMM_SKINNY forces it on the small
