@@ -487,7 +487,7 @@ PART_KERNELS = {
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
-    "broadcast_grad": ["bcast_grad_cols4_kernel", "bcast_grad_final_kernel"],
+    "broadcast_grad": ["bcast_grad_strip_kernel"],
     "cross_entropy": ["cross_entropy_block_kernel<2, 0>", "ordered_sum_kernel"],
     "cross_entropy_backward": ["cross_entropy_block_kernel<2, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],

@@ -163,7 +163,10 @@ def test_matmul_backward_transposed_loads_match_copies(hip, monkeypatch, m, k, n
                                   # a partial block of column quads and a partial last row;
                                   # more than 16384 x 64 rows (chunks of more than 64 rows)
                                   (4100 * 70 + 13, 4100), (530000 * 64 + 3, 64),
-                                  (1100000 * 64 + 3, 64)])
+                                  (1100000 * 64 + 3, 64),
+                                  # the one-pass strip kernel (nb >= 16 per CU): fewer rows
+                                  # than a workgroup's row groups, a partial last row, wide b
+                                  (4096 * 3, 4096), (8192 * 33 + 100, 8192), (16384 * 300, 16384)])
 def test_broadcast_grad_exact(hip, n, nb):
     g = rng(n % 1000 + nb)
     go = g.integers(-8, 9, n).astype(np.float32)
