@@ -483,7 +483,7 @@ PART_KERNELS = {
     "chain_broadcast": ["clove_chain_mul_add_gelu_mul_b0020"],
     "softmax": ["softmax_block_kernel<2>"],
     "layer_norm": ["layer_norm_wave_kernel<16>"],
-    "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 8>", "gemm_splitk_reduce"],
+    "matmul_skinny_32": ["gemm_strip_kernel<16, false, true>"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
