@@ -189,3 +189,42 @@ def test_matmul_empty_dimensions(hip, m, k, n):
     b = np.zeros((k, n), np.float32)
     got = hip.matmul(hip.tensor(a), hip.tensor(b)).numpy()
     assert got.shape == (m, n) and np.all(got == 0)
+
+
+# Interior tiles of the 128 x 256 and 128 x 128 configurations run the
+# DMA-staged kernel (slabs moved by buffer->LDS loads); CLOVE_GEMM_DMA=0 runs
+# the register-staged kernel.  Same tiles, waves and MFMA order: the same
+# bits, single launch and split-K, and both within the matmul bound of the
+# oracle.  CLOVE_GEMM_CFG picks the configuration (2: 128 x 128, 5: 128 x 256).
+@pytest.mark.parametrize("cfg,m,k,n", [(5, 256, 512, 512), (5, 128, 4096, 256),
+                                       (2, 384, 1040, 256), (2, 128, 16, 128),
+                                       (2, 256, 8192, 256), (5, 512, 2048, 768)])
+def test_dma_kernel_matches_register_staged(hip, monkeypatch, cfg, m, k, n):
+    monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
+    g = rng(cfg * 7 + m + k + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    dma = hip.matmul(ta, tb).numpy()
+    monkeypatch.setenv("CLOVE_GEMM_DMA", "0")
+    staged = hip.matmul(ta, tb).numpy()
+    assert np.array_equal(dma, staged)
+    check(dma, oracle.matmul(a, b), f"dma cfg {cfg} {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("cfg", [2, 5])
+def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
+    """The fused bias + GELU epilogue on the DMA-staged kernel: the eager
+    composition's bits."""
+    monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
+    g = rng(60 + cfg)
+    m, k, n = 256, 1024, 512
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = g.normal(0, 1, (k, n)).astype(np.float32)
+    b = g.normal(0, 1, n).astype(np.float32)
+    gr = hip.Graph()
+    x, wi, bi = gr.input(f"{m},{k}"), gr.input(f"{k},{n}"), gr.input(f"{n}")
+    y = gr.op("gelu", gr.op("add", gr.op("matmul", x, wi), bi))
+    (fused,) = gr.compile([y]).execute([hip.tensor(a), hip.tensor(w), hip.tensor(b)])
+    eager = hip.gelu(hip.add(hip.matmul(hip.tensor(a), hip.tensor(w)), hip.tensor(b)))
+    assert np.array_equal(fused.numpy(), eager.numpy())
