@@ -571,6 +571,100 @@ __global__ void __launch_bounds__(kBlockThreads) cross_entropy_block_kernel(
     }
 }
 
+// Cross entropy forward with two rows per workgroup (the block kernel's
+// per-row arithmetic and reduction order, so the same bits): each thread
+// holds P vectors of both rows, and the two rows' maxima and sums go through
+// the same butterflies and the same two barriers.  Measured at [8192, 4096]
+// with cold inputs: 21.3-21.4 us against 22.0-24.0 us for one row per
+// workgroup (four rows: 23.2 us): twice the bytes in flight per workgroup at
+// the same barrier count.  A row past `rows` (odd row counts) loads nothing
+// and writes nothing.
+template <int P>
+__global__ void __launch_bounds__(kBlockThreads) cross_entropy_rows2_kernel(
+    const float *__restrict__ logits, const float *__restrict__ targets, long used, int rows,
+    int cols, float *__restrict__ out, int *err_flag) {
+    __shared__ float red[2][2][kBlockWaves];
+    __shared__ float s_lt[2];
+    const long row0 = 2L * blockIdx.x;
+    const int nvec = cols >> 2;
+    cl_f4 v[2][P];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const bool live = row0 + r < rows;
+        const cl_f4 *lr = reinterpret_cast<const cl_f4 *>(logits + (row0 + r) * (long)cols);
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            const int c = threadIdx.x + kBlockThreads * i;
+            v[r][i] = (live && c < nvec) ? __builtin_nontemporal_load(lr + c)
+                                         : (cl_f4){-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+        }
+    }
+    long t[2];  // the same for every thread of the row; -1: the row counts 0
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const long row = row0 + r;
+        t[r] = -1;
+        if (row < used && row < rows) {
+            t[r] = target_class(targets[row]);
+            if (t[r] >= cols) {
+                if (threadIdx.x == 0) atomicOr(err_flag, kErrClassRange);
+                t[r] = -1;
+            }
+        }
+        if (t[r] >= 0) {
+            const int tv = (int)(t[r] >> 2), ts = (int)(t[r] & 3);
+            if (tv % kBlockThreads == (int)threadIdx.x) {
+#pragma unroll
+                for (int i = 0; i < P; ++i)
+                    if (i == tv / kBlockThreads) s_lt[r] = v[r][i][ts];
+            }
+        }
+    }
+    float m[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        m[r] = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < P; ++i) m[r] = fmaxf(m[r], hmax4(v[r][i]));
+        m[r] = wave_max(m[r]);
+        if ((threadIdx.x & 63) == 0) red[0][r][threadIdx.x >> 6] = m[r];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        float x = red[0][r][0];
+#pragma unroll
+        for (int w = 1; w < kBlockWaves; ++w) x = fmaxf(x, red[0][r][w]);
+        m[r] = x;
+    }
+    float sm[2];
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        sm[r] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+            if (threadIdx.x + kBlockThreads * i < nvec) {
+                const cl_f4 e = {fast_exp(v[r][i].x - m[r]), fast_exp(v[r][i].y - m[r]),
+                                 fast_exp(v[r][i].z - m[r]), fast_exp(v[r][i].w - m[r])};
+                sm[r] += hsum4(e);
+            }
+        }
+        sm[r] = wave_sum(sm[r]);
+        if ((threadIdx.x & 63) == 0) red[1][r][threadIdx.x >> 6] = sm[r];
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        const int r = threadIdx.x;
+        const long row = row0 + r;
+        if (row < rows) {
+            float x = red[1][r][0];
+#pragma unroll
+            for (int w = 1; w < kBlockWaves; ++w) x += red[1][r][w];
+            out[row] = t[r] < 0 ? 0.0f : (s_lt[r] - m[r]) - logf(x);
+        }
+    }
+}
+
 // Vectors per thread of the row-per-workgroup kernels for this width, or 0
 // for the one-wave-per-row kernels (width not a multiple of 4, at most 1024
 // columns, or beyond 16 vectors per thread).
@@ -675,6 +769,14 @@ static void cross_entropy_launch(const float *logits, const float *targets, size
     const long u = (long)used;
     const bool al = aligned16(logits) && (MODE == 0 || aligned16(out));
     const unsigned nrows = (unsigned)rows;
+    if (MODE == 0 && al && (pick_block_p(c) == 1 || pick_block_p(c) == 2)) {
+        const unsigned pairs = (unsigned)((rows + 1) / 2);
+        if (pick_block_p(c) == 1)
+            cross_entropy_rows2_kernel<1><<<pairs, kBlockThreads, 0, s>>>(logits, targets, u, r, c, out, err_flag);
+        else
+            cross_entropy_rows2_kernel<2><<<pairs, kBlockThreads, 0, s>>>(logits, targets, u, r, c, out, err_flag);
+        return;
+    }
     switch (al ? pick_block_p(c) : 0) {
     case 1: cross_entropy_block_kernel<1, MODE><<<nrows, kBlockThreads, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); return;
     case 2: cross_entropy_block_kernel<2, MODE><<<nrows, kBlockThreads, 0, s>>>(logits, targets, u, r, c, grad_loss, out, err_flag); return;

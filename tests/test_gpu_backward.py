@@ -295,3 +295,27 @@ def test_mse_edge_cases(hip):
     assert np.isnan(hip.mse(z, z).numpy()[0, 0])  # 0 / 0, as the reference computes
     with pytest.raises(hip.CloveError):
         hip.mse(hip.tensor(np.ones(4, np.float32)), hip.tensor(np.ones(3, np.float32)))
+
+
+def test_cross_entropy_row_pairs_edge_cases(hip):
+    """The two-rows-per-workgroup forward (widths 1025-4096): fewer targets
+    than rows (a pair with one counted row), an odd row count, and a class
+    >= cols in the second row of a pair (reported; that row counts 0)."""
+    g = rng(52)
+    for cols in (1028, 2048, 4096):
+        logits = g.normal(0, 3, (9, cols)).astype(np.float32)
+        tl = hip.tensor(logits)
+        t5 = g.integers(0, cols, 5).astype(np.float32)
+        got = hip.cross_entropy(tl, hip.tensor(t5)).numpy()[0, 0]
+        want = oracle.cross_entropy(logits, t5)[0, 0]
+        assert abs(got - want) <= 1e-4 * abs(want) + 1e-7, (cols, got, want)
+        bad = t5.copy()
+        bad[3] = cols
+        got = hip.cross_entropy(tl, hip.tensor(bad))
+        with pytest.raises(hip.CloveError) as e:
+            hip.synchronize()
+        assert e.value.code == 7
+        keep = np.array([0, 1, 2, 4], np.int64)  # the rows that still count
+        # the loss over the kept rows, times their count, over all 9 rows
+        want = oracle.cross_entropy(logits[keep], t5[keep])[0, 0] * 4 / 9
+        assert abs(got.numpy()[0, 0] - want) <= 1e-4 * abs(want) + 1e-7
