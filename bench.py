@@ -491,7 +491,7 @@ PART_KERNELS = {
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
     "broadcast_grad": ["bcast_grad_strip_kernel"],
-    "cross_entropy": ["cross_entropy_block_kernel<2, 0>", "ordered_sum_kernel"],
+    "cross_entropy": ["cross_entropy_rows2_kernel<2>", "ordered_sum_kernel"],
     "cross_entropy_backward": ["cross_entropy_block_kernel<2, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
     "mse_backward": ["mse_backward_kernel<true>"],
