@@ -119,6 +119,20 @@ struct GemmCfg {
     static_assert(BK % 8 == 0, "K slab is a whole number of 8-groups");
 };
 
+// Transposed-B slab: thread index idx moves k-quad kq of column n.  Lanes
+// 16q .. 16q+15 of a wave take quad q of 16 consecutive columns, so one
+// wave instruction reads 64 whole bytes of each of 16 rows of the [N, K]
+// matrix, and the column stores of the four k values (rows 4kq + c of the
+// B stage, pitch BN + 4) have no bank conflicts; four lanes per column (the
+// quads of one row side by side) cost 2 conflict cycles per store
+// (measured with SQ_LDS_BANK_CONFLICT on gfx950).
+template <int BK>
+__device__ __forceinline__ void tb_map(int idx, int *kq, int *n) {
+    constexpr int KQ = BK / 4;
+    *kq = (idx / 16) % KQ;
+    *n = idx % 16 + 16 * (idx / (16 * KQ));
+}
+
 // Loads one slab of A (rows m0.., cols k0..) and B (rows k0.., cols n0..)
 // into registers.  EDGE enables bounds checks; VEC selects 16-byte loads
 // (only legal when K % 4 == 0 and N % 4 == 0).
@@ -164,8 +178,8 @@ __device__ __forceinline__ void load_slab(const float *__restrict__ A, const flo
     if constexpr (TB) {
 #pragma unroll
         for (int i = 0; i < C::kLoadsB; ++i) {
-            const int idx = tid + i * C::kThreads;
-            const int kq = idx % (BK / 4), n = idx / (BK / 4);
+            int kq, n;
+            tb_map<BK>(tid + i * C::kThreads, &kq, &n);
             rb[i] = *reinterpret_cast<const f4 *>(B + (size_t)(n0 + n) * K + k0 + 4 * kq);
         }
     }
@@ -190,6 +204,20 @@ __device__ __forceinline__ void load_slab(const float *__restrict__ A, const flo
     }
 }
 
+// Float index of k-quad kq of row r in an A stage.  At BK = 16 the rows are
+// unpadded and the quads of row r are XOR-permuted by (r >> 2) & 3: the
+// MFMA operand reads (one ds_read_b128 per lane, rows l%32, quad 2g + l/32)
+// then have no bank conflicts, where the padded pitch BK + 4 costs 12
+// conflict cycles per read and the permutation by (r >> 1) & 3 costs 4
+// (measured with SQ_LDS_BANK_CONFLICT on gfx950).  The transposed-A slab
+// keeps the padded pitch: its stores write one column of rows 4 apart, and
+// those rows must fall in different banks.
+template <class C, int BK, bool TA>
+__device__ __forceinline__ int a_pos(int r, int kq) {
+    if constexpr (BK == 16 && !TA) return r * BK + 4 * (kq ^ ((r >> 2) & 3));
+    else return r * C::kPitchA + 4 * kq;
+}
+
 template <class C, int BK, int BN, bool TA = false, bool TB = false>
 __device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, const f4 *rb) {
     const int tid = threadIdx.x;
@@ -202,14 +230,15 @@ __device__ __forceinline__ void store_slab(float *sA, float *sB, const f4 *ra, c
             for (int c = 0; c < 4; ++c) sA[(4 * mq + c) * C::kPitchA + k] = ra[i][c];
         } else {
             const int r = idx / (BK / 4), kq = idx % (BK / 4);
-            *reinterpret_cast<f4 *>(sA + r * C::kPitchA + 4 * kq) = ra[i];
+            *reinterpret_cast<f4 *>(sA + a_pos<C, BK, TA>(r, kq)) = ra[i];
         }
     }
 #pragma unroll
     for (int i = 0; i < C::kLoadsB; ++i) {
         const int idx = tid + i * C::kThreads;
         if constexpr (TB) {  // four k of one n: rows 4kq .. 4kq+3 of column n
-            const int kq = idx % (BK / 4), n = idx / (BK / 4);
+            int kq, n;
+            tb_map<BK>(idx, &kq, &n);
 #pragma unroll
             for (int c = 0; c < 4; ++c) sB[(4 * kq + c) * C::kPitchB + n] = rb[i][c];
         } else {
@@ -277,8 +306,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
             float b[Cfg::kBlocksN][4];
 #pragma unroll
             for (int i = 0; i < Cfg::kBlocksM; ++i)
-                a[i] = *reinterpret_cast<const f4 *>(sA + (wm0 + 32 * i + l32) * Cfg::kPitchA +
-                                                     8 * gk + 4 * h);
+                a[i] = *reinterpret_cast<const f4 *>(
+                    sA + a_pos<Cfg, BK, TA>(wm0 + 32 * i + l32, 2 * gk + h));
 #pragma unroll
             for (int j = 0; j < Cfg::kBlocksN; ++j)
 #pragma unroll
@@ -340,8 +369,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 // the lane chooses which global 16 bytes it moves, so the LDS layout is set
 // by the lane-to-address map:
 //  * A stage [BM][BK]: 16-byte slot s of row r holds k-quad
-//    s ^ ((r >> 1) & (BK/4 - 1)), so the eight rows one ds_read_b128 pass
-//    touches fall in different banks;
+//    s ^ ((r >> 2) & (BK/4 - 1)), the layout a_pos gives the register-staged
+//    kernel (bank-conflict free at BK = 16, measured);
 //  * B stage [BK][BN] at pitch BN (rows of 1 KiB at BN = 256): a lane's four
 //    column blocks sit 32 floats apart in one row and pair up in ds_read2_b32.
 // kDmaStages slabs rotate through LDS (72 KiB at 128 x 256, so two
@@ -385,7 +414,7 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
     for (int u = 0; u < IAW; ++u) {
         const int p = (wave * IAW + u) * 64 + lane;  // 16-byte position in the A stage
         const int row = p / KQ, slot = p % KQ;
-        const int kq = slot ^ ((row >> 1) & (KQ - 1));
+        const int kq = slot ^ ((row >> 2) & (KQ - 1));
         aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
     }
 #pragma unroll
@@ -433,7 +462,7 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
             for (int i = 0; i < BMb; ++i) {
                 const int row = wm0 + 32 * i + l32, kq = 2 * gk + h;
                 a[i] = *reinterpret_cast<const f4 *>(sA + row * BK +
-                                                     4 * (kq ^ ((row >> 1) & (KQ - 1))));
+                                                     4 * (kq ^ ((row >> 2) & (KQ - 1))));
             }
 #pragma unroll
             for (int j = 0; j < BNb; ++j)
