@@ -373,6 +373,14 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 //    kernel (bank-conflict free at BK = 16, measured);
 //  * B stage [BK][BN] at pitch BN (rows of 1 KiB at BN = 256): a lane's four
 //    column blocks sit 32 floats apart in one row and pair up in ds_read2_b32.
+//  * TA (the product's A is the transpose of the [K, M] matrix given): the
+//    A stage is k-major [BK][BM], each lane moving four m of one k, and a
+//    wave reads one float per MFMA step as it reads B;
+//  * TB (B is the transpose of the [N, K] matrix given): the B stage is
+//    n-major [BN][BK] with A's XOR layout, each lane moving four k of one n,
+//    so a lane's four k of one column come in one ds_read_b128.
+//    Both read the same values into the same MFMA steps as the plain
+//    layouts, so the product is the same bit for bit as transposing first.
 // kDmaStages slabs rotate through LDS (72 KiB at 128 x 256, so two
 // workgroups still share a CU).  Each wave waits for its own DMAs of slab s
 // (vmcnt), then a bare s_barrier publishes them to the other waves:
@@ -384,7 +392,7 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 // tiles with 8 waves (961-982 us) within noise of it.
 constexpr int kDmaStages = 3;
 
-template <int BM, int BN, int BK, int WM, int WN, bool EPI>
+template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, bool TB = false>
 __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
     constexpr int ST = kDmaStages;
     constexpr int SA = BM * BK, SB = BK * BN, SS = SA + SB;
@@ -413,26 +421,39 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
 #pragma unroll
     for (int u = 0; u < IAW; ++u) {
         const int p = (wave * IAW + u) * 64 + lane;  // 16-byte position in the A stage
-        const int row = p / KQ, slot = p % KQ;
-        const int kq = slot ^ ((row >> 2) & (KQ - 1));
-        aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+        if constexpr (TA) {  // k-major: row k, four m
+            const int row = 4 * p / BM, col = 4 * p % BM;
+            aoff[u] = ((uint32_t)(k_begin + row) * (uint32_t)M + (uint32_t)(m0 + col)) * 4u;
+        } else {
+            const int row = p / KQ, slot = p % KQ;
+            const int kq = slot ^ ((row >> 2) & (KQ - 1));
+            aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+        }
     }
 #pragma unroll
     for (int u = 0; u < IBW; ++u) {
-        const int f = ((wave * IBW + u) * 64 + lane) * 4;  // float position in the B stage
-        const int row = f / BN, col = f % BN;
-        boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
+        const int p = (wave * IBW + u) * 64 + lane;  // 16-byte position in the B stage
+        if constexpr (TB) {  // n-major: row n, four k
+            const int row = p / KQ, slot = p % KQ;
+            const int kq = slot ^ ((row >> 2) & (KQ - 1));
+            boff[u] = ((uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+        } else {
+            const int row = 4 * p / BN, col = 4 * p % BN;
+            boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
+        }
     }
+    const int a_step = TA ? BK * M * 4 : BK * 4;  // bytes per slab
+    const int b_step = TB ? BK * 4 : BK * N * 4;
     auto dma = [&](int sl) {
         float *st = smem + (sl % ST) * SS;
 #pragma unroll
         for (int u = 0; u < IAW; ++u)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(st + (wave * IAW + u) * 256), 16,
-                                                     (int)aoff[u], sl * BK * 4, 0, 0);
+                                                     (int)aoff[u], sl * a_step, 0, 0);
 #pragma unroll
         for (int u = 0; u < IBW; ++u)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(st + SA + (wave * IBW + u) * 256),
-                                                     16, (int)boff[u], sl * BK * N * 4, 0, 0);
+                                                     16, (int)boff[u], sl * b_step, 0, 0);
     };
     f16v acc[BMb][BNb];
 #pragma unroll
@@ -458,17 +479,31 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
         for (int gk = 0; gk < BK / 8; ++gk) {
             f4 a[BMb];
             float b[BNb][4];
+            const int kq = 2 * gk + h;
 #pragma unroll
             for (int i = 0; i < BMb; ++i) {
-                const int row = wm0 + 32 * i + l32, kq = 2 * gk + h;
-                a[i] = *reinterpret_cast<const f4 *>(sA + row * BK +
-                                                     4 * (kq ^ ((row >> 2) & (KQ - 1))));
+                const int row = wm0 + 32 * i + l32;
+                if constexpr (TA) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) a[i][t] = sA[(4 * kq + t) * BM + row];
+                } else {
+                    a[i] = *reinterpret_cast<const f4 *>(sA + row * BK +
+                                                         4 * (kq ^ ((row >> 2) & (KQ - 1))));
+                }
             }
 #pragma unroll
-            for (int j = 0; j < BNb; ++j)
+            for (int j = 0; j < BNb; ++j) {
+                const int col = wn0 + 32 * j + l32;
+                if constexpr (TB) {
+                    const f4 v = *reinterpret_cast<const f4 *>(sB + col * BK +
+                                                               4 * (kq ^ ((col >> 2) & (KQ - 1))));
 #pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    b[j][t] = sB[(8 * gk + 4 * h + t) * BN + wn0 + 32 * j + l32];
+                    for (int t = 0; t < 4; ++t) b[j][t] = v[t];
+                } else {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) b[j][t] = sB[(4 * kq + t) * BN + col];
+                }
+            }
 #pragma unroll
             for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -1395,7 +1430,17 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
     const GemmArgs g{A, B, C, nullptr, p.M, p.N, p.K, p.tiles_n, p.k_per_split, 1, GemmEpilogue{},
                      p.tiles, (p.tiles + 7) / 8};
     const dim3 grid((unsigned)(g.per_xcd * 8), 1u);
-    if (p.cfg == CFG_128x256) {
+    if (p.cfg == CFG_128x256 && dma_ok(p, 128, 256)) {
+        if (ta)
+            gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, true, false><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, false, true><<<grid, 256, 0, s>>>(g);
+    } else if (p.cfg == CFG_128x128 && dma_ok(p, 128, 128)) {
+        if (ta)
+            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, true, false><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true><<<grid, 256, 0, s>>>(g);
+    } else if (p.cfg == CFG_128x256) {
         if (ta)
             gemm_f32_mfma_kernel<128, 256, 16, 64, 128, false, true, false, true, false>
                 <<<grid, 256, 0, s>>>(g);

@@ -138,18 +138,24 @@ def test_matmul_backward_4096(hip):
 
 
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 4096), (4096, 1024, 2048), (2048, 4096, 4096),
+                                   (2048, 2048, 2048), (2048, 2048, 1024),
                                    (3, 5, 7), (1000, 300, 500)])
 def test_matmul_backward_transposed_loads_match_copies(hip, monkeypatch, m, k, n):
     """Where the plan allows, the backward's GEMMs read b^T / a^T straight
-    from b / a; the result must be the same bits as transposing first
-    (CLOVE_GEMM_TRANSPOSED=0), and shapes the direct path does not take
-    must give the same bits either way too."""
+    from b / a, by buffer->LDS DMA (the default) or through registers
+    (CLOVE_GEMM_DMA=0); the result must be the same bits as transposing
+    first (CLOVE_GEMM_TRANSPOSED=0), and shapes the direct path does not
+    take must give the same bits either way too."""
     g = rng(m + 3 * k + 7 * n)
     a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
     b = g.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32)
     dc = g.normal(0, 1, (m, n)).astype(np.float32)
     ta, tb, tdc = hip.tensor(a), hip.tensor(b), hip.tensor(dc)
     da, db = (t.numpy() for t in hip.matmul_backward(ta, tb, tdc))
+    monkeypatch.setenv("CLOVE_GEMM_DMA", "0")
+    da1, db1 = (t.numpy() for t in hip.matmul_backward(ta, tb, tdc))
+    assert np.array_equal(da, da1) and np.array_equal(db, db1)
+    monkeypatch.delenv("CLOVE_GEMM_DMA")
     monkeypatch.setenv("CLOVE_GEMM_TRANSPOSED", "0")
     da0, db0 = (t.numpy() for t in hip.matmul_backward(ta, tb, tdc))
     assert np.array_equal(da, da0) and np.array_equal(db, db0)
