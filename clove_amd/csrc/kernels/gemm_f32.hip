@@ -86,9 +86,12 @@ __device__ __forceinline__ bool gemm_tile(const GemmArgs &g, int *tile) {
 // Epilogue: C = act(acc + bias[(row*N + col) % bias_n]), each step rounded
 // in f32 exactly as Clove's separate Add (backend.rs:1489) and ReLU
 // (:1823) / GELU (:1924) passes round it.
-__device__ __forceinline__ float epilogue(const GemmEpilogue &e, float v, int row, int col, int N) {
+// bcol: bias[col] when the caller has loaded it already (GEMM_BIAS_COL), so
+// that the load is not repeated after every store to C, which may alias it.
+__device__ __forceinline__ float epilogue(const GemmEpilogue &e, float v, int row, int col, int N,
+                                          const float *bcol = nullptr) {
 #pragma clang fp contract(off)
-    if (e.bias_mode == GEMM_BIAS_COL) v = v + e.bias[col];
+    if (e.bias_mode == GEMM_BIAS_COL) v = v + (bcol ? *bcol : e.bias[col]);
     else if (e.bias_mode == GEMM_BIAS_SCALAR) v = v + e.bias[0];
     else if (e.bias_mode == GEMM_BIAS_MOD) v = v + e.bias[((uint64_t)row * N + col) % e.bias_n];
     if (e.act == GEMM_ACT_RELU) {
@@ -98,6 +101,17 @@ __device__ __forceinline__ float epilogue(const GemmEpilogue &e, float v, int ro
         const float x3 = (v * v) * v;
         v = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * x3)));
     }
+    return v;
+}
+
+// One accumulator element read out of its AGPR for the fused epilogue.
+// Without it the compiler copies every accumulator of the wave into VGPRs
+// when the K loop ends (128 more VGPRs at 128 x 256 and 256 x 128: one wave
+// per SIMD instead of two, 4096^3 with bias + ReLU 1.128 ms against 0.973
+// plain); read one at a time, the epilogue needs a few registers.
+__device__ __forceinline__ float acc_read(float x) {
+    float v;
+    asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(x));
     return v;
 }
 
@@ -334,6 +348,12 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
     // Accumulator element e of block (i, j) is tile element (r, c) with
     // r = wm0 + 32*i + 8*(e/4) + 4*h + e%4 and c = wn0 + 32*j + l%32.
     if (g.splits == 1) {
+        float bc[Cfg::kBlocksN];  // per-column bias, loaded before any store
+#pragma unroll
+        for (int j = 0; j < Cfg::kBlocksN; ++j) {
+            const int col = n0 + wn0 + 32 * j + l32;
+            bc[j] = EPI && g.epi.bias_mode == GEMM_BIAS_COL && col < N ? g.epi.bias[col] : 0.0f;
+        }
 #pragma unroll
         for (int i = 0; i < Cfg::kBlocksM; ++i)
 #pragma unroll
@@ -342,9 +362,13 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
                 for (int e = 0; e < 16; ++e) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
-                    if (!EDGE || (row < M && col < N))
-                        g.C[(size_t)row * N + col] =
-                            EPI ? epilogue(g.epi, acc[i][j][e], row, col, N) : acc[i][j][e];
+                    if (!EDGE || (row < M && col < N)) {
+                        if constexpr (EPI)
+                            g.C[(size_t)row * N + col] =
+                                epilogue(g.epi, acc_read(acc[i][j][e]), row, col, N, &bc[j]);
+                        else
+                            g.C[(size_t)row * N + col] = acc[i][j][e];
+                    }
                 }
         return;
     }
@@ -518,6 +542,11 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
     // Accumulator element e of block (i, j) is tile element (r, c) with
     // r = wm0 + 32*i + 8*(e/4) + 4*h + e%4 and c = wn0 + 32*j + l%32.
     if (g.splits == 1) {
+        float bc[BNb];  // per-column bias, loaded before any store
+#pragma unroll
+        for (int j = 0; j < BNb; ++j)
+            bc[j] = EPI && g.epi.bias_mode == GEMM_BIAS_COL ? g.epi.bias[n0 + wn0 + 32 * j + l32]
+                                                            : 0.0f;
 #pragma unroll
         for (int i = 0; i < BMb; ++i)
 #pragma unroll
@@ -526,8 +555,11 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
                 for (int e = 0; e < 16; ++e) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
-                    g.C[(size_t)row * N + col] =
-                        EPI ? epilogue(g.epi, acc[i][j][e], row, col, N) : acc[i][j][e];
+                    if constexpr (EPI)
+                        g.C[(size_t)row * N + col] =
+                            epilogue(g.epi, acc_read(acc[i][j][e]), row, col, N, &bc[j]);
+                    else
+                        g.C[(size_t)row * N + col] = acc[i][j][e];
                 }
         return;
     }
