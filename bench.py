@@ -20,8 +20,9 @@ Rank 0 prints ONE JSON line on stdout:
                unfused passes as Clove's eager CPU path runs them, timed on
                this host's cores; every CPU leg runs after all GPU timings
   parts        the other configurations measured in the same run: the
-               broadcast chain, softmax and layer norm (GB/s), 4096^3 and
-               skinny matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
+               broadcast chain, softmax and layer norm (GB/s), 4096^3 (plain
+               and with the planner's fused bias + GELU epilogue) and skinny
+               matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
                MLP plan (us per forward) and the backward passes and losses
                (GB/s; the matmul backward in TFLOP/s), attention prefill
                (TFLOP/s) and RoPE (GB/s), each with its roofline fraction and
@@ -224,6 +225,25 @@ def bench_matmul(ca, oracle, args, out):
     out["matmul_4096"] = part
     log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
         f"{per.mean():.3f} ms")
+    # the planner's GEMM with a fused bias + GELU epilogue (one step)
+    bias = ca.empty((4096,)).fill_normal(7)
+    g = ca.Graph()
+    x, w, bi = g.input("4096,4096"), g.input("4096,4096"), g.input("4096")
+    model = g.compile([g.op("gelu", g.op("add", g.op("matmul", x, w), bi))])
+    assert model.num_steps == 1, model.describe()
+    wall, per = timed(ca, lambda: model.execute([a, b, bias])[0], steps, args.warmup)
+    tf = flops / (per.mean() * 1e-3) / 1e12
+    epart = {"value": round(tf, 2), "unit": "TFLOP/s", "ms": round(per.mean(), 4),
+             "roofline": roofline("mfma", tf, FP32_MFMA_PEAK_TFS, "TFLOP/s")}
+    if not args.no_cpu:
+        def eleg():
+            ah, bh, biash = a.numpy(), b.numpy(), bias.numpy()
+            t = cpu_time(lambda: oracle.gelu(oracle.add(oracle.matmul(ah, bh), biash)), reps=1)
+            epart["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
+                                               "full 4096^3 product, bias and GELU, one run")
+        defer(eleg)
+    out["matmul_4096_bias_gelu"] = epart
+    log(f"matmul 4096^3 + bias + GELU (fused): {tf:.1f} TFLOP/s, {per.mean():.3f} ms")
     # B (64 MiB) is what the skinny product streams: one copy per input set
     bs = [b] + [ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64) for _ in range(args.sets - 1)]
     wall, per = timed(ca, rotating([lambda bb=bb: ca.matmul(a32, bb) for bb in bs]), args.steps,
