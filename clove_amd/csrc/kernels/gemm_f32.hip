@@ -362,12 +362,16 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
                 for (int e = 0; e < 16; ++e) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
-                    if (!EDGE || (row < M && col < N)) {
-                        if constexpr (EPI)
-                            g.C[(size_t)row * N + col] =
-                                epilogue(g.epi, acc_read(acc[i][j][e]), row, col, N, &bc[j]);
-                        else
-                            g.C[(size_t)row * N + col] = acc[i][j][e];
+                    // the epilogue is evaluated for every element (bc is 0
+                    // past N, the modulo bias index is always in range): an
+                    // accumulator read inside the bounds test stops the loop
+                    // from unrolling, and the accumulators go to scratch
+                    if constexpr (EPI) {
+                        const float v =
+                            epilogue(g.epi, acc_read(acc[i][j][e]), row, col, N, &bc[j]);
+                        if (!EDGE || (row < M && col < N)) g.C[(size_t)row * N + col] = v;
+                    } else {
+                        if (!EDGE || (row < M && col < N)) g.C[(size_t)row * N + col] = acc[i][j][e];
                     }
                 }
         return;

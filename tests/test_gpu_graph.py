@@ -137,6 +137,37 @@ def test_gemm_epilogue_matches_eager_bits(hip, m, k, n, bias_n, act):
     assert np.array_equal(fused.numpy(), eager.numpy())
 
 
+@pytest.mark.parametrize("cfg", ["5", "4"])  # 128x256 and 256x128 tiles
+@pytest.mark.parametrize("m,k,n,bias_n,act", [(1000, 64, 1100, 1100, "gelu"),
+                                               (1000, 64, 1101, 7, "relu"),
+                                               (700, 60, 900, 1, None)])
+def test_gemm_epilogue_edge_tiles_large_configs(hip, monkeypatch, cfg, m, k, n, bias_n, act):
+    """The fused epilogue on the bounds-checked kernels of the two largest
+    tile shapes (ragged M and N, K short enough for one split): the same
+    bits as the eager composition."""
+    monkeypatch.setenv("CLOVE_GEMM_CFG", cfg)
+    gg = rng(3 * m + n + int(cfg))
+    a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    w = gg.normal(0, 1, (k, n)).astype(np.float32)
+    b = gg.normal(0, 1, bias_n).astype(np.float32)
+    g = hip.Graph()
+    x, wi, bi = g.input(f"{m},{k}"), g.input(f"{k},{n}"), g.input(f"{bias_n}")
+    y = g.op("add", g.op("matmul", x, wi), bi)
+    if act:
+        y = g.op(act, y)
+    model = g.compile([y])
+    assert model.num_steps == 1, model.describe()
+    ta, tw, tb = hip.tensor(a), hip.tensor(w), hip.tensor(b)
+    (fused,) = model.execute([ta, tw, tb])
+    eager = hip.add(hip.matmul(ta, tw), tb)
+    if act:
+        eager = getattr(hip, act)(eager)
+    assert np.array_equal(fused.numpy(), eager.numpy())
+    pre = oracle.add(oracle.matmul(a, w), b)
+    want = getattr(oracle, act)(pre) if act else pre
+    assert_close(fused.numpy(), want, 2e-3, 1e-4 * float(np.abs(want).max()), "edge epilogue")
+
+
 def test_concurrent_callers(hip):
     """The C ABI serialises host-side calls under one lock; callers on several
     threads get the same results as one caller."""
