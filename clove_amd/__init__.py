@@ -70,6 +70,7 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_last_error": (C.c_char_p, []),
         "clove_hip_last_status": (C.c_int, []),
         "clove_hip_synchronize": (C.c_int, []),
+        "clove_hip_jit_stats": (C.c_int, [C.POINTER(C.c_int), C.POINTER(C.c_int)]),
         "clove_hip_set_stream": (C.c_int, [vp]),
         "clove_hip_get_stream": (vp, []),
         "clove_hip_empty_cache": (C.c_int, []),
@@ -191,6 +192,14 @@ def shutdown() -> None:
 
 def synchronize() -> None:
     _check(lib().clove_hip_synchronize())
+
+
+def jit_stats() -> tuple:
+    """(chains compiled with hipRTC, chains loaded from the on-disk
+    code-object cache) in this process."""
+    compiled, loaded = C.c_int(0), C.c_int(0)
+    _check(lib().clove_hip_jit_stats(C.byref(compiled), C.byref(loaded)))
+    return compiled.value, loaded.value
 
 
 def empty_cache() -> None:

@@ -91,6 +91,9 @@ void *clove_hip_get_stream(void) {
     guarded([&] { s = clove::ctx().stream; });
     return s;
 }
+int clove_hip_jit_stats(int *compiled, int *disk_loads) {
+    return guarded([&] { clove::jit_stats(compiled, disk_loads); });
+}
 int clove_hip_empty_cache(void) {
     return guarded([] {
         clove::ctx();

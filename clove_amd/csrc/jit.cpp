@@ -18,7 +18,10 @@
 //   - indices are 64-bit and vectorised; the reference dispatches one thread
 //     per element with 32-bit indices and a `%` per operand per element.
 #include <hip/hiprtc.h>
+#include <sys/stat.h>
+#include <unistd.h>
 
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <sstream>
@@ -181,17 +184,117 @@ std::string signature(const std::vector<ChainOp> &ops, const std::vector<int> &m
     return s.str();
 }
 
+const char *const kRtcOpts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++17",
+                                // no packed-f32 instructions in any device code of this library
+                                "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
+constexpr int kNumRtcOpts = (int)(sizeof(kRtcOpts) / sizeof(kRtcOpts[0]));
+
+int g_compiles = 0, g_disk_loads = 0;
+
+// ---- code objects on disk -------------------------------------------------
+// A chain compiled once is kept as a code object under CLOVE_JIT_CACHE (a
+// directory; "0" or "off" turns the cache off), by default
+// $XDG_CACHE_HOME/clove_hip or $HOME/.cache/clove_hip, so a new process
+// loads it instead of running hipRTC again (tens to hundreds of ms per
+// chain).  The file holds the whole key -- generated source, the embedded
+// headers, the compile options and the hipRTC version -- and is used only if
+// that key matches exactly, so a changed library or toolchain never loads a
+// stale object.  Files are written to a temporary name and renamed, so a
+// reader never sees a partial one; any failure to read or write just means
+// compiling.
+const char kCacheMagic[8] = {'C', 'L', 'V', 'J', 'I', 'T', '0', '1'};
+
+std::string cache_dir() {
+    const char *v = std::getenv("CLOVE_JIT_CACHE");
+    if (v) {
+        if (!*v || !std::strcmp(v, "0") || !std::strcmp(v, "off")) return "";
+        return v;
+    }
+    if (const char *x = std::getenv("XDG_CACHE_HOME"); x && *x) return std::string(x) + "/clove_hip";
+    if (const char *h = std::getenv("HOME"); h && *h) return std::string(h) + "/.cache/clove_hip";
+    return "";
+}
+
+std::string cache_key(const std::string &src) {
+    int maj = 0, min = 0;
+    hiprtcVersion(&maj, &min);
+    std::string k = src;
+    for (const char *h : {kAbiSrc, kDeviceSrc, kKernelSrc}) k += std::string("\x01") + h;
+    for (int i = 0; i < kNumRtcOpts; ++i) k += std::string("\x02") + kRtcOpts[i];
+    k += "\x03hiprtc " + std::to_string(maj) + "." + std::to_string(min);
+    return k;
+}
+
+std::string cache_path(const std::string &dir, const std::string &key) {
+    uint64_t h = 1469598103934665603ull;  // FNV-1a
+    for (unsigned char c : key) h = (h ^ c) * 1099511628211ull;
+    char name[32];
+    std::snprintf(name, sizeof(name), "%016llx.co", (unsigned long long)h);
+    return dir + "/" + name;
+}
+
+bool cache_read(const std::string &path, const std::string &key, std::vector<char> *code) {
+    FILE *f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    char magic[8];
+    uint64_t klen = 0, clen = 0;
+    bool ok = std::fread(magic, 1, 8, f) == 8 && !std::memcmp(magic, kCacheMagic, 8) &&
+              std::fread(&klen, 8, 1, f) == 1 && klen == key.size();
+    if (ok) {
+        std::string k(klen, '\0');
+        ok = std::fread(&k[0], 1, klen, f) == klen && k == key && std::fread(&clen, 8, 1, f) == 1 &&
+             clen > 0 && clen < (256u << 20);
+        if (ok) {
+            code->resize(clen);
+            ok = std::fread(code->data(), 1, clen, f) == clen;
+        }
+    }
+    std::fclose(f);
+    return ok;
+}
+
+void cache_write(const std::string &dir, const std::string &path, const std::string &key,
+                 const std::vector<char> &code) {
+    for (size_t i = 1; i <= dir.size(); ++i)  // mkdir -p
+        if (i == dir.size() || dir[i] == '/') (void)mkdir(dir.substr(0, i).c_str(), 0755);
+    const std::string tmp = path + ".tmp" + std::to_string((long)getpid());
+    FILE *f = std::fopen(tmp.c_str(), "wb");
+    if (!f) return;
+    const uint64_t klen = key.size(), clen = code.size();
+    const bool ok = std::fwrite(kCacheMagic, 1, 8, f) == 8 && std::fwrite(&klen, 8, 1, f) == 1 &&
+                    std::fwrite(key.data(), 1, klen, f) == klen &&
+                    std::fwrite(&clen, 8, 1, f) == 1 &&
+                    std::fwrite(code.data(), 1, clen, f) == clen;
+    if (std::fclose(f) != 0 || !ok || std::rename(tmp.c_str(), path.c_str()) != 0)
+        (void)std::remove(tmp.c_str());
+}
+
+Compiled load_code(const std::vector<char> &code, const std::string &name) {
+    Compiled c;
+    CLOVE_HIP_CHECK(hipModuleLoadData(&c.module, code.data()));
+    CLOVE_HIP_CHECK(hipModuleGetFunction(&c.fn, c.module, name.c_str()));
+    return c;
+}
+
 Compiled compile(const std::string &src, const std::string &name) {
+    const std::string dir = cache_dir();
+    std::string key, path;
+    if (!dir.empty()) {
+        key = cache_key(src);
+        path = cache_path(dir, key);
+        std::vector<char> code;
+        if (cache_read(path, key, &code)) {
+            ++g_disk_loads;
+            return load_code(code, name);
+        }
+    }
     hiprtcProgram prog;
     const char *headers[] = {kAbiSrc, kDeviceSrc, kKernelSrc};
     const char *names[] = {"ew_abi.h", "ew_device.h", "ew_chain_kernel.h"};
     if (hiprtcCreateProgram(&prog, src.c_str(), "clove_chain.hip", 3, headers, names) !=
         HIPRTC_SUCCESS)
         fail(CLOVE_HIP_ERR_JIT, "hiprtcCreateProgram failed");
-    const char *opts[] = {"--offload-arch=gfx950", "-O3", "-ffp-contract=off", "-std=c++17",
-                          // no packed-f32 instructions in any device code of this library
-                          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"};
-    hiprtcResult r = hiprtcCompileProgram(prog, (int)(sizeof(opts) / sizeof(opts[0])), opts);
+    hiprtcResult r = hiprtcCompileProgram(prog, kNumRtcOpts, kRtcOpts);
     if (r != HIPRTC_SUCCESS) {
         size_t n = 0;
         hiprtcGetProgramLogSize(prog, &n);
@@ -205,9 +308,9 @@ Compiled compile(const std::string &src, const std::string &name) {
     std::vector<char> code(code_size);
     hiprtcGetCode(prog, code.data());
     hiprtcDestroyProgram(&prog);
-    Compiled c;
-    CLOVE_HIP_CHECK(hipModuleLoadData(&c.module, code.data()));
-    CLOVE_HIP_CHECK(hipModuleGetFunction(&c.fn, c.module, name.c_str()));
+    ++g_compiles;
+    Compiled c = load_code(code, name);
+    if (!dir.empty()) cache_write(dir, path, key, code);
     return c;
 }
 
@@ -348,5 +451,10 @@ void jit_shutdown() {
 }
 
 int jit_compiled_count() { return (int)g_cache.size(); }
+
+void jit_stats(int *compiled, int *disk_loads) {
+    if (compiled) *compiled = g_compiles;
+    if (disk_loads) *disk_loads = g_disk_loads;
+}
 
 }  // namespace clove

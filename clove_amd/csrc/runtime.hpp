@@ -60,6 +60,9 @@ void jit_shutdown();
 void rope_cache_clear();
 // Diagnostics for tests: number of chains compiled so far.
 int jit_compiled_count();
+// Chains compiled with hipRTC and chains loaded from the on-disk cache by
+// this process so far.
+void jit_stats(int *compiled, int *disk_loads);
 
 // ---- eager backend (ops.cpp): mirrors trait Backend (backend.rs:171-257) --
 

@@ -94,6 +94,12 @@ void *clove_hip_get_stream(void);
 int clove_hip_empty_cache(void);
 /* Bytes currently held by the caching allocator (in use + cached). */
 size_t clove_hip_memory_reserved(void);
+/* Fused chains this process compiled with hipRTC, and chains it loaded from
+ * the on-disk code-object cache (directory CLOVE_JIT_CACHE, default
+ * $XDG_CACHE_HOME/clove_hip or $HOME/.cache/clove_hip; "0" turns it off).
+ * No counterpart in the reference (its WGSL pipelines are rebuilt by wgpu
+ * in every process); for callers that track start-up cost. */
+int clove_hip_jit_stats(int *compiled, int *disk_loads);
 
 /* ---------------------------------------------------------------------- */
 /* Tensor lifecycle.  ffi.rs:71-113.                                      */
