@@ -559,7 +559,8 @@ def main():
         ap.error("--sets must be at least 1")
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
-              "build (see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "build (the decode path would shard by sequence and head, the rest by rows)",
+              file=sys.stderr)
         sys.exit(2)
 
     import clove_amd as ca
