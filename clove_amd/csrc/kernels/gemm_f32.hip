@@ -417,12 +417,20 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 // follows its last reads (their values fed MFMAs issued before it).
 // Measured at 4096^3 on one box: 972 us (141 TFLOP/s) against 1005-1026 us
 // for the register-staged form; double buffering (969 us) and 256 x 256
-// tiles with 8 waves (961-982 us) within noise of it.
+// tiles with 8 waves (961-982 us) within noise of it.  Deeper slabs with one
+// workgroup per CU (BK = 32 with 3 or 2 stages, BK = 16 with 4: 96-144 KiB
+// of LDS) ran 1.020-1.047 ms against 0.963-0.967 ms, the same bits: the
+// second workgroup on a CU is what fills each one's barrier and LDS waits.
 constexpr int kDmaStages = 3;
 
-template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, bool TB = false>
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; lgkmcnt and
+// expcnt left at their maxima, so they are not waited for).
+constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
+
+template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, bool TB = false,
+          int ST = kDmaStages>
 __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
-    constexpr int ST = kDmaStages;
     constexpr int SA = BM * BK, SB = BK * BN, SS = SA + SB;
     constexpr int IAW = SA / 256 / 4, IBW = SB / 256 / 4;  // 1 KiB DMAs per wave per slab
     constexpr int KQ = BK / 4;                              // 16-byte slots per A row
@@ -495,10 +503,12 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
         if (sl < slabs) dma(sl);
     for (int sl = 0; sl < slabs; ++sl) {
         // slab sl has landed once at most the later slabs' DMAs (IAW + IBW
-        // per slab, ST - 2 slabs) are outstanding
-        static_assert(ST == 3, "the wait below counts one later slab");
-        if (sl + 1 < slabs) __builtin_amdgcn_s_waitcnt(0x0F70 | (IAW + IBW));
-        else __builtin_amdgcn_s_waitcnt(0x0F70);
+        // per slab; min(ST - 2, slabs - 1 - sl) slabs) are outstanding
+        static_assert(ST >= 2 && ST <= 4 && (ST - 2) * (IAW + IBW) < 64, "vmcnt range");
+        const int later = min(ST - 2, slabs - 1 - sl);
+        if (ST >= 4 && later >= 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * (IAW + IBW)));
+        else if (ST >= 3 && later >= 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm(IAW + IBW));
+        else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
         asm volatile("s_barrier" ::: "memory");
         if (sl + ST - 1 < slabs) dma(sl + ST - 1);
         const float *sA = smem + (sl % ST) * SS, *sB = sA + SA;
