@@ -239,33 +239,38 @@ __device__ __forceinline__ int64_t table_entry(const int (&tab)[kTabRegs], int i
 }
 
 // Folds `n` whole blocks (n <= 64 * kTabRegs) whose table entries `tab`
-// holds, all inside the pool, two register buffers deep: block i + 1's loads
-// are in flight while block i is folded.  Every load is unconditional, so
-// the wait before each fold only drains the older buffer.
-template <int D, int BS>
+// holds, all inside the pool, two register buffers deep: sub-block i + 1's
+// loads are in flight while sub-block i is folded.  A block of BS tokens is
+// folded as BS / SB sub-blocks of SB consecutive tokens (rows), each one
+// step of the online softmax.  Every load is unconditional, so the wait
+// before each fold only drains the older buffer.
+template <int D, int BS, int SB>
 __device__ __forceinline__ void fold_pipelined(const PagedArgs &a, const int (&tab)[kTabRegs],
                                                int n, size_t lane_off, size_t row_stride,
                                                const cl_f4 (&q)[D / 64], WaveState &st,
                                                cl_f4 (&o)[D / 64]) {
+    constexpr int NS = BS / SB;
     const size_t blk_stride = (size_t)BS * row_stride;
-    BlockRegs<D, BS> A, B;
+    auto sub_off = [&](int j) {  // sub-block j of the partition's whole blocks
+        return (size_t)table_entry(tab, j / NS) * blk_stride + lane_off +
+               (size_t)((j % NS) * SB) * row_stride;
+    };
+    const int subs = n * NS;
+    BlockRegs<D, SB> A, B;
     int i = 0;
-    issue_block<D, BS>(a, (size_t)table_entry(tab, 0) * blk_stride + lane_off, row_stride, A);
-    for (; i + 2 < n; i += 2) {
-        issue_block<D, BS>(a, (size_t)table_entry(tab, i + 1) * blk_stride + lane_off, row_stride,
-                           B);
-        consume_block<D, BS>(a, A, q, st, o);
-        issue_block<D, BS>(a, (size_t)table_entry(tab, i + 2) * blk_stride + lane_off, row_stride,
-                           A);
-        consume_block<D, BS>(a, B, q, st, o);
+    issue_block<D, SB>(a, sub_off(0), row_stride, A);
+    for (; i + 2 < subs; i += 2) {
+        issue_block<D, SB>(a, sub_off(i + 1), row_stride, B);
+        consume_block<D, SB>(a, A, q, st, o);
+        issue_block<D, SB>(a, sub_off(i + 2), row_stride, A);
+        consume_block<D, SB>(a, B, q, st, o);
     }
-    if (i + 1 < n) {
-        issue_block<D, BS>(a, (size_t)table_entry(tab, i + 1) * blk_stride + lane_off, row_stride,
-                           B);
-        consume_block<D, BS>(a, A, q, st, o);
-        consume_block<D, BS>(a, B, q, st, o);
+    if (i + 1 < subs) {
+        issue_block<D, SB>(a, sub_off(i + 1), row_stride, B);
+        consume_block<D, SB>(a, A, q, st, o);
+        consume_block<D, SB>(a, B, q, st, o);
     } else {
-        consume_block<D, BS>(a, A, q, st, o);
+        consume_block<D, SB>(a, A, q, st, o);
     }
 }
 
@@ -278,6 +283,13 @@ __device__ __forceinline__ void fold_pipelined(const PagedArgs &a, const int (&t
 template <int D, int BS, int HPW>
 __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
     constexpr int NV = D / 64;
+    // Tokens per online-softmax step.  A whole block at head_dim 256 and 32
+    // tokens is 512 floats of K and V per lane, two of them twice that: the
+    // pipeline spilled to scratch (5.5 against 6.2 TB/s with 16-token
+    // blocks).  There the block is folded as two 16-token halves, in every
+    // path alike, so all paths still round the same way.
+    constexpr int SB = (D >= 256 && BS >= 32) ? BS / 2 : BS;
+    constexpr int NS = BS / SB;
     const int part = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int h = blockIdx.x * HPW + wave;
@@ -326,7 +338,7 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
         bad = bad || tab[r] < 0 || tab[r] >= nb;
     }
     if (n_full > 0 && n_full <= 64 * kTabRegs && !__any(bad)) {
-        fold_pipelined<D, BS>(a, tab, n_full, lane_off, row_stride, q, st, o);
+        fold_pipelined<D, BS, SB>(a, tab, n_full, lane_off, row_stride, q, st, o);
     } else {
         for (int lb = lb_first; lb < full_end; ++lb) {
             const int64_t blk = bt[lb];
@@ -334,9 +346,13 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
                 if (lane == 0) atomicOr(a.err_flag, kErrPagedRange);
                 continue;
             }
-            BlockRegs<D, BS> r;
-            issue_block<D, BS>(a, (size_t)blk * BS * row_stride + lane_off, row_stride, r);
-            consume_block<D, BS>(a, r, q, st, o);
+#pragma unroll
+            for (int sb = 0; sb < NS; ++sb) {
+                BlockRegs<D, SB> r;
+                issue_block<D, SB>(a, (size_t)(blk * BS + sb * SB) * row_stride + lane_off,
+                                   row_stride, r);
+                consume_block<D, SB>(a, r, q, st, o);
+            }
         }
     }
     if (tail_checked) {
@@ -345,8 +361,13 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
             if (lane == 0) atomicOr(a.err_flag, kErrPagedRange);
         } else {
             const size_t off = (size_t)blk * BS * row_stride + lane_off;
-            fold_block<D, BS, true>(a, a.k_cache + off, a.v_cache + off, row_stride, lb_last * BS,
-                                    t_end, ctx, row, new_off, q, st, o);
+#pragma unroll
+            for (int sb = 0; sb < NS; ++sb) {
+                const size_t so = off + (size_t)(sb * SB) * row_stride;
+                fold_block<D, SB, true>(a, a.k_cache + so, a.v_cache + so, row_stride,
+                                        lb_last * BS + sb * SB, t_end, ctx, row, new_off, q, st,
+                                        o);
+            }
         }
     }
     st.l += __shfl_xor(st.l, 16, 64);

@@ -42,10 +42,13 @@ def test_head_dims_and_block_sizes(hip, D, bs):
     assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs}")
 
 
-@pytest.mark.parametrize("ctx", [[1, 2, 15, 16], [17, 511, 512, 513], [1024, 1535, 2049, 0]])
-def test_context_edges_with_new_token(hip, ctx):
-    H, D, bs, mb = 4, 128, 16, 160
-    q, kn, vn, kv, bt, cl = make(sum(ctx), 4, H, D, bs, 4 * mb, mb, ctx)
+@pytest.mark.parametrize("D,bs,ctx", [(128, 16, [1, 2, 15, 16]), (128, 16, [17, 511, 512, 513]),
+                                      (128, 16, [1024, 1535, 2049, 0]),
+                                      (256, 32, [1, 16, 17, 32]), (256, 32, [33, 511, 512, 2049])])
+def test_context_edges_with_new_token(hip, D, bs, ctx):
+    H = 4
+    mb = 2560 // bs
+    q, kn, vn, kv, bt, cl = make(sum(ctx) + D, 4, H, D, bs, 4 * mb, mb, ctx)
     want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(4, H * D)
     assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"ctx={ctx}")
     want = oracle.paged_attention(q, None, None, kv, bt, cl).reshape(4, H * D)
@@ -179,10 +182,17 @@ def test_config5_f32_tables_equal_int32_tables(hip, config5):
                                                   int(c["ctx"].max())))
 
 
-def test_kv_append_then_cached_decode_equals_new_token_decode(hip):
+@pytest.mark.parametrize("D,bs,ctx", [(128, 16, [1, 16, 17, 300]), (256, 32, [1, 32, 33, 320]),
+                                      (256, 16, [2, 16, 31, 300]), (64, 32, [1, 31, 64, 301])])
+def test_kv_append_then_cached_decode_equals_new_token_decode(hip, D, bs, ctx):
     """The append writes k/v at slot ctx-1; decoding from the cache afterwards
-    gives exactly the new-token decode (same rows, same order)."""
-    q, kn, vn, kv, bt, cl = make(10, 4, 4, 128, 16, 200, 32, [1, 16, 17, 300])
+    gives exactly the new-token decode (same rows, same order).  A context
+    that ends on a block edge folds its last block through the pipelined path
+    when cached and through the checked one with the new token, so the two
+    paths must round alike (also where a block is folded in two halves,
+    head_dim 256 with 32-token blocks)."""
+    q, kn, vn, kv, bt, cl = make(10 + D + bs, 4, 4, D, bs, 4 * (320 // bs + 1) + 8,
+                                 320 // bs + 1, ctx)
     t = hip.tensor
     tkv, tbt, tcl = t(kv), t(bt), t(cl)
     fresh = hip.paged_attention(t(q), t(kn), t(vn), tkv, tbt, tcl).numpy()
