@@ -1411,10 +1411,27 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         p.vec = true;
         return p;
     }
-    // 128x256 tiles measured ~3% faster than 128x128 at 4096^3; they are used
-    // whenever they alone still give every CU a tile.
+    // 128x256 or 128x128 tiles, once 128x256 tiles alone give every CU one.
+    // All tiles of a launch take equally long, so a launch costs its rounds
+    // of co-resident workgroups (two 128x256 or three 128x128 per CU, as
+    // their LDS allows) times the time of one tile: a 128x128 tile three to
+    // a CU takes about 3/4 of a 128x256 tile two to a CU (measured:
+    // 4096 x 4096 x 16384 runs equally fast either way).  A tile count just
+    // past a whole round is what this avoids: 4097 x 4096 x 4096 makes 528
+    // 128x256 tiles, two rounds on 256 CUs (1.616 ms), or 1056 128x128
+    // tiles, also two rounds but of shorter tiles (1.345 ms); 3072 x 4096 x
+    // 4096 leaves a quarter of the 128x256 slots idle (0.963 against 0.746
+    // ms).  128x256 keeps one round at 4096^3 (0.968 against 1.161 ms).
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
-    if (cfg == CFG_128x128 && ((M + 127) / 128) * ((N + 255) / 256) >= num_cus) cfg = CFG_128x256;
+    if (cfg == CFG_128x128) {
+        const int64_t rows = (M + 127) / 128;
+        const int64_t t256 = rows * ((N + 255) / 256), t128 = rows * ((N + 127) / 128);
+        if (t256 >= num_cus) {
+            const int64_t r256 = (t256 + 2 * num_cus - 1) / (2 * num_cus);
+            const int64_t r128 = (t128 + 3 * num_cus - 1) / (3 * num_cus);
+            if (4 * r256 <= 3 * r128) cfg = CFG_128x256;
+        }
+    }
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
     p.cfg = cfg;
     const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
