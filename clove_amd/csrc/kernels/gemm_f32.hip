@@ -422,15 +422,41 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 // of LDS) ran 1.020-1.047 ms against 0.963-0.967 ms, the same bits: the
 // second workgroup on a CU is what fills each one's barrier and LDS waits.
 constexpr int kDmaStages = 3;
+// 128 x 128 tiles keep two stages (32 KiB of LDS): four or five workgroups
+// share a CU and hide each other's waits, where three stages (48 KiB) fit
+// three.  Measured: 4096^3 in 128 x 128 tiles 0.973 against 1.201 ms, 5000
+// x 4096 x 4096 1.228 against 1.484 ms.  128 x 256 tiles keep three (two
+// stages ran 8192 x 4096 x 4096 at 2.384 against 1.939 ms).
+constexpr int dma_stages(int BN) { return BN == 128 ? 2 : kDmaStages; }
 
 // s_waitcnt immediate that waits until at most n vector-memory operations
 // are outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14; lgkmcnt and
 // expcnt left at their maxima, so they are not waited for).
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
+// EDGE: tiles may reach past M or N (K and every split whole slabs).  Rows
+// of A past M and columns of B past N (N % 4 == 0, so a 16-byte piece is all
+// in or all out) get the offset kOutside, past the end of both buffers, so
+// the DMA writes zeros there whether or not the range check counts the slab
+// step in soffset; kOutside plus any step (under K * N * 4 < 2^31) stays
+// below 2^32.  Stores and bias loads are bounds-checked.  The stored results
+// are the same bits as the register-staged kernel's, which also reads zeros.
+//
+// Workgroups of the DMA kernel that fit one CU (one wave each per SIMD): the
+// LDS ring's share of 160 KiB, and 512 registers a lane over the
+// accumulators plus 40 more.
+constexpr int dma_waves(int BM, int BN, int BK, int WM, int WN, int ST) {
+    const int lds = (160 * 1024) / (ST * (BM * BK + BK * BN) * 4);
+    const int regs = 512 / (((WM / 32) * (WN / 32) * 16 + 40 + 7) / 8 * 8);
+    return lds < regs ? lds : regs;
+}
+
 template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, bool TB = false,
-          int ST = kDmaStages>
-__global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
+          int ST = kDmaStages, bool EDGE = false>
+__global__ void __launch_bounds__(256)
+    __attribute__((amdgpu_waves_per_eu(dma_waves(BM, BN, BK, WM, WN, ST))))
+    gemm_f32_dma_kernel(GemmArgs g) {
+    static_assert(!EDGE || !(TA || TB), "transposed operands are interior-only");
     constexpr int SA = BM * BK, SB = BK * BN, SS = SA + SB;
     constexpr int IAW = SA / 256 / 4, IBW = SB / 256 / 4;  // 1 KiB DMAs per wave per slab
     constexpr int KQ = BK / 4;                              // 16-byte slots per A row
@@ -453,6 +479,7 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 4));
     const __amdgpu_buffer_rsrc_t rb = make_rsrc(g.B, (uint32_t)((size_t)K * N * 4));
     // this lane's DMA offsets at k = k_begin; each slab's step rides in soffset
+    constexpr uint32_t kOutside = 0x80000000u;
     uint32_t aoff[IAW], boff[IBW];
 #pragma unroll
     for (int u = 0; u < IAW; ++u) {
@@ -464,6 +491,7 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
             const int row = p / KQ, slot = p % KQ;
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
             aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+            if (EDGE && m0 + row >= M) aoff[u] = kOutside;
         }
     }
 #pragma unroll
@@ -476,6 +504,7 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
         } else {
             const int row = 4 * p / BN, col = 4 * p % BN;
             boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
+            if (EDGE && n0 + col >= N) boff[u] = kOutside;
         }
     }
     const int a_step = TA ? BK * M * 4 : BK * 4;  // bytes per slab
@@ -558,22 +587,29 @@ __global__ void __launch_bounds__(256) gemm_f32_dma_kernel(GemmArgs g) {
     if (g.splits == 1) {
         float bc[BNb];  // per-column bias, loaded before any store
 #pragma unroll
-        for (int j = 0; j < BNb; ++j)
-            bc[j] = EPI && g.epi.bias_mode == GEMM_BIAS_COL ? g.epi.bias[n0 + wn0 + 32 * j + l32]
-                                                            : 0.0f;
+        for (int j = 0; j < BNb; ++j) {
+            const int col = n0 + wn0 + 32 * j + l32;
+            bc[j] = EPI && g.epi.bias_mode == GEMM_BIAS_COL && (!EDGE || col < N) ? g.epi.bias[col]
+                                                                                   : 0.0f;
+        }
+        // a row's columns one after another: the row's address is live only
+        // while its BNb elements are stored
 #pragma unroll
         for (int i = 0; i < BMb; ++i)
 #pragma unroll
-            for (int j = 0; j < BNb; ++j)
+            for (int e = 0; e < 16; ++e)
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
+                for (int j = 0; j < BNb; ++j) {
                     const int row = m0 + wm0 + 32 * i + 8 * (e / 4) + 4 * h + (e % 4);
                     const int col = n0 + wn0 + 32 * j + l32;
-                    if constexpr (EPI)
-                        g.C[(size_t)row * N + col] =
+                    const bool in = !EDGE || (row < M && col < N);
+                    if constexpr (EPI) {
+                        const float v =
                             epilogue(g.epi, acc_read(acc[i][j][e]), row, col, N, &bc[j]);
-                    else
-                        g.C[(size_t)row * N + col] = acc[i][j][e];
+                        if (in) g.C[(size_t)row * N + col] = v;
+                    } else {
+                        if (in) g.C[(size_t)row * N + col] = acc[i][j][e];
+                    }
                 }
         return;
     }
@@ -1201,6 +1237,16 @@ bool dma_ok(const GemmPlan &p, int BM, int BN) {
            (uint64_t)p.M * p.K * 4 < (1ull << 31) && (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
 
+// The same for tiles reaching past M or N: 16-byte aligned rows (p.vec after
+// the pointer check) and K and every split a whole number of 16-deep slabs.
+bool dma_edge_ok(const GemmPlan &p, int BM, int BN) {
+    const char *v = std::getenv("CLOVE_GEMM_DMA");
+    const bool enabled = !(v && *v && std::atoi(v) == 0);
+    return enabled && !p.interior && p.vec && BM == 128 && (BN == 256 || BN == 128) &&
+           p.K % 16 == 0 && p.k_per_split % 16 == 0 &&
+           (uint64_t)p.M * p.K * 4 < (1ull << 31) && (uint64_t)p.K * p.N * 4 < (1ull << 31);
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     const dim3 grid((unsigned)(g.per_xcd * 8), (unsigned)p.splits);
@@ -1209,9 +1255,21 @@ void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     const bool epi = p.splits == 1 &&
                      (g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE);
     if constexpr (BM == 128 && (BN == 256 || BN == 128) && BK == 16) {
+        constexpr int ST = dma_stages(BN);
         if (dma_ok(p, BM, BN)) {
-            if (epi) gemm_f32_dma_kernel<BM, BN, BK, WM, WN, true><<<grid, 256, 0, s>>>(g);
-            else gemm_f32_dma_kernel<BM, BN, BK, WM, WN, false><<<grid, 256, 0, s>>>(g);
+            if (epi)
+                gemm_f32_dma_kernel<BM, BN, BK, WM, WN, true, false, false, ST><<<grid, 256, 0, s>>>(g);
+            else
+                gemm_f32_dma_kernel<BM, BN, BK, WM, WN, false, false, false, ST><<<grid, 256, 0, s>>>(g);
+            return;
+        }
+        if (dma_edge_ok(p, BM, BN)) {
+            if (epi)
+                gemm_f32_dma_kernel<BM, BN, BK, WM, WN, true, false, false, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
+            else
+                gemm_f32_dma_kernel<BM, BN, BK, WM, WN, false, false, false, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
             return;
         }
     }
@@ -1411,37 +1469,27 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         p.vec = true;
         return p;
     }
-    // 128x256 or 128x128 tiles, once 128x256 tiles alone give every CU one.
-    // All tiles of a launch take equally long, so a launch costs its rounds
-    // of co-resident workgroups (two 128x256 or three 128x128 per CU, as
-    // their LDS allows) times the time of one tile: a 128x128 tile three to
-    // a CU takes about 3/4 of a 128x256 tile two to a CU (measured:
-    // 4096 x 4096 x 16384 runs equally fast either way).  A tile count just
-    // past a whole round is what this avoids: 4097 x 4096 x 4096 makes 528
-    // 128x256 tiles, two rounds on 256 CUs (1.616 ms), or 1056 128x128
-    // tiles, also two rounds but of shorter tiles (1.345 ms); 3072 x 4096 x
-    // 4096 leaves a quarter of the 128x256 slots idle (0.963 against 0.746
-    // ms).  128x256 keeps one round at 4096^3 (0.968 against 1.161 ms).
+    // 128x128 tiles above 64 rows.  Their two-stage DMA ring (32 KiB of LDS)
+    // lets four or five workgroups share a CU, and the time then follows the
+    // work with no steps at whole rounds of co-resident workgroups: 5000 x
+    // 4096 x 4096 1.230 ms against 1.657 in 128x256 tiles (two to a CU, 640
+    // tiles: two rounds), 7168 x 4096 x 4096 1.700 against 1.944, 4096^3
+    // 0.974 against 0.975 (one round of each).  128x256 stays selectable
+    // (CLOVE_GEMM_CFG=5).
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
-    if (cfg == CFG_128x128) {
-        const int64_t rows = (M + 127) / 128;
-        const int64_t t256 = rows * ((N + 255) / 256), t128 = rows * ((N + 127) / 128);
-        if (t256 >= num_cus) {
-            const int64_t r256 = (t256 + 2 * num_cus - 1) / (2 * num_cus);
-            const int64_t r128 = (t128 + 3 * num_cus - 1) / (3 * num_cus);
-            if (4 * r256 <= 3 * r128) cfg = CFG_128x256;
-        }
-    }
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
     p.cfg = cfg;
     const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
     p.tiles_n = (N + BN - 1) / BN;
     p.tiles = ((M + BM - 1) / BM) * p.tiles_n;
-    // Split K when the tiles alone cannot fill the chip: aim for about two
-    // workgroups per CU, each split covering at least four K slabs.
+    // Split K when the tiles alone cannot fill the chip, and for 128-row
+    // tiles over K >= 1024 when they give a CU fewer than two workgroups (one
+    // alone waits on its own loads and barriers: 1024 x 4096 x 4096 in 256
+    // tiles ran 0.276 ms, 2047 x 4096 x 2052 in 272 0.497 ms): aim for about
+    // two, each split covering at least four K slabs.
     const int slabs = (K + BK - 1) / BK;
     int splits = 1;
-    if (p.tiles < num_cus) {
+    if (p.tiles < num_cus || (BM == 128 && slabs >= 64 && p.tiles < 2 * num_cus)) {
         splits = (2 * num_cus + p.tiles - 1) / p.tiles;
         const int max_splits = slabs / 4 > 1 ? slabs / 4 : 1;
         if (splits > max_splits) splits = max_splits;
@@ -1499,10 +1547,11 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
         else
             gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, false, true><<<grid, 256, 0, s>>>(g);
     } else if (p.cfg == CFG_128x128 && dma_ok(p, 128, 128)) {
+        constexpr int ST = dma_stages(128);
         if (ta)
-            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, true, false><<<grid, 256, 0, s>>>(g);
+            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, true, false, ST><<<grid, 256, 0, s>>>(g);
         else
-            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true><<<grid, 256, 0, s>>>(g);
+            gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true, ST><<<grid, 256, 0, s>>>(g);
     } else if (p.cfg == CFG_128x256) {
         if (ta)
             gemm_f32_mfma_kernel<128, 256, 16, 64, 128, false, true, false, true, false>

@@ -228,3 +228,36 @@ def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
     (fused,) = gr.compile([y]).execute([hip.tensor(a), hip.tensor(w), hip.tensor(b)])
     eager = hip.gelu(hip.add(hip.matmul(hip.tensor(a), hip.tensor(w)), hip.tensor(b)))
     assert np.array_equal(fused.numpy(), eager.numpy())
+
+
+# Tiles reaching past M or N run the DMA-staged kernel too when N % 4 == 0
+# and K % 16 == 0 (rows of A past M and columns of B past N read as zeros,
+# stores bounds-checked): the register-staged kernel's bits, single launch
+# and split-K, plain and with the fused column-bias epilogue.  N % 4 != 0 or
+# K % 16 != 0 keeps the register-staged kernel (the last two shapes).
+@pytest.mark.parametrize("cfg,m,k,n", [(5, 300, 512, 516), (2, 129, 1040, 132),
+                                       (2, 200, 8192, 260), (5, 1000, 64, 1100),
+                                       (5, 4097, 256, 4096), (2, 130, 4096, 1000),
+                                       (5, 257, 4096, 4), (2, 1, 16, 4),
+                                       (2, 300, 512, 514), (5, 300, 520, 516)])
+def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
+    monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
+    g = rng(cfg * 5 + m + 3 * k + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    bias = g.normal(0, 1, n).astype(np.float32)
+    gr = hip.Graph()
+    x, wi, bi = gr.input(f"{m},{k}"), gr.input(f"{k},{n}"), gr.input(f"{n}")
+    model = gr.compile([gr.op("add", gr.op("matmul", x, wi), bi)])
+    ta, tb, tbias = hip.tensor(a), hip.tensor(b), hip.tensor(bias)
+    dma = hip.matmul(ta, tb).numpy()
+    (dma_fused,) = model.execute([ta, tb, tbias])
+    dma_fused = dma_fused.numpy()
+    monkeypatch.setenv("CLOVE_GEMM_DMA", "0")
+    staged = hip.matmul(ta, tb).numpy()
+    (staged_fused,) = model.execute([ta, tb, tbias])
+    assert np.array_equal(dma, staged)
+    assert np.array_equal(dma_fused, staged_fused.numpy())
+    want = oracle.matmul(a, b)
+    check(dma, want, f"dma edge cfg {cfg} {m}x{k}x{n}")
+    check(dma_fused, oracle.add(want, bias), f"dma edge + bias cfg {cfg} {m}x{k}x{n}")
