@@ -391,8 +391,10 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
             }
 }
 
-// Interior tiles, A and B under 2 GiB: the same tile, waves and MFMA order
-// with the slabs moved by buffer->LDS DMA instead of through registers.
+// The 128 x 128 and 128 x 256 configurations (tiles past M or N too: EDGE
+// below), A and B under 2 GiB: the register-staged kernel's tile, waves and
+// MFMA order with the slabs moved by buffer->LDS DMA instead of through
+// registers.
 // Each lane's 16 bytes land at its instruction's LDS base + 16 * lane, and
 // the lane chooses which global 16 bytes it moves, so the LDS layout is set
 // by the lane-to-address map:
@@ -409,18 +411,21 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
 //    so a lane's four k of one column come in one ds_read_b128.
 //    Both read the same values into the same MFMA steps as the plain
 //    layouts, so the product is the same bit for bit as transposing first.
-// kDmaStages slabs rotate through LDS (72 KiB at 128 x 256, so two
-// workgroups still share a CU).  Each wave waits for its own DMAs of slab s
+// ST slabs rotate through LDS (dma_stages below: three at 128 x 256, 72 KiB,
+// two workgroups per CU; two at 128 x 128, 32 KiB, five workgroups per CU).
+// Each wave waits for its own DMAs of slab s
 // (vmcnt), then a bare s_barrier publishes them to the other waves:
 // __syncthreads() carries a fence that would wait for every DMA in flight,
 // the next slab's too.  A stage is refilled only after the barrier that
 // follows its last reads (their values fed MFMAs issued before it).
-// Measured at 4096^3 on one box: 972 us (141 TFLOP/s) against 1005-1026 us
-// for the register-staged form; double buffering (969 us) and 256 x 256
-// tiles with 8 waves (961-982 us) within noise of it.  Deeper slabs with one
-// workgroup per CU (BK = 32 with 3 or 2 stages, BK = 16 with 4: 96-144 KiB
-// of LDS) ran 1.020-1.047 ms against 0.963-0.967 ms, the same bits: the
-// second workgroup on a CU is what fills each one's barrier and LDS waits.
+// Measured at 4096^3 in 128 x 256 tiles on one box: 972 us (141 TFLOP/s)
+// against 1005-1026 us for the register-staged form; double buffering (969
+// us) and 256 x 256 tiles with 8 waves (961-982 us) within noise of it.
+// Deeper slabs with one workgroup per CU (BK = 32 with 3 or 2 stages, BK =
+// 16 with 4: 96-144 KiB of LDS) ran 1.020-1.047 ms against 0.963-0.967 ms,
+// the same bits, and BK = 32 at 128 x 128 (two workgroups per CU) lost 3%:
+// the other workgroups on a CU are what fill each one's barrier and LDS
+// waits.
 constexpr int kDmaStages = 3;
 // 128 x 128 tiles keep two stages (32 KiB of LDS): four or five workgroups
 // share a CU and hide each other's waits, where three stages (48 KiB) fit
