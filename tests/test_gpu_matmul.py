@@ -31,6 +31,21 @@ def test_matmul_shapes(hip, m, k, n):
     check(got.numpy(), oracle.matmul(a, b), f"matmul {m}x{k}x{n}")
 
 
+@pytest.mark.parametrize("m,k,n", [(2048, 1024, 2176), (1152, 2048, 3968), (2047, 1040, 2052)])
+def test_matmul_split_k_between_one_and_two_tiles_per_cu(hip, m, k, n):
+    """128x128 tiles numbering between one and two per CU with K >= 1024
+    (272, 279 and 272 tiles on 256 CUs) are split over K so that a CU gets
+    about two workgroups; the splits are summed in a fixed order, so a
+    repeated call gives the same bits."""
+    g = rng(m + 3 * k + 7 * n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, oracle.matmul(a, b), f"split {m}x{k}x{n}")
+    assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
+
+
 def test_matmul_leading_dims_and_errors(hip):
     g = rng(5)
     a = g.standard_normal((2, 3, 5)).astype(np.float32)
