@@ -200,8 +200,8 @@ int g_compiles = 0, g_disk_loads = 0;
 // headers, the compile options and the hipRTC version -- and is used only if
 // that key matches exactly, so a changed library or toolchain never loads a
 // stale object.  Files are written to a temporary name and renamed, so a
-// reader never sees a partial one; any failure to read or write just means
-// compiling.
+// reader never sees a partial one; any failure to read, load or write just
+// means compiling.
 const char kCacheMagic[8] = {'C', 'L', 'V', 'J', 'I', 'T', '0', '1'};
 
 std::string cache_dir() {
@@ -276,6 +276,17 @@ Compiled load_code(const std::vector<char> &code, const std::string &name) {
     return c;
 }
 
+// A cached object whose key matched but that the runtime will not load
+// (damaged on disk) is not fatal: the caller compiles and rewrites it.
+bool try_load_code(const std::vector<char> &code, const std::string &name, Compiled *c) {
+    if (hipModuleLoadData(&c->module, code.data()) != hipSuccess) return false;
+    if (hipModuleGetFunction(&c->fn, c->module, name.c_str()) != hipSuccess) {
+        (void)hipModuleUnload(c->module);
+        return false;
+    }
+    return true;
+}
+
 Compiled compile(const std::string &src, const std::string &name) {
     const std::string dir = cache_dir();
     std::string key, path;
@@ -283,9 +294,10 @@ Compiled compile(const std::string &src, const std::string &name) {
         key = cache_key(src);
         path = cache_path(dir, key);
         std::vector<char> code;
-        if (cache_read(path, key, &code)) {
+        Compiled c;
+        if (cache_read(path, key, &code) && try_load_code(code, name, &c)) {
             ++g_disk_loads;
-            return load_code(code, name);
+            return c;
         }
     }
     hiprtcProgram prog;

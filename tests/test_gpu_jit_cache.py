@@ -3,7 +3,8 @@
 Each case runs fresh processes (the in-memory cache would hide the disk):
 the first compiles the chain with hipRTC and writes its code object, a
 later one loads it and compiles nothing, and both give the same bits.  A
-damaged file is ignored and rewritten; CLOVE_JIT_CACHE=0 writes nothing.
+damaged file (its header, or a code object the runtime refuses) is ignored
+and rewritten; CLOVE_JIT_CACHE=0 writes nothing.
 """
 import os
 import subprocess
@@ -45,6 +46,17 @@ def test_chain_code_object_reused_across_processes(tmp_path):
     assert (compiled, loaded) == (0, 1) and again == first
     # a damaged object is ignored: compiled again, rewritten, then reused
     files[0].write_bytes(b"CLVJIT01 not a code object")
+    compiled, loaded, again = run(env)
+    assert (compiled, loaded) == (1, 0) and again == first
+    compiled, loaded, again = run(env)
+    assert (compiled, loaded) == (0, 1) and again == first
+    # the key matches but the code object is damaged: the runtime refuses
+    # it, so the chain is compiled again and the file rewritten
+    data = bytearray(files[0].read_bytes())
+    klen = int.from_bytes(data[8:16], "little")
+    code_at = 16 + klen + 8
+    data[code_at:] = bytes(len(data) - code_at)
+    files[0].write_bytes(bytes(data))
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (1, 0) and again == first
     compiled, loaded, again = run(env)
