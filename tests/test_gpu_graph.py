@@ -137,14 +137,15 @@ def test_gemm_epilogue_matches_eager_bits(hip, m, k, n, bias_n, act):
     assert np.array_equal(fused.numpy(), eager.numpy())
 
 
-@pytest.mark.parametrize("cfg", ["5", "4"])  # 128x256 and 256x128 tiles
+@pytest.mark.parametrize("cfg", ["5", "4", "2"])  # 128x256, 256x128 and 128x128 tiles
 @pytest.mark.parametrize("m,k,n,bias_n,act", [(1000, 64, 1100, 1100, "gelu"),
                                                (1000, 64, 1101, 7, "relu"),
                                                (700, 60, 900, 1, None)])
 def test_gemm_epilogue_edge_tiles_large_configs(hip, monkeypatch, cfg, m, k, n, bias_n, act):
-    """The fused epilogue on the bounds-checked kernels of the two largest
-    tile shapes (ragged M and N, K short enough for one split): the same
-    bits as the eager composition."""
+    """The fused epilogue on the bounds-checked kernels of the largest tile
+    shapes (ragged M and N, K short enough for one split; with N % 4 == 0
+    the 128-row tiles take the DMA kernel's edge form): the same bits as
+    the eager composition."""
     monkeypatch.setenv("CLOVE_GEMM_CFG", cfg)
     gg = rng(3 * m + n + int(cfg))
     a = gg.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
