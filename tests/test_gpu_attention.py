@@ -102,7 +102,9 @@ def test_flash_attention_prefill_4096_sampled(hip):
 
 @pytest.mark.parametrize("B,S,Sk,H,D,flags,q_pos,k_pos", [(1, 130, 130, 2, 128, 3, 0, 0),
                                                           (2, 65, 200, 3, 64, 2, 135, 0),
-                                                          (1, 300, 300, 1, 128, 3, 7, 7)])
+                                                          (1, 300, 300, 1, 128, 3, 7, 7),
+                                                          (1, 64, 300, 2, 128, 3, 236, 3),
+                                                          (2, 100, 333, 3, 64, 3, 400, 167)])
 def test_attention_rope_equals_rope_then_attention(hip, B, S, Sk, H, D, flags, q_pos, k_pos):
     """The RoPE flag rotates k in a pass and q inside the kernel; both use the
     RoPE op's arithmetic and table, so the result equals rotating q and k with
