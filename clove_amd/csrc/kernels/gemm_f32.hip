@@ -1367,7 +1367,7 @@ void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
 
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned,
                    bool force_skinny, int force_skinny_nb, int force_skinny_splits,
-                   bool force_strip) {
+                   bool force_strip, bool b_aligned) {
     GemmPlan p{};
     p.M = M;
     p.N = N;
@@ -1415,7 +1415,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
             return p;
         }
     }
-    const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned &&
+    const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned && b_aligned &&
                           b_bytes < (1ull << 31) && force_cfg < 0;
     // Strip path (one launch, no workspace): M <= 32, even N, B of 4 MiB or
     // more, enough 16 x 32 tiles for every CU, and K within the longest

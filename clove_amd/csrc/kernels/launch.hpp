@@ -127,8 +127,10 @@ struct GemmEpilogue {
 constexpr int kGemmGroupMax = 8;
 void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float *const *B,
                       float *const *C, const GemmEpilogue *epi, int count, hipStream_t s);
-// Picks the tile configuration and K split for a shape.  a_aligned: A is
-// 16-byte aligned (the skinny path needs it).  force_cfg >= 0 overrides the
+// Picks the tile configuration and K split for a shape.  a_aligned / b_aligned:
+// A / B is 16-byte aligned (the small path needs A aligned, the strip and
+// skinny paths both, as they read them in 8- and 16-byte vectors).
+// force_cfg >= 0 overrides the
 // configuration and turns the skinny path off; force_skinny takes the skinny
 // path wherever it is legal, with force_skinny_nb (1, 2, 4) /
 // force_skinny_splits > 0 overriding its plan; force_strip takes the strip
@@ -136,7 +138,8 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 // and tests).  Every plan computes the same product.
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned = true,
                    bool force_skinny = false, int force_skinny_nb = 0,
-                   int force_skinny_splits = 0, bool force_strip = false);
+                   int force_skinny_splits = 0, bool force_strip = false,
+                   bool b_aligned = true);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
 // C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the

@@ -226,8 +226,9 @@ static k::GemmPlan prepare_matmul(const Tensor &a, const Tensor &b, const Tensor
     int sk_nb, sk_splits;
     const bool sk_force = gemm_skinny_override(&sk_nb, &sk_splits);
     const bool a_aligned = (reinterpret_cast<uintptr_t>(a.data) & 15) == 0;
+    const bool b_aligned = (reinterpret_cast<uintptr_t>(b.data) & 15) == 0;
     return k::gemm_plan((int)m, (int)n, (int)kk, ctx().num_cus, gemm_cfg_override(), a_aligned,
-                        sk_force, sk_nb, sk_splits, gemm_strip_override());
+                        sk_force, sk_nb, sk_splits, gemm_strip_override(), b_aligned);
 }
 
 // A product the grouped small kernel can take: the small path, and for a

@@ -104,7 +104,7 @@ def test_strip_shapes(hip, monkeypatch, m, k, n):
     assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
 
 
-# The skinny path (M <= 64, K % 4 == 0, 16-byte aligned A): 32*nb columns
+# The skinny path (M <= 64, K % 4 == 0, 16-byte aligned A and B): 32*nb columns
 # per workgroup, a K split over the workgroup's waves and across workgroups.
 # The plan picks it for B >= 4 MiB; CLOVE_GEMM_SKINNY forces it on the small
 # edge shapes here.
@@ -276,3 +276,43 @@ def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
     want = oracle.matmul(a, b)
     check(dma, want, f"dma edge cfg {cfg} {m}x{k}x{n}")
     check(dma_fused, oracle.add(want, bias), f"dma edge + bias cfg {cfg} {m}x{k}x{n}")
+
+
+def test_matmul_random_shapes_sweep(hip):
+    """120 seeded random shapes across every plan the GEMM chooses (small,
+    strip, skinny, split-K and single-launch tiles, DMA-staged interior and
+    edge tiles, register-staged tiles for N or K not a multiple of 4 or 16):
+    each product within the matmul bound of the float64 product.  (float64
+    stands in for the oracle here to keep the sweep fast; the oracle's own
+    f32 result lies within the same bound of it, which the shape tests
+    above check.)"""
+    g = np.random.default_rng(2024)
+    for _ in range(120):
+        m = int(g.choice([g.integers(1, 65), g.integers(65, 2500)]))
+        k = int(g.choice([g.integers(1, 64), g.integers(64, 2500), 16 * g.integers(4, 160)]))
+        n = int(g.choice([g.integers(1, 2500), 4 * g.integers(1, 600), 128 * g.integers(1, 20)]))
+        a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+        b = g.normal(0, 1, (k, n)).astype(np.float32)
+        got = hip.matmul(hip.tensor(a), hip.tensor(b)).numpy()
+        check(got, a.astype(np.float64) @ b.astype(np.float64), f"sweep {m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(300, 512, 516), (32, 4096, 4096)])
+@pytest.mark.parametrize("which", ["a", "b"])
+def test_tiled_misaligned_operand_falls_back(hip, which, m, k, n):
+    """An A or B that is not 16-byte aligned takes the register-staged kernel's
+    scalar-load form: the DMA kernel moves 16-byte pieces, and the strip and
+    skinny kernels read A and B in 8- and 16-byte vectors.  At shapes whose
+    aligned operands take the DMA kernel's edge tiles (300 x 512 x 516) or
+    the strip kernel (32 x 4096 x 4096) the product is unchanged within the
+    matmul bound."""
+    g = rng((23 if which == "a" else 24) + m)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    src = a if which == "a" else b
+    buf = hip.tensor(np.concatenate([[0.0], src.ravel()]).astype(np.float32))
+    view = hip.wrap(buf.device_ptr + 4, src.shape)
+    ta = view if which == "a" else hip.tensor(a)
+    tb = view if which == "b" else hip.tensor(b)
+    check(hip.matmul(ta, tb).numpy(), oracle.matmul(a, b), f"misaligned {which}")
+    del view
