@@ -439,13 +439,16 @@ constexpr int dma_stages(int BN) { return BN == 128 ? 2 : kDmaStages; }
 // expcnt left at their maxima, so they are not waited for).
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
-// EDGE: tiles may reach past M or N (K and every split whole slabs).  Rows
-// of A past M and columns of B past N (N % 4 == 0, so a 16-byte piece is all
-// in or all out) get the offset kOutside, past the end of both buffers, so
-// the DMA writes zeros there whether or not the range check counts the slab
-// step in soffset; kOutside plus any step (under K * N * 4 < 2^31) stays
-// below 2^32.  Stores and bias loads are bounds-checked.  The stored results
-// are the same bits as the register-staged kernel's, which also reads zeros.
+// EDGE: tiles may reach past M or N, and K may end inside the last slab of
+// the last split.  Rows of A past M and columns of B past N (N % 4 == 0, so
+// a 16-byte piece is all in or all out) get the offset kOutside, past the
+// end of both buffers, so the DMA writes zeros there whether or not the
+// range check counts the slab step in soffset; kOutside plus any step
+// (under K * N * 4 < 2^31) stays below 2^32.  In a last slab that K ends
+// inside (K % 4 == 0: again whole pieces), A's pieces and B's rows past K
+// get kOutside too, with the slab step moved into the unmasked offsets.
+// Stores and bias loads are bounds-checked.  The stored results are the same
+// bits as the register-staged kernel's, which also reads zeros there.
 //
 // Workgroups of the DMA kernel that fit one CU (one wave each per SIMD): the
 // LDS ring's share of 160 KiB, and 512 registers a lane over the
@@ -477,7 +480,11 @@ __global__ void __launch_bounds__(256)
     const int m0 = (tile / g.tiles_n) * BM;
     const int n0 = (tile % g.tiles_n) * BN;
     const int k_begin = split * g.k_per_split;
-    const int slabs = min(g.k_per_split, K - k_begin) / BK;
+    const int k_len = min(g.k_per_split, K - k_begin);
+    const int slabs = EDGE ? (k_len + BK - 1) / BK : k_len / BK;
+    // EDGE: a last slab that K ends inside (K % 4 == 0) is loaded with the
+    // pieces past K masked to zeros, as the register-staged kernel fills them
+    const int tail_sl = EDGE && k_len % BK ? slabs - 1 : -1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm0 = (wave / WN_) * WM, wn0 = (wave % WN_) * WN;
     const int l32 = lane & 31, h = lane >> 5;
@@ -486,6 +493,7 @@ __global__ void __launch_bounds__(256)
     // this lane's DMA offsets at k = k_begin; each slab's step rides in soffset
     constexpr uint32_t kOutside = 0x80000000u;
     uint32_t aoff[IAW], boff[IBW];
+    int ak[IAW], bk[IBW];  // (EDGE) the k within a slab of this lane's A piece / B row
 #pragma unroll
     for (int u = 0; u < IAW; ++u) {
         const int p = (wave * IAW + u) * 64 + lane;  // 16-byte position in the A stage
@@ -497,6 +505,7 @@ __global__ void __launch_bounds__(256)
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
             aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
             if (EDGE && m0 + row >= M) aoff[u] = kOutside;
+            ak[u] = 4 * kq;
         }
     }
 #pragma unroll
@@ -510,12 +519,33 @@ __global__ void __launch_bounds__(256)
             const int row = 4 * p / BN, col = 4 * p % BN;
             boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
             if (EDGE && n0 + col >= N) boff[u] = kOutside;
+            bk[u] = row;
         }
     }
     const int a_step = TA ? BK * M * 4 : BK * 4;  // bytes per slab
     const int b_step = TB ? BK * 4 : BK * N * 4;
     auto dma = [&](int sl) {
         float *st = smem + (sl % ST) * SS;
+        if (EDGE && sl == tail_sl) {  // the slab step moves into the masked offsets
+            const int k0 = sl * BK;   // within this split
+#pragma unroll
+            for (int u = 0; u < IAW; ++u) {
+                const uint32_t o = aoff[u] != kOutside && k0 + ak[u] < k_len
+                                       ? aoff[u] + (uint32_t)(sl * a_step)
+                                       : kOutside;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(st + (wave * IAW + u) * 256),
+                                                         16, (int)o, 0, 0, 0);
+            }
+#pragma unroll
+            for (int u = 0; u < IBW; ++u) {
+                const uint32_t o = boff[u] != kOutside && k0 + bk[u] < k_len
+                                       ? boff[u] + (uint32_t)(sl * b_step)
+                                       : kOutside;
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                    rb, (lds_void *)(st + SA + (wave * IBW + u) * 256), 16, (int)o, 0, 0, 0);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < IAW; ++u)
             __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(st + (wave * IAW + u) * 256), 16,
@@ -1242,14 +1272,15 @@ bool dma_ok(const GemmPlan &p, int BM, int BN) {
            (uint64_t)p.M * p.K * 4 < (1ull << 31) && (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
 
-// The same for tiles reaching past M or N: 16-byte aligned rows (p.vec after
-// the pointer check) and K and every split a whole number of 16-deep slabs.
+// The same for tiles reaching past M or N, or K ending inside a slab:
+// 16-byte aligned rows (p.vec after the pointer check: K % 4 == N % 4 == 0)
+// and every split but the last a whole number of 16-deep slabs.
 bool dma_edge_ok(const GemmPlan &p, int BM, int BN) {
     const char *v = std::getenv("CLOVE_GEMM_DMA");
     const bool enabled = !(v && *v && std::atoi(v) == 0);
     return enabled && !p.interior && p.vec && BM == 128 && (BN == 256 || BN == 128) &&
-           p.K % 16 == 0 && p.k_per_split % 16 == 0 &&
-           (uint64_t)p.M * p.K * 4 < (1ull << 31) && (uint64_t)p.K * p.N * 4 < (1ull << 31);
+           p.k_per_split % 16 == 0 && (uint64_t)p.M * p.K * 4 < (1ull << 31) &&
+           (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
 
 template <int BM, int BN, int BK, int WM, int WN>

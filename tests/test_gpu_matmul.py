@@ -245,16 +245,20 @@ def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
     assert np.array_equal(fused.numpy(), eager.numpy())
 
 
-# Tiles reaching past M or N run the DMA-staged kernel too when N % 4 == 0
-# and K % 16 == 0 (rows of A past M and columns of B past N read as zeros,
-# stores bounds-checked): the register-staged kernel's bits, single launch
-# and split-K, plain and with the fused column-bias epilogue.  N % 4 != 0 or
-# K % 16 != 0 keeps the register-staged kernel (the last two shapes).
+# Tiles reaching past M or N, or K ending inside the last slab, run the
+# DMA-staged kernel too when N % 4 == K % 4 == 0 (rows of A past M, columns
+# of B past N and pieces past K read as zeros, stores bounds-checked): the
+# register-staged kernel's bits, single launch and split-K (the K tail in
+# the last split), plain and with the fused column-bias epilogue.
+# N % 4 != 0 or K % 4 != 0 keeps the register-staged kernel (the last two).
 @pytest.mark.parametrize("cfg,m,k,n", [(5, 300, 512, 516), (2, 129, 1040, 132),
                                        (2, 200, 8192, 260), (5, 1000, 64, 1100),
                                        (5, 4097, 256, 4096), (2, 130, 4096, 1000),
                                        (5, 257, 4096, 4), (2, 1, 16, 4),
-                                       (2, 300, 512, 514), (5, 300, 520, 516)])
+                                       (5, 300, 520, 516), (2, 300, 1028, 516),
+                                       (2, 2049, 4100, 2048), (2, 200, 8196, 260),
+                                       (5, 129, 100, 132), (2, 64, 4, 128),
+                                       (2, 300, 512, 514), (2, 300, 1030, 516)])
 def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
     monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
     g = rng(cfg * 5 + m + 3 * k + n)
