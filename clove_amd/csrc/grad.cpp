@@ -89,10 +89,11 @@ TensorNode HipBackend::softmax_backward(const TensorNode &y_, const TensorNode &
 
 // backend.rs:1314-1360: grad_a = grad_out . b^T (a's shape, m = prod of a's
 // leading dims), grad_b = a^T . grad_out ([k, n]).  Each product is the MFMA
-// GEMM; where its plan allows (interior tiles of the 128x128 / 128x256
-// configurations) the GEMM reads the transposed operand directly
-// (k::gemm_f32_transposed), else it runs on a transposed copy.  Both give the
-// same bits.  CLOVE_GEMM_TRANSPOSED=0 forces the copies (tests).
+// GEMM; where its plan allows (unsplit 128x128 / 128x256 tilings whose
+// operand rows hold whole 16-byte pieces) the GEMM reads the transposed
+// operand directly (k::gemm_f32_transposed), else it runs on a transposed
+// copy.  Both give the same bits.  CLOVE_GEMM_TRANSPOSED=0 forces the copies
+// (tests).
 static bool transposed_loads_enabled() {
     const char *v = std::getenv("CLOVE_GEMM_TRANSPOSED");
     return !(v && v[0] == '0');

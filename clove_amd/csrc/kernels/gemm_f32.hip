@@ -447,8 +447,11 @@ constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 // (under K * N * 4 < 2^31) stays below 2^32.  In a last slab that K ends
 // inside (K % 4 == 0: again whole pieces), A's pieces and B's rows past K
 // get kOutside too, with the slab step moved into the unmasked offsets.
-// Stores and bias loads are bounds-checked.  The stored results are the same
-// bits as the register-staged kernel's, which also reads zeros there.
+// A transposed operand takes the same masks: TA's pieces of four m past M
+// (M % 4 == 0) and its rows past K, TB's rows past N and its pieces of four
+// k past K (K % 4 == 0).  Stores and bias loads are bounds-checked.  The
+// stored results are the same bits as the register-staged kernel's (and, for
+// TA and TB, as transposing first), which also reads zeros there.
 //
 // Workgroups of the DMA kernel that fit one CU (one wave each per SIMD): the
 // LDS ring's share of 160 KiB, and 512 registers a lane over the
@@ -464,7 +467,6 @@ template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, boo
 __global__ void __launch_bounds__(256)
     __attribute__((amdgpu_waves_per_eu(dma_waves(BM, BN, BK, WM, WN, ST))))
     gemm_f32_dma_kernel(GemmArgs g) {
-    static_assert(!EDGE || !(TA || TB), "transposed operands are interior-only");
     constexpr int SA = BM * BK, SB = BK * BN, SS = SA + SB;
     constexpr int IAW = SA / 256 / 4, IBW = SB / 256 / 4;  // 1 KiB DMAs per wave per slab
     constexpr int KQ = BK / 4;                              // 16-byte slots per A row
@@ -493,13 +495,15 @@ __global__ void __launch_bounds__(256)
     // this lane's DMA offsets at k = k_begin; each slab's step rides in soffset
     constexpr uint32_t kOutside = 0x80000000u;
     uint32_t aoff[IAW], boff[IBW];
-    int ak[IAW], bk[IBW];  // (EDGE) the k within a slab of this lane's A piece / B row
+    int ak[IAW], bk[IBW];  // (EDGE) the k within a slab of this lane's A and B pieces
 #pragma unroll
     for (int u = 0; u < IAW; ++u) {
         const int p = (wave * IAW + u) * 64 + lane;  // 16-byte position in the A stage
-        if constexpr (TA) {  // k-major: row k, four m
+        if constexpr (TA) {  // k-major: row k, four m (M % 4 == 0 for EDGE)
             const int row = 4 * p / BM, col = 4 * p % BM;
             aoff[u] = ((uint32_t)(k_begin + row) * (uint32_t)M + (uint32_t)(m0 + col)) * 4u;
+            if (EDGE && m0 + col >= M) aoff[u] = kOutside;
+            ak[u] = row;
         } else {
             const int row = p / KQ, slot = p % KQ;
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
@@ -515,6 +519,8 @@ __global__ void __launch_bounds__(256)
             const int row = p / KQ, slot = p % KQ;
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
             boff[u] = ((uint32_t)(n0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+            if (EDGE && n0 + row >= N) boff[u] = kOutside;
+            bk[u] = 4 * kq;
         } else {
             const int row = 4 * p / BN, col = 4 * p % BN;
             boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
@@ -1571,12 +1577,39 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
                          bool tb, hipStream_t s) {
     if (ta == tb) return false;  // exactly one operand read transposed (the matmul backward)
-    if (p.small || p.skinny || p.strip || p.splits != 1 || !p.interior || p.K <= 0) return false;
+    if (p.small || p.skinny || p.strip || p.splits != 1 || p.K <= 0) return false;
     if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) return false;
     if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128) return false;
     const GemmArgs g{A, B, C, nullptr, p.M, p.N, p.K, p.tiles_n, p.k_per_split, 1, GemmEpilogue{},
                      p.tiles, (p.tiles + 7) / 8};
     const dim3 grid((unsigned)(g.per_xcd * 8), 1u);
+    if (!p.interior) {
+        // ragged tiles or a K tail: the DMA kernel's edge form, whose 16-byte
+        // pieces need whole quads along each stored row (A^T's M and B's N
+        // for ta, K for tb); anything else transposes first
+        const char *v = std::getenv("CLOVE_GEMM_DMA");
+        const bool rows4 = ta ? (p.M % 4 == 0 && p.N % 4 == 0) : p.K % 4 == 0;
+        if ((v && *v && std::atoi(v) == 0) || !rows4 ||
+            (uint64_t)p.M * p.K * 4 >= (1ull << 31) || (uint64_t)p.K * p.N * 4 >= (1ull << 31))
+            return false;
+        constexpr int ST = dma_stages(128);
+        if (p.cfg == CFG_128x256) {
+            if (ta)
+                gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, true, false, kDmaStages, true>
+                    <<<grid, 256, 0, s>>>(g);
+            else
+                gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, false, true, kDmaStages, true>
+                    <<<grid, 256, 0, s>>>(g);
+        } else {
+            if (ta)
+                gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, true, false, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
+            else
+                gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
+        }
+        return true;
+    }
     if (p.cfg == CFG_128x256 && dma_ok(p, 128, 256)) {
         if (ta)
             gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, true, false><<<grid, 256, 0, s>>>(g);

@@ -139,13 +139,16 @@ def test_matmul_backward_4096(hip):
 
 @pytest.mark.parametrize("m,k,n", [(4096, 4096, 4096), (4096, 1024, 2048), (2048, 4096, 4096),
                                    (2048, 2048, 2048), (2048, 2048, 1024),
-                                   (3, 5, 7), (1000, 300, 500)])
+                                   (3, 5, 7), (1000, 300, 500),
+                                   # ragged tiles and K tails (edge form of the DMA kernel)
+                                   (4100, 4096, 4100), (4100, 2052, 2052), (2052, 4100, 4104)])
 def test_matmul_backward_transposed_loads_match_copies(hip, monkeypatch, m, k, n):
     """Where the plan allows, the backward's GEMMs read b^T / a^T straight
-    from b / a, by buffer->LDS DMA (the default) or through registers
-    (CLOVE_GEMM_DMA=0); the result must be the same bits as transposing
-    first (CLOVE_GEMM_TRANSPOSED=0), and shapes the direct path does not
-    take must give the same bits either way too."""
+    from b / a, by buffer->LDS DMA (the default; ragged tiles and K tails
+    included) or through registers (CLOVE_GEMM_DMA=0, interior tiles); the
+    result must be the same bits as transposing first
+    (CLOVE_GEMM_TRANSPOSED=0), and shapes the direct path does not take must
+    give the same bits either way too."""
     g = rng(m + 3 * k + 7 * n)
     a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
     b = g.normal(0, 1 / np.sqrt(k), (k, n)).astype(np.float32)
