@@ -89,8 +89,8 @@ TensorNode HipBackend::softmax_backward(const TensorNode &y_, const TensorNode &
 
 // backend.rs:1314-1360: grad_a = grad_out . b^T (a's shape, m = prod of a's
 // leading dims), grad_b = a^T . grad_out ([k, n]).  Each product is the MFMA
-// GEMM; where its plan allows (unsplit 128x128 / 128x256 tilings whose
-// operand rows hold whole 16-byte pieces) the GEMM reads the transposed
+// GEMM; where its plan allows (128x128 / 128x256 tilings, split over K or
+// not, whose operand rows hold whole 16-byte pieces) the GEMM reads the transposed
 // operand directly (k::gemm_f32_transposed), else it runs on a transposed
 // copy.  Both give the same bits.  CLOVE_GEMM_TRANSPOSED=0 forces the copies
 // (tests).
@@ -127,7 +127,10 @@ void HipBackend::matmul_backward(const TensorNode &a_, const TensorNode &b_, con
         Tensor dav;
         view2d(*da, m, kk, &dav);
         const k::GemmPlan p = k::gemm_plan((int)m, (int)kk, (int)n, cus, -1);
-        if (!(direct && k::gemm_f32_transposed(p, g.f32(), b.f32(), da->f32(), false, true, s))) {
+        TensorNode ws;
+        if (direct && p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
+        if (!(direct && k::gemm_f32_transposed(p, g.f32(), b.f32(), da->f32(),
+                                               ws ? ws->f32() : nullptr, false, true, s))) {
             TensorNode bt = new_tensor({n, kk}, CLOVE_HIP_F32);
             k::transpose(b.f32(), bt->f32(), kk, n, s);
             matmul_into(gv, *bt, dav);
@@ -137,7 +140,10 @@ void HipBackend::matmul_backward(const TensorNode &a_, const TensorNode &b_, con
     if (grad_b) {  // ([m, kk])^T . [m, n]
         TensorNode db = new_tensor({kk, n}, CLOVE_HIP_F32);
         const k::GemmPlan p = k::gemm_plan((int)kk, (int)n, (int)m, cus, -1);
-        if (!(direct && k::gemm_f32_transposed(p, a.f32(), g.f32(), db->f32(), true, false, s))) {
+        TensorNode ws;
+        if (direct && p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
+        if (!(direct && k::gemm_f32_transposed(p, a.f32(), g.f32(), db->f32(),
+                                               ws ? ws->f32() : nullptr, true, false, s))) {
             TensorNode at = new_tensor({kk, m}, CLOVE_HIP_F32);
             k::transpose(a.f32(), at->f32(), m, kk, s);
             matmul_into(*at, gv, *db);

@@ -455,7 +455,11 @@ constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 //
 // Workgroups of the DMA kernel that fit one CU (one wave each per SIMD): the
 // LDS ring's share of 160 KiB, and 512 registers a lane over the
-// accumulators plus 40 more.
+// accumulators plus 40 more (four at 128 x 128).  Asking for five there
+// (accumulators plus 32) made the fused-epilogue variants spill (their
+// accumulators sit in AGPRs and a tighter budget is split between the two
+// files) and the edge kernel slower: 5000 x 4096 x 4096 1.361 against 1.230
+// ms, five co-resident workgroups against four and then one.
 constexpr int dma_waves(int BM, int BN, int BK, int WM, int WN, int ST) {
     const int lds = (160 * 1024) / (ST * (BM * BK + BK * BN) * 4);
     const int regs = 512 / (((WM / 32) * (WN / 32) * 16 + 40 + 7) / 8 * 8);
@@ -1574,15 +1578,26 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
     }
 }
 
-bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
-                         bool tb, hipStream_t s) {
+bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
+                         bool ta, bool tb, hipStream_t s) {
     if (ta == tb) return false;  // exactly one operand read transposed (the matmul backward)
-    if (p.small || p.skinny || p.strip || p.splits != 1 || p.K <= 0) return false;
+    if (p.small || p.skinny || p.strip || p.K <= 0 || (p.splits > 1 && !ws)) return false;
     if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) return false;
     if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128) return false;
-    const GemmArgs g{A, B, C, nullptr, p.M, p.N, p.K, p.tiles_n, p.k_per_split, 1, GemmEpilogue{},
-                     p.tiles, (p.tiles + 7) / 8};
-    const dim3 grid((unsigned)(g.per_xcd * 8), 1u);
+    const GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits,
+                     GemmEpilogue{}, p.tiles, (p.tiles + 7) / 8};
+    const dim3 grid((unsigned)(g.per_xcd * 8), (unsigned)p.splits);
+    // split K: each split parks its tile in ws, then the splits are summed in
+    // order (gemm_f32's reduce)
+    auto reduce = [&] {
+        if (p.splits <= 1) return;
+        const int BM = kCfgBM[p.cfg], BN = kCfgBN[p.cfg];
+        const int64_t work = (int64_t)p.tiles * BM * (BN / 4);
+        int64_t blocks = (work + 63) / 64;
+        if (blocks > 32768) blocks = 32768;
+        gemm_splitk_reduce<<<(unsigned)blocks, 64, 0, s>>>(ws, C, p.M, p.N, BM, BN, p.tiles_n,
+                                                           p.tiles, p.splits, GemmEpilogue{});
+    };
     if (!p.interior) {
         // ragged tiles or a K tail: the DMA kernel's edge form, whose 16-byte
         // pieces need whole quads along each stored row (A^T's M and B's N
@@ -1608,6 +1623,7 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
                 gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true, ST, true>
                     <<<grid, 256, 0, s>>>(g);
         }
+        reduce();
         return true;
     }
     if (p.cfg == CFG_128x256 && dma_ok(p, 128, 256)) {
@@ -1636,6 +1652,7 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
             gemm_f32_mfma_kernel<128, 128, 16, 64, 64, false, true, false, false, true>
                 <<<grid, 256, 0, s>>>(g);
     }
+    reduce();
     return true;
 }
 

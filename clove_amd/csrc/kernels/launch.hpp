@@ -144,12 +144,13 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
               const GemmEpilogue &epi, hipStream_t s);
 // C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the
 // [N, K] matrix), read transposed inside the tiled kernel's slab loads: the
-// same bits as transposing first.  Launches nothing and returns false unless
-// exactly one of ta, tb is set and p is an interior, unsplit 128x128 or
-// 128x256 tiled plan with 16-byte aligned operands; the caller then
-// transposes explicitly.
-bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, bool ta,
-                         bool tb, hipStream_t s);
+// same bits as transposing first.  ws: p.ws_floats floats when p splits K.
+// Launches nothing and returns false unless exactly one of ta, tb is set and
+// p is a 128x128 or 128x256 tiled plan with 16-byte aligned operands whose
+// transposed rows hold whole 16-byte pieces where its tiles are ragged; the
+// caller then transposes explicitly.
+bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
+                         bool ta, bool tb, hipStream_t s);
 
 // Bits of the device error word (runtime.cpp) that the next synchronising
 // call reports: kernels OR them in when they meet a bad index.
