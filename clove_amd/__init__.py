@@ -95,6 +95,8 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_sub": (vp, [vp, vp]),
         "clove_hip_mul": (vp, [vp, vp]),
         "clove_hip_mul_scalar": (vp, [vp, f]),
+        "clove_hip_transpose": (vp, [vp]),
+        "clove_hip_flatten": (vp, [vp]),
         "clove_hip_relu": (vp, [vp]),
         "clove_hip_gelu": (vp, [vp]),
         "clove_hip_sigmoid": (vp, [vp]),
@@ -342,6 +344,16 @@ def mul(a: Tensor, b: Tensor) -> Tensor:
 
 def mul_scalar(a: Tensor, s: float) -> Tensor:
     return _handle(lib().clove_hip_mul_scalar(a.handle, s))
+
+
+def transpose(a: Tensor) -> Tensor:
+    """2-d [rows, cols] -> [cols, rows] (backend.rs:2266)."""
+    return _handle(lib().clove_hip_transpose(a.handle))
+
+
+def flatten(a: Tensor) -> Tensor:
+    """A copy with shape [1, numel] (backend.rs:2337)."""
+    return _handle(lib().clove_hip_flatten(a.handle))
 
 
 def relu(a: Tensor) -> Tensor:

@@ -267,6 +267,20 @@ CTensor clove_hip_mul_scalar(CTensor a, float s) {
     });
 }
 
+CTensor clove_hip_transpose(CTensor a) {
+    return guarded_tensor([&] {
+        deref(a, "a");
+        return HipBackend::transpose(as_node(a));
+    });
+}
+
+CTensor clove_hip_flatten(CTensor a) {
+    return guarded_tensor([&] {
+        deref(a, "a");
+        return HipBackend::flatten(as_node(a));
+    });
+}
+
 CTensor clove_hip_layer_norm(CTensor a, CTensor gamma, CTensor beta) {
     return guarded_tensor([&] {
         deref(a, "a");

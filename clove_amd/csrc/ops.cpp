@@ -107,6 +107,28 @@ TensorNode HipBackend::unary(int opcode, const TensorNode &a_, float param) {
     return out;
 }
 
+// backend.rs:2266-2336: the 2-d transpose [rows, cols] -> [cols, rows] (the
+// LDS-tiled transpose the matmul backward uses; a pure permutation, so the
+// same bits as the reference's loop).
+TensorNode HipBackend::transpose(const TensorNode &a_) {
+    const Tensor &a = need(a_, "a");
+    need_f32(a, "a");
+    CLOVE_REQUIRE(a.shape.size() == 2, CLOVE_HIP_ERR_SHAPE,
+                  "transpose: a must be 2-d, got " + shape_str(a.shape));
+    const size_t rows = a.shape[0], cols = a.shape[1];
+    TensorNode out = new_tensor({cols, rows}, CLOVE_HIP_F32);
+    if (a.numel) k::transpose(a.f32(), out->f32(), rows, cols, ctx().stream);
+    return out;
+}
+
+// backend.rs:2337-2370: a copy of a with shape [1, numel] (the fused chain's
+// Flatten copy, 16-byte streaming loads and stores).
+TensorNode HipBackend::flatten(const TensorNode &a_) {
+    TensorNode out = unary(CLOVE_OP_FLATTEN, a_);
+    out->shape = {1, out->numel};
+    return out;
+}
+
 TensorNode HipBackend::add(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_ADD, a, b); }
 TensorNode HipBackend::sub(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_SUB, a, b); }
 TensorNode HipBackend::mul(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_MUL, a, b); }

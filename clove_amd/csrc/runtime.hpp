@@ -74,6 +74,8 @@ struct HipBackend {
     static TensorNode sub(const TensorNode &a, const TensorNode &b);
     static TensorNode mul(const TensorNode &a, const TensorNode &b);
     static TensorNode mul_scalar(const TensorNode &a, float s);
+    static TensorNode transpose(const TensorNode &a);
+    static TensorNode flatten(const TensorNode &a);
     static TensorNode relu(const TensorNode &a);
     static TensorNode gelu(const TensorNode &a);
     static TensorNode sigmoid(const TensorNode &a);

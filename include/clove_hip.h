@@ -142,6 +142,11 @@ CTensor clove_hip_add(CTensor a, CTensor b);          /* ffi.rs:119-122, backend
 CTensor clove_hip_sub(CTensor a, CTensor b);          /* ffi.rs:124-127, backend.rs:1748 */
 CTensor clove_hip_mul(CTensor a, CTensor b);          /* ffi.rs:129-132, backend.rs:1598 */
 CTensor clove_hip_mul_scalar(CTensor a, float s);     /* ffi.rs:139-142, backend.rs:1686 */
+/* 2-d a [rows, cols] -> [cols, rows]; other ranks are CLOVE_HIP_ERR_SHAPE
+ * (the reference reads shape[0] and shape[1] only). */
+CTensor clove_hip_transpose(CTensor a);                 /* ffi.rs:144-147, backend.rs:2266 */
+/* A copy of a with shape [1, numel(a)]. */
+CTensor clove_hip_flatten(CTensor a);                   /* ffi.rs:149-152, backend.rs:2337 */
 CTensor clove_hip_relu(CTensor a);                    /* ffi.rs:163-166, backend.rs:1815 */
 CTensor clove_hip_gelu(CTensor a);                    /* ffi.rs:168-171, backend.rs:1917 */
 CTensor clove_hip_sigmoid(CTensor a);                 /* ffi.rs:173-176, backend.rs:2951 */

@@ -135,3 +135,28 @@ def test_chain_rejects_bad_operands(hip):
         hip.fused_chain([("add", -1, 3)], [x])     # forward reference
     with pytest.raises(hip.CloveError):
         hip.fused_chain([("softmax", -1)], [x])    # not elementwise
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (3, 5), (64, 64), (65, 129), (4096, 17), (1, 4099),
+                                   (1000, 1000), (0, 5), (7, 0)])
+def test_transpose(hip, shape):
+    """backend.rs:2266-2336: [rows, cols] -> [cols, rows], a pure permutation
+    (bit-exact)."""
+    x = rng(shape[0] * 3 + shape[1]).standard_normal(shape).astype(np.float32)
+    t = hip.transpose(hip.tensor(x))
+    assert t.shape == (shape[1], shape[0])
+    assert np.array_equal(t.numpy(), x.T)
+
+
+def test_transpose_needs_2d(hip):
+    with pytest.raises(hip.CloveError):
+        hip.transpose(hip.tensor(np.ones((2, 3, 4), np.float32)))
+
+
+@pytest.mark.parametrize("shape", [(2, 3, 4), (5,), (1, 1), (4096, 1025), (0, 3)])
+def test_flatten(hip, shape):
+    """backend.rs:2337-2370: a copy of the data with shape [1, numel]."""
+    x = rng(sum(shape) + 11).standard_normal(shape).astype(np.float32)
+    t = hip.flatten(hip.tensor(x))
+    assert t.shape == (1, x.size)
+    assert np.array_equal(t.numpy(), x.reshape(1, -1))
