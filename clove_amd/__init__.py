@@ -97,6 +97,7 @@ def _declare(lib: C.CDLL) -> None:
         "clove_hip_mul_scalar": (vp, [vp, f]),
         "clove_hip_transpose": (vp, [vp]),
         "clove_hip_flatten": (vp, [vp]),
+        "clove_hip_concat": (vp, [vp, vp]),
         "clove_hip_relu": (vp, [vp]),
         "clove_hip_gelu": (vp, [vp]),
         "clove_hip_sigmoid": (vp, [vp]),
@@ -354,6 +355,11 @@ def transpose(a: Tensor) -> Tensor:
 def flatten(a: Tensor) -> Tensor:
     """A copy with shape [1, numel] (backend.rs:2337)."""
     return _handle(lib().clove_hip_flatten(a.handle))
+
+
+def concat_seq(a: Tensor, b: Tensor) -> Tensor:
+    """Per batch, a's rows then b's (backend.rs:1437)."""
+    return _handle(lib().clove_hip_concat(a.handle, b.handle))
 
 
 def relu(a: Tensor) -> Tensor:

@@ -281,6 +281,14 @@ CTensor clove_hip_flatten(CTensor a) {
     });
 }
 
+CTensor clove_hip_concat(CTensor a, CTensor b) {
+    return guarded_tensor([&] {
+        deref(a, "a");
+        deref(b, "b");
+        return HipBackend::concat_seq(as_node(a), as_node(b));
+    });
+}
+
 CTensor clove_hip_layer_norm(CTensor a, CTensor gamma, CTensor beta) {
     return guarded_tensor([&] {
         deref(a, "a");

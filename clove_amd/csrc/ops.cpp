@@ -129,6 +129,43 @@ TensorNode HipBackend::flatten(const TensorNode &a_) {
     return out;
 }
 
+// backend.rs:1437-1482: per batch, a's s1 rows and then b's s2 rows of h
+// floats; a 2-d operand is one batch, and the result has a's rank ([B, s1 +
+// s2, h] or [s1 + s2, h]).  The reference builds it on the host; here two
+// strided device copies.
+TensorNode HipBackend::concat_seq(const TensorNode &a_, const TensorNode &b_) {
+    const Tensor &a = need(a_, "a");
+    const Tensor &b = need(b_, "b");
+    need_f32(a, "a");
+    need_f32(b, "b");
+    auto bsh = [](const Tensor &t, size_t *B, size_t *S, size_t *H) {
+        const size_t r = t.shape.size();
+        CLOVE_REQUIRE(r == 2 || r == 3, CLOVE_HIP_ERR_SHAPE,
+                      "concat_seq: operands must be 2-d or 3-d, got " + shape_str(t.shape));
+        *B = r == 3 ? t.shape[0] : 1;
+        *S = t.shape[r - 2];
+        *H = t.shape[r - 1];
+    };
+    size_t B, s1, h, Bb, s2, hb;
+    bsh(a, &B, &s1, &h);
+    bsh(b, &Bb, &s2, &hb);
+    CLOVE_REQUIRE(Bb == B && hb == h, CLOVE_HIP_ERR_SHAPE,
+                  "concat_seq: batch and hidden sizes differ, a " + shape_str(a.shape) + " b " +
+                      shape_str(b.shape));
+    TensorNode out = new_tensor(a.shape.size() == 3 ? std::vector<size_t>{B, s1 + s2, h}
+                                                    : std::vector<size_t>{s1 + s2, h},
+                                CLOVE_HIP_F32);
+    hipStream_t s = ctx().stream;
+    const size_t pitch = (s1 + s2) * h * 4, wa = s1 * h * 4, wb = s2 * h * 4;
+    if (B && wa)
+        CLOVE_HIP_CHECK(hipMemcpy2DAsync(out->data, pitch, a.data, wa, wa, B,
+                                         hipMemcpyDeviceToDevice, s));
+    if (B && wb)
+        CLOVE_HIP_CHECK(hipMemcpy2DAsync(static_cast<char *>(out->data) + wa, pitch, b.data, wb,
+                                         wb, B, hipMemcpyDeviceToDevice, s));
+    return out;
+}
+
 TensorNode HipBackend::add(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_ADD, a, b); }
 TensorNode HipBackend::sub(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_SUB, a, b); }
 TensorNode HipBackend::mul(const TensorNode &a, const TensorNode &b) { return binary(CLOVE_OP_MUL, a, b); }

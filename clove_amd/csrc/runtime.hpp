@@ -76,6 +76,7 @@ struct HipBackend {
     static TensorNode mul_scalar(const TensorNode &a, float s);
     static TensorNode transpose(const TensorNode &a);
     static TensorNode flatten(const TensorNode &a);
+    static TensorNode concat_seq(const TensorNode &a, const TensorNode &b);
     static TensorNode relu(const TensorNode &a);
     static TensorNode gelu(const TensorNode &a);
     static TensorNode sigmoid(const TensorNode &a);

@@ -147,6 +147,10 @@ CTensor clove_hip_mul_scalar(CTensor a, float s);     /* ffi.rs:139-142, backend
 CTensor clove_hip_transpose(CTensor a);                 /* ffi.rs:144-147, backend.rs:2266 */
 /* A copy of a with shape [1, numel(a)]. */
 CTensor clove_hip_flatten(CTensor a);                   /* ffi.rs:149-152, backend.rs:2337 */
+/* Per batch, a's rows then b's: [B, s1, h] + [B, s2, h] -> [B, s1 + s2, h]
+ * (a 2-d operand is one batch; the result has a's rank).  Different batch or
+ * hidden sizes are CLOVE_HIP_ERR_SHAPE. */
+CTensor clove_hip_concat(CTensor a, CTensor b);         /* ffi.rs:154-157, backend.rs:1437 */
 CTensor clove_hip_relu(CTensor a);                    /* ffi.rs:163-166, backend.rs:1815 */
 CTensor clove_hip_gelu(CTensor a);                    /* ffi.rs:168-171, backend.rs:1917 */
 CTensor clove_hip_sigmoid(CTensor a);                 /* ffi.rs:173-176, backend.rs:2951 */

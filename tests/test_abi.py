@@ -5,6 +5,7 @@ import ctypes as C
 import os
 import re
 import subprocess
+import sys
 
 import numpy as np
 import pytest
@@ -55,13 +56,20 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_calls_before_init_fail_with_status():
-    lib = ca.lib()
-    shape = (C.c_size_t * 2)(2, 3)
-    p = lib.clove_hip_tensor_empty(shape, 2, ca.F32)
-    assert not p
-    assert lib.clove_hip_last_status() == ca.ERR_NOT_INIT
-    assert "clove_hip_init" in ca.last_error()
-    assert lib.clove_hip_synchronize() == ca.ERR_NOT_INIT
+    """In a fresh process (in this one a GPU test may already have called
+    clove_hip_init): calls before init fail with ERR_NOT_INIT."""
+    code = (
+        "import sys, ctypes as C; sys.path.insert(0, %r)\n"
+        "import clove_amd as ca\n"
+        "lib = ca.lib()\n"
+        "shape = (C.c_size_t * 2)(2, 3)\n"
+        "assert not lib.clove_hip_tensor_empty(shape, 2, ca.F32)\n"
+        "assert lib.clove_hip_last_status() == ca.ERR_NOT_INIT\n"
+        "assert 'clove_hip_init' in ca.last_error()\n"
+        "assert lib.clove_hip_synchronize() == ca.ERR_NOT_INIT\n"
+        "print('ok')\n" % ROOT)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0 and r.stdout.strip() == "ok", (r.stdout, r.stderr[-2000:])
 
 
 def test_null_handles_are_errors_not_crashes():

@@ -160,3 +160,31 @@ def test_flatten(hip, shape):
     t = hip.flatten(hip.tensor(x))
     assert t.shape == (1, x.size)
     assert np.array_equal(t.numpy(), x.reshape(1, -1))
+
+
+@pytest.mark.parametrize("sa,sb", [((3, 8), (5, 8)), ((2, 7, 16), (2, 9, 16)), ((4, 33), (1, 4, 33)),
+                                   ((0, 4), (3, 4)), ((2, 5, 3), (2, 0, 3)), ((64, 4096), (1, 4096))])
+def test_concat_seq(hip, sa, sb):
+    """backend.rs:1437-1482: per batch, a's rows then b's (bit-exact); a 2-d
+    operand is one batch and the result has a's rank."""
+    g = rng(len(sa) * 7 + sa[-1])
+    a = g.standard_normal(sa).astype(np.float32)
+    b = g.standard_normal(sb).astype(np.float32)
+    got = hip.concat_seq(hip.tensor(a), hip.tensor(b))
+    a3 = a if a.ndim == 3 else a[None]
+    b3 = b if b.ndim == 3 else b[None]
+    want = np.concatenate([a3, b3], axis=1)
+    if a.ndim == 2:
+        want = want[0]
+    assert got.shape == want.shape
+    assert np.array_equal(got.numpy(), want)
+
+
+def test_concat_seq_shape_errors(hip):
+    t = hip.tensor
+    with pytest.raises(hip.CloveError):  # hidden sizes differ
+        hip.concat_seq(t(np.ones((2, 4), np.float32)), t(np.ones((2, 5), np.float32)))
+    with pytest.raises(hip.CloveError):  # batch sizes differ
+        hip.concat_seq(t(np.ones((2, 3, 4), np.float32)), t(np.ones((3, 3, 4), np.float32)))
+    with pytest.raises(hip.CloveError):  # rank 1
+        hip.concat_seq(t(np.ones(4, np.float32)), t(np.ones(4, np.float32)))
