@@ -1267,18 +1267,18 @@ __global__ void __launch_bounds__(256) gemm_k0_kernel(float *__restrict__ C, int
 
 // Tile configurations: (BM, BN, BK, WM, WN).
 enum { CFG_32x128 = 0, CFG_64x64 = 1, CFG_128x128 = 2, CFG_128x128_K32 = 3, CFG_256x128 = 4,
-       CFG_128x256 = 5, CFG_COUNT = 6 };
-const int kCfgBM[CFG_COUNT] = {32, 64, 128, 128, 256, 128};
-const int kCfgBN[CFG_COUNT] = {128, 64, 128, 128, 128, 256};
-const int kCfgBK[CFG_COUNT] = {32, 16, 16, 32, 16, 16};
+       CFG_128x256 = 5, CFG_64x128 = 6, CFG_COUNT = 7 };
+const int kCfgBM[CFG_COUNT] = {32, 64, 128, 128, 256, 128, 64};
+const int kCfgBN[CFG_COUNT] = {128, 64, 128, 128, 128, 256, 128};
+const int kCfgBK[CFG_COUNT] = {32, 16, 16, 32, 16, 16, 16};
 
-// Whether the DMA-staged kernel takes a plan: interior tiles of the 128 x 256
-// and 128 x 128 configurations with A and B under 2 GiB (32-bit buffer
-// offsets).  CLOVE_GEMM_DMA=0 keeps the register-staged kernel (tests).
+// Whether the DMA-staged kernel takes a plan: interior tiles of the 128 x 256,
+// 128 x 128 and 64 x 128 configurations with A and B under 2 GiB (32-bit
+// buffer offsets).  CLOVE_GEMM_DMA=0 keeps the register-staged kernel (tests).
 bool dma_ok(const GemmPlan &p, int BM, int BN) {
     const char *v = std::getenv("CLOVE_GEMM_DMA");
     const bool enabled = !(v && *v && std::atoi(v) == 0);
-    return enabled && p.interior && BM == 128 && (BN == 256 || BN == 128) &&
+    return enabled && p.interior && ((BM == 128 && (BN == 256 || BN == 128)) || (BM == 64 && BN == 128)) &&
            (uint64_t)p.M * p.K * 4 < (1ull << 31) && (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
 
@@ -1288,7 +1288,7 @@ bool dma_ok(const GemmPlan &p, int BM, int BN) {
 bool dma_edge_ok(const GemmPlan &p, int BM, int BN) {
     const char *v = std::getenv("CLOVE_GEMM_DMA");
     const bool enabled = !(v && *v && std::atoi(v) == 0);
-    return enabled && !p.interior && p.vec && BM == 128 && (BN == 256 || BN == 128) &&
+    return enabled && !p.interior && p.vec && ((BM == 128 && (BN == 256 || BN == 128)) || (BM == 64 && BN == 128)) &&
            p.k_per_split % 16 == 0 && (uint64_t)p.M * p.K * 4 < (1ull << 31) &&
            (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
@@ -1300,7 +1300,7 @@ void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     // one (and split-K kernels, whose reduce applies it) are built without it.
     const bool epi = p.splits == 1 &&
                      (g.epi.bias_mode != GEMM_BIAS_NONE || g.epi.act != GEMM_ACT_NONE);
-    if constexpr (BM == 128 && (BN == 256 || BN == 128) && BK == 16) {
+    if constexpr (((BM == 128 && (BN == 256 || BN == 128)) || (BM == 64 && BN == 128)) && BK == 16) {
         constexpr int ST = dma_stages(BN);
         if (dma_ok(p, BM, BN)) {
             if (epi)
@@ -1479,7 +1479,15 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
             return p;
         }
     }
-    if (eligible && (force_skinny || b_bytes >= (4ull << 20))) {
+    // 33-64 rows over a long K (and N >= 2048, whole 16-byte pieces): 64x128
+    // DMA-staged tiles split over K run ahead of the skinny kernel, whose
+    // per-wave chains grow with K: 64x14336x4096 80.2 against 103.3 us,
+    // 64x8192x8192 89.8 against 110.5, 48x11008x4096 63.0 against 73.5; at
+    // K = 4096 the skinny kernel stays ahead (64x4096x4096 28.5 against
+    // 30.4 us), as it does for N = 1024.
+    const bool long_k64 = eligible && !force_skinny && M > 32 && K > 4096 && N >= 2048 &&
+                          N % 4 == 0;
+    if (eligible && !long_k64 && (force_skinny || b_bytes >= (4ull << 20))) {
         p.skinny = true;
         p.mb = M <= 32 ? 1 : 2;
         int nb = p.mb == 1 ? 4 : 2;
@@ -1522,7 +1530,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // tiles: two rounds), 7168 x 4096 x 4096 1.700 against 1.944, 4096^3
     // 0.974 against 0.975 (one round of each).  128x256 stays selectable
     // (CLOVE_GEMM_CFG=5).
-    int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? CFG_64x64 : CFG_128x128);
+    int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? (long_k64 ? CFG_64x128 : CFG_64x64) : CFG_128x128);
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
     p.cfg = cfg;
     const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
@@ -1699,6 +1707,7 @@ void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float
     case CFG_128x128: launch_cfg<128, 128, 16, 64, 64>(q, g, s); break;
     case CFG_128x128_K32: launch_cfg<128, 128, 32, 64, 64>(q, g, s); break;
     case CFG_256x128: launch_cfg<256, 128, 16, 128, 64>(q, g, s); break;
+    case CFG_64x128: launch_cfg<64, 128, 16, 32, 64>(q, g, s); break;
     default: launch_cfg<128, 256, 16, 64, 128>(q, g, s); break;
     }
     if (p.splits > 1) {

@@ -206,14 +206,16 @@ def test_matmul_empty_dimensions(hip, m, k, n):
     assert got.shape == (m, n) and np.all(got == 0)
 
 
-# Interior tiles of the 128 x 256 and 128 x 128 configurations run the
+# Interior tiles of the 128 x 256, 128 x 128 and 64 x 128 configurations run the
 # DMA-staged kernel (slabs moved by buffer->LDS loads); CLOVE_GEMM_DMA=0 runs
 # the register-staged kernel.  Same tiles, waves and MFMA order: the same
 # bits, single launch and split-K, and both within the matmul bound of the
-# oracle.  CLOVE_GEMM_CFG picks the configuration (2: 128 x 128, 5: 128 x 256).
+# oracle.  CLOVE_GEMM_CFG picks the configuration (2: 128 x 128, 5: 128 x 256,
+# 6: 64 x 128).
 @pytest.mark.parametrize("cfg,m,k,n", [(5, 256, 512, 512), (5, 128, 4096, 256),
                                        (2, 384, 1040, 256), (2, 128, 16, 128),
-                                       (2, 256, 8192, 256), (5, 512, 2048, 768)])
+                                       (2, 256, 8192, 256), (5, 512, 2048, 768),
+                                       (6, 64, 8192, 4096), (6, 128, 2048, 256)])
 def test_dma_kernel_matches_register_staged(hip, monkeypatch, cfg, m, k, n):
     monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
     g = rng(cfg * 7 + m + k + n)
@@ -258,6 +260,7 @@ def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
                                        (5, 300, 520, 516), (2, 300, 1028, 516),
                                        (2, 2049, 4100, 2048), (2, 200, 8196, 260),
                                        (5, 129, 100, 132), (2, 64, 4, 128),
+                                       (6, 40, 6160, 2052), (6, 48, 6148, 2048),
                                        (2, 300, 512, 514), (2, 300, 1030, 516)])
 def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
     monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
@@ -320,3 +323,21 @@ def test_tiled_misaligned_operand_falls_back(hip, which, m, k, n):
     tb = view if which == "b" else hip.tensor(b)
     check(hip.matmul(ta, tb).numpy(), oracle.matmul(a, b), f"misaligned {which}")
     del view
+
+
+@pytest.mark.parametrize("m,k,n,long_k", [(64, 8192, 4096, True), (40, 6148, 2048, True),
+                                          (64, 4096, 4096, False), (48, 8192, 1024, False)])
+def test_long_k_rows_33_to_64_take_64x128_tiles(hip, monkeypatch, m, k, n, long_k):
+    """33-64 rows over K > 4096 with N >= 2048 run 64x128 DMA-staged tiles
+    split over K (the plan gives the bits of forcing that configuration);
+    other such shapes keep the skinny kernel (different bits: another K
+    split).  Both within the matmul bound of the oracle."""
+    g = rng(m + k + n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, oracle.matmul(a, b), f"plan {m}x{k}x{n}")
+    monkeypatch.setenv("CLOVE_GEMM_CFG", "6")
+    forced = hip.matmul(ta, tb).numpy()
+    assert np.array_equal(got, forced) == long_k
