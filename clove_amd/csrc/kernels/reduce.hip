@@ -109,7 +109,9 @@ __global__ void __launch_bounds__(kColThreads) bcast_grad_cols4_kernel(const flo
 // Measured at [4096, 4096] -> [4096] with cold inputs: 12.1 us (69% of HBM)
 // against 14.0 us for the two passes; 16-column strips (half lines, twice
 // the workgroups) 13-15.7 us, 64-column strips 15.7 us, 128 or 1024
-// threads 14.7-15.1 us, non-temporal loads 17.7 us.
+// threads 14.7-15.1 us, 512 threads 14.1 us, non-temporal loads 17.7 us;
+// batches of 4, 6 and 16 loads 13.6-14.0, 13.1-13.4 and 33 us against
+// 12.7-12.9 us for 8 (more requests in flight per CU return later).
 constexpr int kStripThreads = 256, kStripQuads = 8, kStripGroups = kStripThreads / kStripQuads;
 constexpr int kStripBatch = 8;
 __global__ void __launch_bounds__(kStripThreads) bcast_grad_strip_kernel(
