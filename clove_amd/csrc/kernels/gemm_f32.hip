@@ -1406,9 +1406,65 @@ void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
 
 }  // namespace
 
+// Tile shape and K split above 64 rows, for shapes the DMA kernels take
+// (whole 16-byte pieces along K and N, aligned operands under 2 GiB).  Each
+// candidate (128x128 or 64x128 tiles, K split s ways) is priced as its padded
+// MFMA work over how evenly its workgroups fill the CUs and an occupancy
+// factor, plus a split's reduce pass (the partial tiles written and read
+// back, the result written, one more launch):
+//  * balance u / ceil(u), u = workgroups per CU: a CU's share comes in whole
+//    workgroups, so 2.25 per CU takes as long as 3;
+//  * one workgroup alone on a CU waits on its own loads and barriers (x0.85
+//    for 128x128; x0.80 for 64x128, whose waves hold half the MFMA work
+//    each), and 64x128 tiles still trail at two per CU (x0.95);
+//  * 128x128 tiles are preferred by 2% where the rest ties.
+// Against the fixed rule it replaces (128x128 tiles, split only below two
+// per CU), measured in TFLOP/s with HIP events: 2048^3 122 -> 131, 2100^3
+// 90 -> 110, 2560^3 106 -> 121, 2900^3 92 -> 118, 1536^3 88 -> 100,
+// 768x4096x4096 100 -> 124, 4096x1024x1024 109 -> 125, 16384x784x128
+// 80 -> 101, 3500x700x2900 105 -> 120; shapes that fill the chip evenly keep
+// unsplit 128x128 tiles (4096^3, 3072x4096x4096, 2048x4096x4096).
+struct TileChoice {
+    int cfg, splits;
+};
+
+static TileChoice choose_tiles(int M, int N, int K, int num_cus) {
+    constexpr double kMfma = 1.4e14;  // sustained FP32 MFMA FLOP/s
+    constexpr double kHbm = 8e12;     // bytes/s
+    constexpr double kLaunch = 3e-6;  // a second launch, s
+    static const int kSplits[] = {1, 2, 3, 4, 6, 8, 12, 16, 24, 32, 48, 64};
+    const int slabs = (K + 15) / 16;  // BK = 16 in both configurations
+    TileChoice best{CFG_128x128, 1};
+    double best_t = 0.0;
+    for (const int cfg : {CFG_128x128, CFG_64x128}) {
+        const int BM = kCfgBM[cfg], BN = kCfgBN[cfg];
+        const int64_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
+        for (const int s : kSplits) {
+            if (s > 1 && s > slabs / 4) break;  // at least four slabs per split
+            const int per = (slabs + s - 1) / s;
+            const int made = (slabs + per - 1) / per;
+            const double u = (double)(tm * tn * made) / num_cus;
+            const double bal = u / std::ceil(u);
+            double occ = 1.0;
+            if (u <= 1.0) occ = cfg == CFG_128x128 ? 0.85 : 0.80;
+            else if (u <= 2.0 && cfg == CFG_64x128) occ = 0.95;
+            const double pref = cfg == CFG_128x128 ? 1.02 : 1.0;
+            const double work = 2.0 * (double)(tm * BM) * (double)(tn * BN) * (double)made *
+                                (double)per * 16.0;
+            double t = work / kMfma / (bal * occ * pref);
+            if (made > 1) t += (2.0 * made + 1.0) * 4.0 * (double)M * (double)N / kHbm + kLaunch;
+            if (best_t == 0.0 || t < best_t) {
+                best_t = t;
+                best = {cfg, made};
+            }
+        }
+    }
+    return best;
+}
+
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned,
                    bool force_skinny, int force_skinny_nb, int force_skinny_splits,
-                   bool force_strip, bool b_aligned) {
+                   bool force_strip, bool b_aligned, bool rows64) {
     GemmPlan p{};
     p.M = M;
     p.N = N;
@@ -1529,21 +1585,31 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // 4096 x 4096 1.230 ms against 1.657 in 128x256 tiles (two to a CU, 640
     // tiles: two rounds), 7168 x 4096 x 4096 1.700 against 1.944, 4096^3
     // 0.974 against 0.975 (one round of each).  128x256 stays selectable
-    // (CLOVE_GEMM_CFG=5).
+    // (CLOVE_GEMM_CFG=5).  Where the DMA kernels take the shape, choose_tiles
+    // weighs 64x128 tiles and the K split against them.
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? (long_k64 ? CFG_64x128 : CFG_64x64) : CFG_128x128);
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
+    const bool modeled = rows64 && force_cfg < 0 && M > 64 && K % 4 == 0 && N % 4 == 0 &&
+                         a_aligned && b_aligned && (uint64_t)M * K * 4 < (1ull << 31) &&
+                         b_bytes < (1ull << 31);
+    TileChoice choice{cfg, 1};
+    if (modeled) choice = choose_tiles(M, N, K, num_cus);
+    cfg = choice.cfg;
     p.cfg = cfg;
     const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
     p.tiles_n = (N + BN - 1) / BN;
     p.tiles = ((M + BM - 1) / BM) * p.tiles_n;
-    // Split K when the tiles alone cannot fill the chip, and for 128-row
+    // Shapes choose_tiles does not take: split K when the tiles alone cannot
+    // fill the chip, and for 128-row
     // tiles over K >= 1024 when they give a CU fewer than two workgroups (one
     // alone waits on its own loads and barriers: 1024 x 4096 x 4096 in 256
     // tiles ran 0.276 ms, 2047 x 4096 x 2052 in 272 0.497 ms): aim for about
     // two, each split covering at least four K slabs.
     const int slabs = (K + BK - 1) / BK;
     int splits = 1;
-    if (p.tiles < num_cus || (BM == 128 && slabs >= 64 && p.tiles < 2 * num_cus)) {
+    if (modeled) {
+        splits = choice.splits;
+    } else if (p.tiles < num_cus || (BM == 128 && slabs >= 64 && p.tiles < 2 * num_cus)) {
         splits = (2 * num_cus + p.tiles - 1) / p.tiles;
         const int max_splits = slabs / 4 > 1 ? slabs / 4 : 1;
         if (splits > max_splits) splits = max_splits;

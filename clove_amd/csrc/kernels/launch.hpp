@@ -135,11 +135,12 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 // path wherever it is legal, with force_skinny_nb (1, 2, 4) /
 // force_skinny_splits > 0 overriding its plan; force_strip takes the strip
 // path wherever it is legal (M <= 32, even N, K % 4 == 0, K <= 16384; tuning
-// and tests).  Every plan computes the same product.
+// and tests).  rows64 = false keeps 128-row tiles above 64 rows (the tilings
+// gemm_f32_transposed takes).  Every plan computes the same product.
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned = true,
                    bool force_skinny = false, int force_skinny_nb = 0,
                    int force_skinny_splits = 0, bool force_strip = false,
-                   bool b_aligned = true);
+                   bool b_aligned = true, bool rows64 = true);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
 // C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the

@@ -341,3 +341,30 @@ def test_long_k_rows_33_to_64_take_64x128_tiles(hip, monkeypatch, m, k, n, long_
     monkeypatch.setenv("CLOVE_GEMM_CFG", "6")
     forced = hip.matmul(ta, tb).numpy()
     assert np.array_equal(got, forced) == long_k
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (3000, 3000, 3000),   # 64x128 tiles, K split two ways; ragged edges and a K tail
+    (1536, 1536, 1536),   # 64x128 tiles, four splits
+    (2100, 2100, 2100),   # 64x128 tiles, four splits, ragged
+    (2048, 2048, 2048),   # 64x128 tiles unsplit (two per CU)
+    (256, 4096, 4096),    # 64x128 tiles, six splits
+    (16384, 784, 128),    # 64x128 tiles, one per CU over a short K
+    (2560, 2560, 2560),   # 128x128 tiles, three splits
+    (768, 4096, 4096)])   # 64x128 tiles, two splits
+def test_planner_tile_and_split_choices(hip, m, k, n):
+    """Above 64 rows the planner weighs 128x128 against 64x128 tiles and
+    the K split by their load balance over the CUs, occupancy and the
+    reduce pass.  Sampled row ranges of each resulting plan (first, last,
+    and across a 64- and a 128-row tile edge) against the oracle; a
+    repeated call gives the same bits."""
+    g = rng(m + 5 * k + 11 * n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    for lo, hi in ((0, 3), (62, 66), (126, 130), (m - 3, m)):
+        lo, hi = max(0, lo), min(m, hi)
+        want = oracle.matmul(a, b, rows=(lo, hi))[lo:hi]
+        check(got[lo:hi], want, f"plan {m}x{k}x{n} rows {lo}..{hi}")
+    assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
