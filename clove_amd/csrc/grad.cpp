@@ -89,11 +89,10 @@ TensorNode HipBackend::softmax_backward(const TensorNode &y_, const TensorNode &
 
 // backend.rs:1314-1360: grad_a = grad_out . b^T (a's shape, m = prod of a's
 // leading dims), grad_b = a^T . grad_out ([k, n]).  Each product is the MFMA
-// GEMM; where its plan allows (128x128 / 128x256 tilings, split over K or
-// not, whose operand rows hold whole 16-byte pieces) the GEMM reads the transposed
-// operand directly (k::gemm_f32_transposed), else it runs on a transposed
-// copy.  Both plan with 128-row tiles (rows64 = false: the transposed loads
-// exist for those tilings), so both give the same bits.
+// GEMM; where its plan allows (128x128, 128x256 and 64x128 tilings, split
+// over K or not, whose operand rows hold whole 16-byte pieces) the GEMM reads
+// the transposed operand directly (k::gemm_f32_transposed), else it runs on a
+// transposed copy with the same plan.  Both give the same bits.
 // CLOVE_GEMM_TRANSPOSED=0 forces the copies (tests).
 static bool transposed_loads_enabled() {
     const char *v = std::getenv("CLOVE_GEMM_TRANSPOSED");
@@ -127,29 +126,27 @@ void HipBackend::matmul_backward(const TensorNode &a_, const TensorNode &b_, con
         TensorNode da = new_tensor(a.shape, CLOVE_HIP_F32);
         Tensor dav;
         view2d(*da, m, kk, &dav);
-        const k::GemmPlan p = k::gemm_plan((int)m, (int)kk, (int)n, cus, -1, true, false, 0, 0,
-                                           false, true, /*rows64=*/false);
+        const k::GemmPlan p = k::gemm_plan((int)m, (int)kk, (int)n, cus, -1);
         TensorNode ws;
         if (direct && p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
         if (!(direct && k::gemm_f32_transposed(p, g.f32(), b.f32(), da->f32(),
                                                ws ? ws->f32() : nullptr, false, true, s))) {
             TensorNode bt = new_tensor({n, kk}, CLOVE_HIP_F32);
             k::transpose(b.f32(), bt->f32(), kk, n, s);
-            matmul_into(gv, *bt, dav, nullptr, 0, /*rows64=*/false);
+            matmul_into(gv, *bt, dav);
         }
         *grad_a = da;
     }
     if (grad_b) {  // ([m, kk])^T . [m, n]
         TensorNode db = new_tensor({kk, n}, CLOVE_HIP_F32);
-        const k::GemmPlan p = k::gemm_plan((int)kk, (int)n, (int)m, cus, -1, true, false, 0, 0,
-                                           false, true, /*rows64=*/false);
+        const k::GemmPlan p = k::gemm_plan((int)kk, (int)n, (int)m, cus, -1);
         TensorNode ws;
         if (direct && p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);
         if (!(direct && k::gemm_f32_transposed(p, a.f32(), g.f32(), db->f32(),
                                                ws ? ws->f32() : nullptr, true, false, s))) {
             TensorNode at = new_tensor({kk, m}, CLOVE_HIP_F32);
             k::transpose(a.f32(), at->f32(), m, kk, s);
-            matmul_into(*at, gv, *db, nullptr, 0, /*rows64=*/false);
+            matmul_into(*at, gv, *db);
         }
         *grad_b = db;
     }

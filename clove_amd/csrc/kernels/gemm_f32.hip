@@ -1465,7 +1465,7 @@ static TileChoice choose_tiles(int M, int N, int K, int num_cus) {
 
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned,
                    bool force_skinny, int force_skinny_nb, int force_skinny_splits,
-                   bool force_strip, bool b_aligned, bool rows64) {
+                   bool force_strip, bool b_aligned) {
     GemmPlan p{};
     p.M = M;
     p.N = N;
@@ -1590,7 +1590,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // weighs 64x128 tiles and the K split against them.
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? (long_k64 ? CFG_64x128 : CFG_64x64) : CFG_128x128);
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
-    const bool modeled = rows64 && force_cfg < 0 && M > 64 && K % 4 == 0 && N % 4 == 0 &&
+    const bool modeled = force_cfg < 0 && M > 64 && K % 4 == 0 && N % 4 == 0 &&
                          a_aligned && b_aligned && (uint64_t)M * K * 4 < (1ull << 31) &&
                          b_bytes < (1ull << 31);
     TileChoice choice{cfg, 1};
@@ -1658,7 +1658,7 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
     if (ta == tb) return false;  // exactly one operand read transposed (the matmul backward)
     if (p.small || p.skinny || p.strip || p.K <= 0 || (p.splits > 1 && !ws)) return false;
     if (((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) != 0) return false;
-    if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128) return false;
+    if (p.cfg != CFG_128x256 && p.cfg != CFG_128x128 && p.cfg != CFG_64x128) return false;
     const GemmArgs g{A, B, C, ws, p.M, p.N, p.K, p.tiles_n, p.k_per_split, p.splits,
                      GemmEpilogue{}, p.tiles, (p.tiles + 7) / 8};
     const dim3 grid((unsigned)(g.per_xcd * 8), (unsigned)p.splits);
@@ -1690,6 +1690,13 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
             else
                 gemm_f32_dma_kernel<128, 256, 16, 64, 128, false, false, true, kDmaStages, true>
                     <<<grid, 256, 0, s>>>(g);
+        } else if (p.cfg == CFG_64x128) {
+            if (ta)
+                gemm_f32_dma_kernel<64, 128, 16, 32, 64, false, true, false, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
+            else
+                gemm_f32_dma_kernel<64, 128, 16, 32, 64, false, false, true, ST, true>
+                    <<<grid, 256, 0, s>>>(g);
         } else {
             if (ta)
                 gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, true, false, ST, true>
@@ -1698,6 +1705,17 @@ bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, floa
                 gemm_f32_dma_kernel<128, 128, 16, 64, 64, false, false, true, ST, true>
                     <<<grid, 256, 0, s>>>(g);
         }
+        reduce();
+        return true;
+    }
+    if (p.cfg == CFG_64x128) {
+        // DMA only: the register-staged kernel has no transposed 64x128 form
+        if (!dma_ok(p, 64, 128)) return false;
+        constexpr int ST = dma_stages(128);
+        if (ta)
+            gemm_f32_dma_kernel<64, 128, 16, 32, 64, false, true, false, ST><<<grid, 256, 0, s>>>(g);
+        else
+            gemm_f32_dma_kernel<64, 128, 16, 32, 64, false, false, true, ST><<<grid, 256, 0, s>>>(g);
         reduce();
         return true;
     }

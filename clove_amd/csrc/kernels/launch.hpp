@@ -135,21 +135,20 @@ void gemm_f32_grouped(const GemmPlan *plans, const float *const *A, const float 
 // path wherever it is legal, with force_skinny_nb (1, 2, 4) /
 // force_skinny_splits > 0 overriding its plan; force_strip takes the strip
 // path wherever it is legal (M <= 32, even N, K % 4 == 0, K <= 16384; tuning
-// and tests).  rows64 = false keeps 128-row tiles above 64 rows (the tilings
-// gemm_f32_transposed takes).  Every plan computes the same product.
+// and tests).  Every plan computes the same product.
 GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_aligned = true,
                    bool force_skinny = false, int force_skinny_nb = 0,
                    int force_skinny_splits = 0, bool force_strip = false,
-                   bool b_aligned = true, bool rows64 = true);
+                   bool b_aligned = true);
 void gemm_f32(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
               const GemmEpilogue &epi, hipStream_t s);
 // C = A^T . B (ta: A holds the [K, M] matrix) or C = A . B^T (tb: B holds the
 // [N, K] matrix), read transposed inside the tiled kernel's slab loads: the
 // same bits as transposing first.  ws: p.ws_floats floats when p splits K.
 // Launches nothing and returns false unless exactly one of ta, tb is set and
-// p is a 128x128 or 128x256 tiled plan with 16-byte aligned operands whose
-// transposed rows hold whole 16-byte pieces where its tiles are ragged; the
-// caller then transposes explicitly.
+// p is a 128x128 or 128x256 tiled plan, or a 64x128 one the DMA kernel takes,
+// with 16-byte aligned operands whose transposed rows hold whole 16-byte
+// pieces where its tiles are ragged; the caller then transposes explicitly.
 bool gemm_f32_transposed(const GemmPlan &p, const float *A, const float *B, float *C, float *ws,
                          bool ta, bool tb, hipStream_t s);
 

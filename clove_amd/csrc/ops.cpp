@@ -265,7 +265,7 @@ static bool gemm_skinny_override(int *nb, int *splits) {
 
 // Validates one product and builds its epilogue and plan.
 static k::GemmPlan prepare_matmul(const Tensor &a, const Tensor &b, const Tensor *bias, int act,
-                                  k::GemmEpilogue *epi, bool rows64 = true) {
+                                  k::GemmEpilogue *epi) {
     need_f32(a, "a");
     need_f32(b, "b");
     size_t m, kk, n;
@@ -287,7 +287,7 @@ static k::GemmPlan prepare_matmul(const Tensor &a, const Tensor &b, const Tensor
     const bool a_aligned = (reinterpret_cast<uintptr_t>(a.data) & 15) == 0;
     const bool b_aligned = (reinterpret_cast<uintptr_t>(b.data) & 15) == 0;
     return k::gemm_plan((int)m, (int)n, (int)kk, ctx().num_cus, gemm_cfg_override(), a_aligned,
-                        sk_force, sk_nb, sk_splits, gemm_strip_override(), b_aligned, rows64);
+                        sk_force, sk_nb, sk_splits, gemm_strip_override(), b_aligned);
 }
 
 // A product the grouped small kernel can take: the small path, and for a
@@ -297,9 +297,9 @@ static bool groupable(const k::GemmPlan &p, int act) {
 }
 
 void HipBackend::matmul_into(const Tensor &a, const Tensor &b, Tensor &out, const Tensor *bias,
-                             int act, bool rows64) {
+                             int act) {
     k::GemmEpilogue epi;
-    const k::GemmPlan p = prepare_matmul(a, b, bias, act, &epi, rows64);
+    const k::GemmPlan p = prepare_matmul(a, b, bias, act, &epi);
     hipStream_t s = ctx().stream;
     TensorNode ws;
     if (p.ws_floats) ws = new_tensor({p.ws_floats}, CLOVE_HIP_F32);

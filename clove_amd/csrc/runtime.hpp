@@ -153,9 +153,8 @@ struct HipBackend {
                                 Tensor &out);
     // Optional fused epilogue: out = act(a.b + bias[i % numel(bias)]) with
     // act 0 none, 1 ReLU, 2 GELU (CLOVE_OP_* elementwise semantics).
-    // rows64 = false keeps 128-row tiles (the backward's plans).
     static void matmul_into(const Tensor &a, const Tensor &b, Tensor &out,
-                            const Tensor *bias = nullptr, int act = 0, bool rows64 = true);
+                            const Tensor *bias = nullptr, int act = 0);
     // One member of a horizontal MatMul group: out = act(a.b + bias).
     struct GemmMember {
         const Tensor *a, *b;

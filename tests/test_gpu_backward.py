@@ -141,7 +141,10 @@ def test_matmul_backward_4096(hip):
                                    (2048, 2048, 2048), (2048, 2048, 1024),
                                    (3, 5, 7), (1000, 300, 500),
                                    # ragged tiles and K tails (edge form of the DMA kernel)
-                                   (4100, 4096, 4100), (4100, 2052, 2052), (2052, 4100, 4104)])
+                                   (4100, 4096, 4100), (4100, 2052, 2052), (2052, 4100, 4104),
+                                   # 64x128 tiles: unsplit, split, ragged with a K tail
+                                   (768, 4096, 4096), (1536, 1536, 1536), (3000, 3000, 3000),
+                                   (2100, 2100, 2100)])
 def test_matmul_backward_transposed_loads_match_copies(hip, monkeypatch, m, k, n):
     """Where the plan allows, the backward's GEMMs read b^T / a^T straight
     from b / a, by buffer->LDS DMA (the default; ragged tiles and K tails
