@@ -466,14 +466,30 @@ constexpr int dma_waves(int BM, int BN, int BK, int WM, int WN, int ST) {
     return lds < regs ? lds : regs;
 }
 
+// One buffer->LDS DMA of ONE float (4 bytes) or four (16 bytes) a lane.
+template <bool ONE>
+__device__ __forceinline__ void dma_lds(__amdgpu_buffer_rsrc_t r, float *dst, uint32_t voff,
+                                        int soff) {
+    if constexpr (ONE)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 4, (int)voff, soff, 0, 0);
+    else
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void *)dst, 16, (int)voff, soff, 0, 0);
+}
+
+// A1 / B1 (EDGE only): A's rows (K % 4 != 0) or B's rows (N % 4 != 0) are not
+// 16-byte aligned, so that operand moves one float a lane (4-byte DMA) into
+// the same LDS places, with the masks per element: the same bits again.
 template <int BM, int BN, int BK, int WM, int WN, bool EPI, bool TA = false, bool TB = false,
-          int ST = kDmaStages, bool EDGE = false>
+          int ST = kDmaStages, bool EDGE = false, bool A1 = false, bool B1 = false>
 __global__ void __launch_bounds__(256)
     __attribute__((amdgpu_waves_per_eu(dma_waves(BM, BN, BK, WM, WN, ST))))
     gemm_f32_dma_kernel(GemmArgs g) {
     constexpr int SA = BM * BK, SB = BK * BN, SS = SA + SB;
-    constexpr int IAW = SA / 256 / 4, IBW = SB / 256 / 4;  // 1 KiB DMAs per wave per slab
+    constexpr int AE = A1 ? 1 : 4, BE = B1 ? 1 : 4;    // floats a lane moves per DMA
+    constexpr int IAW = SA / 64 / AE / 4, IBW = SB / 64 / BE / 4;  // DMAs per wave per slab
     constexpr int KQ = BK / 4;                              // 16-byte slots per A row
+    static_assert(!(A1 && TA) && !(B1 && TB) && (EDGE || !(A1 || B1)),
+                  "4-byte DMA only for untransposed operands in the edge form");
     constexpr int WN_ = BN / WN, BMb = WM / 32, BNb = WN / 32;
     static_assert(SA % 1024 == 0 && SB % 1024 == 0, "whole DMA instructions per wave");
     static_assert(256 % BN == 0 || BN % 256 == 0, "B rows tile the 1 KiB pieces");
@@ -502,23 +518,24 @@ __global__ void __launch_bounds__(256)
     int ak[IAW], bk[IBW];  // (EDGE) the k within a slab of this lane's A and B pieces
 #pragma unroll
     for (int u = 0; u < IAW; ++u) {
-        const int p = (wave * IAW + u) * 64 + lane;  // 16-byte position in the A stage
+        const int p = (wave * IAW + u) * 64 + lane;  // AE-float position in the A stage
         if constexpr (TA) {  // k-major: row k, four m (M % 4 == 0 for EDGE)
             const int row = 4 * p / BM, col = 4 * p % BM;
             aoff[u] = ((uint32_t)(k_begin + row) * (uint32_t)M + (uint32_t)(m0 + col)) * 4u;
             if (EDGE && m0 + col >= M) aoff[u] = kOutside;
             ak[u] = row;
-        } else {
-            const int row = p / KQ, slot = p % KQ;
+        } else {  // row m: 16-byte slot s holds k-piece s ^ ((m >> 2) & (KQ - 1))
+            const int e = p * AE, row = e / BK, slot = (e % BK) / 4, within = e % 4;
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
-            aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq)) * 4u;
+            aoff[u] = ((uint32_t)(m0 + row) * (uint32_t)K + (uint32_t)(k_begin + 4 * kq + within)) *
+                      4u;
             if (EDGE && m0 + row >= M) aoff[u] = kOutside;
-            ak[u] = 4 * kq;
+            ak[u] = 4 * kq + within;
         }
     }
 #pragma unroll
     for (int u = 0; u < IBW; ++u) {
-        const int p = (wave * IBW + u) * 64 + lane;  // 16-byte position in the B stage
+        const int p = (wave * IBW + u) * 64 + lane;  // BE-float position in the B stage
         if constexpr (TB) {  // n-major: row n, four k
             const int row = p / KQ, slot = p % KQ;
             const int kq = slot ^ ((row >> 2) & (KQ - 1));
@@ -526,7 +543,7 @@ __global__ void __launch_bounds__(256)
             if (EDGE && n0 + row >= N) boff[u] = kOutside;
             bk[u] = 4 * kq;
         } else {
-            const int row = 4 * p / BN, col = 4 * p % BN;
+            const int row = BE * p / BN, col = BE * p % BN;
             boff[u] = ((uint32_t)(k_begin + row) * (uint32_t)N + (uint32_t)(n0 + col)) * 4u;
             if (EDGE && n0 + col >= N) boff[u] = kOutside;
             bk[u] = row;
@@ -543,27 +560,23 @@ __global__ void __launch_bounds__(256)
                 const uint32_t o = aoff[u] != kOutside && k0 + ak[u] < k_len
                                        ? aoff[u] + (uint32_t)(sl * a_step)
                                        : kOutside;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(st + (wave * IAW + u) * 256),
-                                                         16, (int)o, 0, 0, 0);
+                dma_lds<A1>(ra, st + (wave * IAW + u) * 64 * AE, o, 0);
             }
 #pragma unroll
             for (int u = 0; u < IBW; ++u) {
                 const uint32_t o = boff[u] != kOutside && k0 + bk[u] < k_len
                                        ? boff[u] + (uint32_t)(sl * b_step)
                                        : kOutside;
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                    rb, (lds_void *)(st + SA + (wave * IBW + u) * 256), 16, (int)o, 0, 0, 0);
+                dma_lds<B1>(rb, st + SA + (wave * IBW + u) * 64 * BE, o, 0);
             }
             return;
         }
 #pragma unroll
         for (int u = 0; u < IAW; ++u)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (lds_void *)(st + (wave * IAW + u) * 256), 16,
-                                                     (int)aoff[u], sl * a_step, 0, 0);
+            dma_lds<A1>(ra, st + (wave * IAW + u) * 64 * AE, aoff[u], sl * a_step);
 #pragma unroll
         for (int u = 0; u < IBW; ++u)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rb, (lds_void *)(st + SA + (wave * IBW + u) * 256),
-                                                     16, (int)boff[u], sl * b_step, 0, 0);
+            dma_lds<B1>(rb, st + SA + (wave * IBW + u) * 64 * BE, boff[u], sl * b_step);
     };
     f16v acc[BMb][BNb];
 #pragma unroll
@@ -1293,6 +1306,30 @@ bool dma_edge_ok(const GemmPlan &p, int BM, int BN) {
            (uint64_t)p.K * p.N * 4 < (1ull << 31);
 }
 
+// Rows that are not 16-byte aligned (K or N not a multiple of 4, or an
+// operand that starts off a 16-byte boundary) in 128x128 or 64x128 tiles:
+// the edge form with that operand moved one float a lane.
+bool dma_odd_ok(const GemmPlan &p, int BM, int BN) {
+    const char *v = std::getenv("CLOVE_GEMM_DMA");
+    const bool enabled = !(v && *v && std::atoi(v) == 0);
+    return enabled && !p.vec && BN == 128 && (BM == 128 || BM == 64) &&
+           p.k_per_split % 16 == 0 && (uint64_t)p.M * p.K * 4 < (1ull << 31) &&
+           (uint64_t)p.K * p.N * 4 < (1ull << 31);
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int ST, bool EPI>
+void launch_dma_odd(bool a1, bool b1, dim3 grid, const GemmArgs &g, hipStream_t s) {
+    if (a1 && b1)
+        gemm_f32_dma_kernel<BM, BN, BK, WM, WN, EPI, false, false, ST, true, true, true>
+            <<<grid, 256, 0, s>>>(g);
+    else if (a1)
+        gemm_f32_dma_kernel<BM, BN, BK, WM, WN, EPI, false, false, ST, true, true, false>
+            <<<grid, 256, 0, s>>>(g);
+    else
+        gemm_f32_dma_kernel<BM, BN, BK, WM, WN, EPI, false, false, ST, true, false, true>
+            <<<grid, 256, 0, s>>>(g);
+}
+
 template <int BM, int BN, int BK, int WM, int WN>
 void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
     const dim3 grid((unsigned)(g.per_xcd * 8), (unsigned)p.splits);
@@ -1317,6 +1354,17 @@ void launch_cfg(const GemmPlan &p, GemmArgs g, hipStream_t s) {
                 gemm_f32_dma_kernel<BM, BN, BK, WM, WN, false, false, false, ST, true>
                     <<<grid, 256, 0, s>>>(g);
             return;
+        }
+        if constexpr (BN == 128) {
+            if (dma_odd_ok(p, BM, BN)) {
+                const bool a1 = p.K % 4 != 0 || (reinterpret_cast<uintptr_t>(g.A) & 15) != 0;
+                const bool b1 = p.N % 4 != 0 || (reinterpret_cast<uintptr_t>(g.B) & 15) != 0;
+                if (epi)
+                    launch_dma_odd<BM, BN, BK, WM, WN, ST, true>(a1, b1, grid, g, s);
+                else
+                    launch_dma_odd<BM, BN, BK, WM, WN, ST, false>(a1, b1, grid, g, s);
+                return;
+            }
         }
     }
     if (epi) {
@@ -1406,8 +1454,8 @@ void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
 
 }  // namespace
 
-// Tile shape and K split above 64 rows, for shapes the DMA kernels take
-// (whole 16-byte pieces along K and N, aligned operands under 2 GiB).  Each
+// Tile shape and K split above 64 rows, for operands under 2 GiB (the DMA
+// kernels' limit).  Each
 // candidate (128x128 or 64x128 tiles, K split s ways) is priced as its padded
 // MFMA work over how evenly its workgroups fill the CUs and an occupancy
 // factor, plus a split's reduce pass (the partial tiles written and read
@@ -1587,11 +1635,11 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // tiles: two rounds), 7168 x 4096 x 4096 1.700 against 1.944, 4096^3
     // 0.974 against 0.975 (one round of each).  128x256 stays selectable
     // (CLOVE_GEMM_CFG=5).  Where the DMA kernels take the shape, choose_tiles
-    // weighs 64x128 tiles and the K split against them.
+    // weighs 64x128 tiles and the K split against them (either tiling runs
+    // on DMA whatever the alignment of the rows).
     int cfg = M <= 32 ? CFG_32x128 : (M <= 64 ? (long_k64 ? CFG_64x128 : CFG_64x64) : CFG_128x128);
     if (force_cfg >= 0 && force_cfg < CFG_COUNT) cfg = force_cfg;
-    const bool modeled = force_cfg < 0 && M > 64 && K % 4 == 0 && N % 4 == 0 &&
-                         a_aligned && b_aligned && (uint64_t)M * K * 4 < (1ull << 31) &&
+    const bool modeled = force_cfg < 0 && M > 64 && (uint64_t)M * K * 4 < (1ull << 31) &&
                          b_bytes < (1ull << 31);
     TileChoice choice{cfg, 1};
     if (modeled) choice = choose_tiles(M, N, K, num_cus);

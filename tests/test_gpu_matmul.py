@@ -252,7 +252,8 @@ def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
 # of B past N and pieces past K read as zeros, stores bounds-checked): the
 # register-staged kernel's bits, single launch and split-K (the K tail in
 # the last split), plain and with the fused column-bias epilogue.
-# N % 4 != 0 or K % 4 != 0 keeps the register-staged kernel (the last two).
+# N % 4 != 0 or K % 4 != 0 (the last eight, 128x128 and 64x128 tiles) moves
+# that operand one float a lane, with the masks per element: the same bits.
 @pytest.mark.parametrize("cfg,m,k,n", [(5, 300, 512, 516), (2, 129, 1040, 132),
                                        (2, 200, 8192, 260), (5, 1000, 64, 1100),
                                        (5, 4097, 256, 4096), (2, 130, 4096, 1000),
@@ -261,7 +262,10 @@ def test_dma_kernel_epilogue(hip, monkeypatch, cfg):
                                        (2, 2049, 4100, 2048), (2, 200, 8196, 260),
                                        (5, 129, 100, 132), (2, 64, 4, 128),
                                        (6, 40, 6160, 2052), (6, 48, 6148, 2048),
-                                       (2, 300, 512, 514), (2, 300, 1030, 516)])
+                                       (2, 300, 512, 514), (2, 300, 1030, 516),
+                                       (2, 130, 1001, 257), (6, 300, 1030, 514),
+                                       (6, 200, 3001, 300), (2, 1000, 777, 1001),
+                                       (6, 65, 13, 131), (2, 257, 4099, 129)])
 def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
     monkeypatch.setenv("CLOVE_GEMM_CFG", str(cfg))
     g = rng(cfg * 5 + m + 3 * k + n)
@@ -307,12 +311,11 @@ def test_matmul_random_shapes_sweep(hip):
 @pytest.mark.parametrize("m,k,n", [(300, 512, 516), (32, 4096, 4096)])
 @pytest.mark.parametrize("which", ["a", "b"])
 def test_tiled_misaligned_operand_falls_back(hip, which, m, k, n):
-    """An A or B that is not 16-byte aligned takes the register-staged kernel's
-    scalar-load form: the DMA kernel moves 16-byte pieces, and the strip and
-    skinny kernels read A and B in 8- and 16-byte vectors.  At shapes whose
-    aligned operands take the DMA kernel's edge tiles (300 x 512 x 516) or
-    the strip kernel (32 x 4096 x 4096) the product is unchanged within the
-    matmul bound."""
+    """An A or B that is not 16-byte aligned moves one float a lane in the DMA
+    kernel's edge form (tiled shapes, 300 x 512 x 516), or takes the
+    register-staged kernel where the strip and skinny kernels would read it
+    in 8- and 16-byte vectors (32 x 4096 x 4096).  The product is unchanged
+    within the matmul bound."""
     g = rng((23 if which == "a" else 24) + m)
     a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
     b = g.normal(0, 1, (k, n)).astype(np.float32)
