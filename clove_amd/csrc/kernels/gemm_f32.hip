@@ -1564,18 +1564,25 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned && b_aligned &&
                           b_bytes < (1ull << 31) && force_cfg < 0;
     // Strip path (one launch, no workspace): M <= 32, even N, B of 4 MiB or
-    // more, enough 16 x 32 tiles for every CU, and K within the longest
-    // unrolled walk (4 waves x 64 chunks of 64 k).
+    // more, K within the longest unrolled walk (4 waves x 64 chunks of 64 k)
+    // and filling at least 90% of the walk it takes (the walks come in
+    // powers of two: K = 6144 on an 8192 walk measured 43.0 us at 32 x K x
+    // 4096 against 24.1 for the skinny kernel, K = 11008 on 16384 84.5
+    // against 41.9), and between half a workgroup and three per CU (one
+    // 96 KiB workgroup fits a CU: 32 x 4096 x 50256, 3142 workgroups, 260 us
+    // against 185; 1 x 4096 x 4096, 128 workgroups, 13.0 us against 16.5).
     {
         const int halves = (M + 15) / 16, strips = (N + 31) / 32;
+        int nch = 1;
+        while (nch < 64 && kStripWaves * 64 * nch < K) nch *= 2;
+        const int64_t wgs = (int64_t)halves * strips;
+        const bool fits = 10 * (int64_t)K >= 9 * (int64_t)(kStripWaves * 64 * nch);
         if (eligible && !force_skinny && M <= 32 && N % 2 == 0 && K <= kStripWaves * 64 * 64 &&
-            (force_strip ||
-             (b_bytes >= (4ull << 20) && (int64_t)halves * strips >= num_cus))) {
+            (force_strip || (b_bytes >= (4ull << 20) && fits && 2 * wgs >= num_cus &&
+                             wgs <= 3 * (int64_t)num_cus))) {
             p.strip = true;
             p.tiles_n = strips;
             p.tiles = halves * strips;
-            int nch = 1;
-            while (nch < 64 && kStripWaves * 64 * nch < K) nch *= 2;
             p.k_per_wave = 64 * nch;
             p.waves = kStripWaves;
             p.splits = 1;
@@ -1598,6 +1605,8 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         int nb = p.mb == 1 ? 4 : 2;
         if (force_skinny_nb == 1 || force_skinny_nb == 2 || (force_skinny_nb == 4 && p.mb == 1))
             nb = force_skinny_nb;
+        // (four 4-byte loads a lane for N % 4 != 0, keeping four column
+        // blocks, measured no faster: 16 x 4096 x 50257 243 us against 248)
         while (nb > 1 && N % nb != 0) nb /= 2;
         p.nb = nb;
         p.waves = (nb == 1 || (nb == 2 && p.mb == 1)) ? 8 : 4;

@@ -107,11 +107,13 @@ def test_strip_shapes(hip, monkeypatch, m, k, n):
 # The skinny path (M <= 64, K % 4 == 0, 16-byte aligned A and B): 32*nb columns
 # per workgroup, a K split over the workgroup's waves and across workgroups.
 # The plan picks it for B >= 4 MiB; CLOVE_GEMM_SKINNY forces it on the small
-# edge shapes here.
+# edge shapes here; N % 4 != 0 (N = 1, 33, 31, 5003, 4099, 8191) narrows the
+# column blocks per wave.
 @pytest.mark.parametrize("m,k,n", [(1, 4, 1), (5, 12, 33), (31, 20, 100), (32, 4096, 96),
                                    (33, 784, 128), (63, 1028, 200), (64, 4100, 64),
                                    (17, 8, 31), (64, 784, 10), (48, 2052, 40), (32, 36, 4096),
-                                   (30, 4096, 1000), (64, 2048, 1536)])
+                                   (30, 4096, 1000), (64, 2048, 1536), (16, 4096, 5003),
+                                   (40, 2048, 4099), (1, 4096, 8191)])
 def test_skinny_shapes(hip, monkeypatch, m, k, n):
     monkeypatch.setenv("CLOVE_GEMM_SKINNY", "0")
     g = rng(m * 11 + k * 5 + n)
@@ -370,4 +372,22 @@ def test_planner_tile_and_split_choices(hip, m, k, n):
         lo, hi = max(0, lo), min(m, hi)
         want = oracle.matmul(a, b, rows=(lo, hi))[lo:hi]
         check(got[lo:hi], want, f"plan {m}x{k}x{n} rows {lo}..{hi}")
+    assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (1, 4096, 4096),      # strip kernel at half a workgroup per CU
+    (32, 6144, 4096),     # a K the strip kernel's walks do not fit: skinny
+    (32, 4096, 14336),    # more strips than three per CU: skinny
+    (16, 4096, 50257),    # odd N: skinny with one column block per wave
+    (32, 4096, 11008)])   # strip kernel, 688 workgroups
+def test_decode_shapes_as_planned(hip, m, k, n):
+    """Decode-sized products on the paths the plan picks for them, against
+    the oracle; a repeated call gives the same bits."""
+    g = rng(m + 7 * k + 3 * n)
+    a = g.normal(0, 1 / np.sqrt(k), (m, k)).astype(np.float32)
+    b = g.normal(0, 1, (k, n)).astype(np.float32)
+    ta, tb = hip.tensor(a), hip.tensor(b)
+    got = hip.matmul(ta, tb).numpy()
+    check(got, oracle.matmul(a, b), f"decode {m}x{k}x{n}")
     assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
