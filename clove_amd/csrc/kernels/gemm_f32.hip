@@ -1562,7 +1562,8 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
         }
     }
     const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned && b_aligned &&
-                          b_bytes < (1ull << 31) && force_cfg < 0;
+                          b_bytes < (1ull << 31) && (uint64_t)M * K * 4 < (1ull << 31) &&
+                          force_cfg < 0;
     // Strip path (one launch, no workspace): M <= 32, even N, B of 4 MiB or
     // more, K within the longest unrolled walk (4 waves x 64 chunks of 64 k)
     // and filling at least 90% of the walk it takes (the walks come in

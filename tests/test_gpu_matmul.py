@@ -391,3 +391,24 @@ def test_decode_shapes_as_planned(hip, m, k, n):
     got = hip.matmul(ta, tb).numpy()
     check(got, oracle.matmul(a, b), f"decode {m}x{k}x{n}")
     assert np.array_equal(hip.matmul(ta, tb).numpy(), got)
+
+
+@pytest.mark.parametrize("which", ["a", "b"])
+def test_operands_past_2_gib(hip, which):
+    """An A or B of 2 GiB or more is past the 32-bit offsets of the buffer
+    loads (DMA, strip, skinny), so the product takes the register-staged
+    kernel, which indexes in 64 bits.  Rows (A) or columns (B) whose offsets
+    lie past 2^31 bytes are checked against the oracle."""
+    g = rng(31 if which == "a" else 32)
+    if which == "a":
+        m, k, n = 140000, 4096, 256
+    else:
+        m, k, n = 256, 4096, 140000
+    a = g.standard_normal((m, k), dtype=np.float32)
+    a *= np.float32(1 / 64)
+    b = g.standard_normal((k, n), dtype=np.float32)
+    got = hip.matmul(hip.tensor(a), hip.tensor(b)).numpy()
+    rows = ((0, 2), (131070, 131074), (m - 2, m)) if which == "a" else ((0, 2), (m - 2, m))
+    for lo, hi in rows:
+        want = oracle.matmul(a, b, rows=(lo, hi))[lo:hi]
+        check(got[lo:hi], want, f"{which} past 2 GiB rows {lo}..{hi}")
