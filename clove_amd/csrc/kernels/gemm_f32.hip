@@ -1455,11 +1455,10 @@ void launch_small(const GemmPlan &p, const GemmArgs &g, hipStream_t s) {
 }  // namespace
 
 // Tile shape and K split above 64 rows, for operands under 2 GiB (the DMA
-// kernels' limit).  Each
-// candidate (128x128 or 64x128 tiles, K split s ways) is priced as its padded
-// MFMA work over how evenly its workgroups fill the CUs and an occupancy
-// factor, plus a split's reduce pass (the partial tiles written and read
-// back, the result written, one more launch):
+// kernels' limit).  Each candidate (128x128 or 64x128 tiles, K split s ways)
+// is priced as its padded MFMA work over how evenly its workgroups fill the
+// CUs and an occupancy factor, plus a split's reduce pass (the partial tiles
+// written and read back, the result written, one more launch):
 //  * balance u / ceil(u), u = workgroups per CU: a CU's share comes in whole
 //    workgroups, so 2.25 per CU takes as long as 3;
 //  * one workgroup alone on a CU waits on its own loads and barriers (x0.85
