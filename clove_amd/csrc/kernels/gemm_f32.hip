@@ -1597,8 +1597,13 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // 64x8192x8192 89.8 against 110.5, 48x11008x4096 63.0 against 73.5; at
     // K = 4096 the skinny kernel stays ahead (64x4096x4096 28.5 against
     // 30.4 us), as it does for N = 1024.
-    const bool long_k64 = eligible && !force_skinny && M > 32 && K > 4096 && N >= 2048 &&
-                          N % 4 == 0;
+    // The same tiles win for 33-64 rows over a vocabulary-sized N (any
+    // alignment, on the 4-byte DMA form where N % 4 != 0): 64 x 4096 x 50256
+    // 279 against 308 us, 40 x 4096 x 32000 149 against 163, 36 x 4096 x 50257
+    // 317 against 346 (48 x 4096 x 50256 a tie; at N = 14336 the skinny
+    // kernel stays ahead, 75.5 against 84.1).
+    const bool long_k64 = eligible && !force_skinny && M > 32 &&
+                          ((K > 4096 && N >= 2048 && N % 4 == 0) || N >= 30000);
     if (eligible && !long_k64 && (force_skinny || b_bytes >= (4ull << 20))) {
         p.skinny = true;
         p.mb = M <= 32 ? 1 : 2;

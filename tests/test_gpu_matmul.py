@@ -331,10 +331,12 @@ def test_tiled_misaligned_operand_falls_back(hip, which, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n,long_k", [(64, 8192, 4096, True), (40, 6148, 2048, True),
-                                          (64, 4096, 4096, False), (48, 8192, 1024, False)])
+                                          (64, 4096, 4096, False), (48, 8192, 1024, False),
+                                          (40, 2048, 40001, True), (64, 1024, 32000, True)])
 def test_long_k_rows_33_to_64_take_64x128_tiles(hip, monkeypatch, m, k, n, long_k):
-    """33-64 rows over K > 4096 with N >= 2048 run 64x128 DMA-staged tiles
-    split over K (the plan gives the bits of forcing that configuration);
+    """33-64 rows over K > 4096 with N >= 2048, or over N >= 30000, run
+    64x128 DMA-staged tiles (the plan gives the bits of forcing that
+    configuration);
     other such shapes keep the skinny kernel (different bits: another K
     split).  Both within the matmul bound of the oracle."""
     g = rng(m + k + n)
