@@ -1476,7 +1476,9 @@ struct TileChoice {
     int cfg, splits;
 };
 
-static TileChoice choose_tiles(int M, int N, int K, int num_cus) {
+// only64: price 64x128 tiles alone (33-64 rows, where 128-row tiles waste
+// half their work).
+static TileChoice choose_tiles(int M, int N, int K, int num_cus, bool only64 = false) {
     constexpr double kMfma = 1.4e14;  // sustained FP32 MFMA FLOP/s
     constexpr double kHbm = 8e12;     // bytes/s
     constexpr double kLaunch = 3e-6;  // a second launch, s
@@ -1485,6 +1487,7 @@ static TileChoice choose_tiles(int M, int N, int K, int num_cus) {
     TileChoice best{CFG_128x128, 1};
     double best_t = 0.0;
     for (const int cfg : {CFG_128x128, CFG_64x128}) {
+        if (only64 && cfg != CFG_64x128) continue;
         const int BM = kCfgBM[cfg], BN = kCfgBN[cfg];
         const int64_t tm = (M + BM - 1) / BM, tn = (N + BN - 1) / BN;
         for (const int s : kSplits) {
@@ -1657,6 +1660,12 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
                          b_bytes < (1ull << 31);
     TileChoice choice{cfg, 1};
     if (modeled) choice = choose_tiles(M, N, K, num_cus);
+    // 33-64 rows on 64x128 tiles take the model's K split too: 40 x 2048 x
+    // 40001 157 -> 104 us, 33 x 4096 x 50257 316 -> 241, 64 x 4096 x 50256
+    // 280 -> 247, 64 x 1024 x 32000 45 -> 41 (40 x 4096 x 32000 149 -> 151,
+    // 64 x 8192 x 8192 78 -> 82 the other way; the rest within 1%).
+    const bool modeled64 = long_k64 && force_cfg < 0;
+    if (modeled64) choice = choose_tiles(M, N, K, num_cus, true);
     cfg = choice.cfg;
     p.cfg = cfg;
     const int BM = kCfgBM[cfg], BN = kCfgBN[cfg], BK = kCfgBK[cfg];
@@ -1670,7 +1679,7 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     // two, each split covering at least four K slabs.
     const int slabs = (K + BK - 1) / BK;
     int splits = 1;
-    if (modeled) {
+    if (modeled || modeled64) {
         splits = choice.splits;
     } else if (p.tiles < num_cus || (BM == 128 && slabs >= 64 && p.tiles < 2 * num_cus)) {
         splits = (2 * num_cus + p.tiles - 1) / p.tiles;
