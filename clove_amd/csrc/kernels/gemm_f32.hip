@@ -391,8 +391,8 @@ __global__ void __launch_bounds__(256) gemm_f32_mfma_kernel(GemmArgs g) {
             }
 }
 
-// The 128 x 128 and 128 x 256 configurations (tiles past M or N too: EDGE
-// below), A and B under 2 GiB: the register-staged kernel's tile, waves and
+// The 128 x 128, 128 x 256 and 64 x 128 configurations (tiles past M or N
+// too: EDGE below), A and B under 2 GiB: the register-staged kernel's tile, waves and
 // MFMA order with the slabs moved by buffer->LDS DMA instead of through
 // registers.
 // Each lane's 16 bytes land at its instruction's LDS base + 16 * lane, and

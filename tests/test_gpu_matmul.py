@@ -293,8 +293,9 @@ def test_dma_kernel_edge_tiles(hip, monkeypatch, cfg, m, k, n):
 
 def test_matmul_random_shapes_sweep(hip):
     """120 seeded random shapes across every plan the GEMM chooses (small,
-    strip, skinny, split-K and single-launch tiles, DMA-staged interior and
-    edge tiles, register-staged tiles for N or K not a multiple of 4 or 16):
+    strip, skinny, split-K and single-launch tiles in 128x128 and 64x128,
+    DMA-staged interior and edge tiles, the 4-byte DMA form for N or K not a
+    multiple of 4):
     each product within the matmul bound of the float64 product.  (float64
     stands in for the oracle here to keep the sweep fast; the oracle's own
     f32 result lies within the same bound of it, which the shape tests
