@@ -1659,7 +1659,15 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     const bool modeled = force_cfg < 0 && M > 64 && (uint64_t)M * K * 4 < (1ull << 31) &&
                          b_bytes < (1ull << 31);
     TileChoice choice{cfg, 1};
-    if (modeled) choice = choose_tiles(M, N, K, num_cus);
+    // Both operands in the 4-byte DMA form (K and N not multiples of 4, or
+    // unaligned operands) take 64x128 tiles: a 128x128 tile would issue 16
+    // DMAs per wave and slab and hold 121 VGPRs (749 x 3725 x 1673: 67
+    // TFLOP/s against 91 in 64x128 tiles; over the 12 such shapes timed the
+    // mean time fell about 2%, the others within run-to-run noise).  With one
+    // operand in that form the choice stays open (restricting it too cost
+    // 1-4% on most such shapes).
+    const bool both_four_byte = (K % 4 != 0 || !a_aligned) && (N % 4 != 0 || !b_aligned);
+    if (modeled) choice = choose_tiles(M, N, K, num_cus, both_four_byte);
     // 33-64 rows on 64x128 tiles take the model's K split too: 40 x 2048 x
     // 40001 157 -> 104 us, 33 x 4096 x 50257 316 -> 241, 64 x 4096 x 50256
     // 280 -> 247, 64 x 1024 x 32000 45 -> 41 (40 x 4096 x 32000 149 -> 151,
