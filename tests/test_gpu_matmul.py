@@ -356,7 +356,8 @@ def test_rows_33_to_64_plans(hip, m, k, n):
     (256, 4096, 4096),    # 64x128 tiles, six splits
     (16384, 784, 128),    # 64x128 tiles, one per CU over a short K
     (2560, 2560, 2560),   # 128x128 tiles, three splits
-    (768, 4096, 4096)])   # 64x128 tiles, two splits
+    (768, 4096, 4096),    # 64x128 tiles, two splits
+    (749, 3725, 1673)])   # K and N odd: 64x128 tiles on the 4-byte DMA form
 def test_planner_tile_and_split_choices(hip, m, k, n):
     """Above 64 rows the planner weighs 128x128 against 64x128 tiles and
     the K split by their load balance over the CUs, occupancy and the
