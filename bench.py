@@ -22,7 +22,8 @@ Rank 0 prints ONE JSON line on stdout:
   parts        the other configurations measured in the same run: the
                broadcast chain, softmax and layer norm (GB/s), 4096^3 (plain
                and with the planner's fused bias + GELU epilogue) and skinny
-               matmul (TFLOP/s), paged decode (tokens/s and GB/s), the
+               matmul (TFLOP/s), paged decode (tokens/s and GB/s; config 5
+               at D = 128 and the same shape at D = 96, the general kernel), the
                MLP plan (us per forward) and the backward passes and losses
                (GB/s; the matmul backward in TFLOP/s), attention prefill
                (TFLOP/s) and RoPE (GB/s), each with its roofline fraction and
@@ -30,6 +31,12 @@ Rank 0 prints ONE JSON line on stdout:
                on sampled query rows: the full one is ~20 s of host time),
                with the host CPU model; an HBM-bound part's `traffic` is the
                measured bytes per step of its kernels from the same summary.
+  parity_checked  true when every checked part's output (one more launch
+               of its first input set after all timings, the timed steps'
+               bits: the kernels are deterministic) is within its parity
+               bound of the oracle's output, computed by its CPU leg; else
+               the failing parts, and the exit status is 1.  parity_parts
+               names the parts checked.
 Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
 exits with a message.
 """
@@ -107,13 +114,42 @@ def defer(leg):
     CPU_LEGS.append(leg)
 
 
-def cpu_time(fn, reps=3):
+def cpu_time(fn, reps=3, keep=None):
+    """Median seconds of `reps` runs of fn; the last run's result is appended
+    to `keep` when a list is given."""
     best = []
     for _ in range(reps):
         t0 = time.perf_counter()
-        fn()
+        r = fn()
         best.append(time.perf_counter() - t0)
+    if keep is not None:
+        keep.append(r)
     return float(np.median(best))
+
+
+# Output parity of the timed parts: after every GPU timing, each checked part
+# runs once more on its first input set (the bytes its timed steps read; every
+# kernel here is deterministic, so these are the timed steps' output bits)
+# and is compared with the oracle's output, which its CPU leg computes anyway,
+# at the bound its parity tests use: |g - c| <= atol + rtol |c|.
+PARITY = {}
+
+
+def check_parity(name, got, want, rtol, atol):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    if got.shape != want.shape:
+        PARITY[name] = f"shape {got.shape} != {want.shape}"
+        return
+    err = np.abs(got - want)
+    bad = ~(err <= atol + rtol * np.abs(want))
+    PARITY[name] = "ok" if not bad.any() else \
+        f"{int(bad.sum())} of {err.size} elements out of bound (max abs err {err.max():.3e})"
+    log(f"parity {name}: {PARITY[name]}")
+
+
+def gemm_atol(want):
+    return 1e-4 * float(np.abs(want).max() or 1.0)
 
 
 def cpu_model():
@@ -187,19 +223,27 @@ def bench_rows(ca, oracle, args, out):
                 gh, bh = gam.numpy(), bet.numpy()
                 fn = (lambda: oracle.softmax(xs)) if name == "softmax" else \
                     (lambda: oracle.layer_norm(xs, gh, bh))
-                t = cpu_time(fn)
+                want = []
+                t = cpu_time(fn, keep=want)
                 part["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
                                                   "full [8192, 4096] workload, median of 3")
+                if name == "softmax":
+                    check_parity(name, ca.softmax(x).numpy(), want[0], 1e-4, 1e-9)
+                else:
+                    check_parity(name, ca.layer_norm(x, gam, bet).numpy(), want[0], 1e-4, 1e-5)
             defer(leg)
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), {per.mean() * 1e3:.1f} us")
 
 
-def bench_matmul(ca, oracle, args, out):
+def bench_matmul(ca, oracle, args, out, skinny_only=False):
     K = 4096
     a = ca.empty((4096, K)).fill_normal(3, 0.0, 1 / 64)
     b = ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64)
     a32 = ca.empty((32, K)).fill_normal(333, 0.0, 1 / 64)
+    if skinny_only:
+        bench_skinny(ca, oracle, args, out, a32, b)
+        return
     steps = max(5, args.steps // 10)
     # 30 untimed launches (~30 ms) bring the clocks from the HBM-bound parts
     # before to their steady MFMA level (10 left the first timed launches
@@ -212,15 +256,21 @@ def bench_matmul(ca, oracle, args, out):
     if not args.no_cpu:
         def leg():
             ah, bh = a.numpy(), b.numpy()
-            t = cpu_time(lambda: oracle.matmul(ah, bh), reps=1)
+            want = []
+            t = cpu_time(lambda: oracle.matmul(ah, bh), reps=1, keep=want)
             part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
                                               "full 4096^3 product (B transpose included), "
                                               "one run")
+            check_parity("matmul_4096", ca.matmul(a, b).numpy(), want[0], 2e-3,
+                         gemm_atol(want[0]))
             ah32 = a32.numpy()
-            t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=3)
+            want = []
+            t = cpu_time(lambda: oracle.matmul(ah32, bh), reps=3, keep=want)
             out["matmul_skinny_32"]["cpu_baseline"] = cpu_record(
                 oracle, round(2.0 * 32 * K * 4096 / t / 1e12, 5), "TFLOP/s",
                 "full 32x4096x4096 product (B transpose included), median of 3")
+            check_parity("matmul_skinny_32", ca.matmul(a32, b).numpy(), want[0], 2e-3,
+                         gemm_atol(want[0]))
         defer(leg)
     out["matmul_4096"] = part
     log(f"matmul 4096^3: {tf:.1f} TFLOP/s ({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), "
@@ -238,12 +288,21 @@ def bench_matmul(ca, oracle, args, out):
     if not args.no_cpu:
         def eleg():
             ah, bh, biash = a.numpy(), b.numpy(), bias.numpy()
-            t = cpu_time(lambda: oracle.gelu(oracle.add(oracle.matmul(ah, bh), biash)), reps=1)
+            want = []
+            t = cpu_time(lambda: oracle.gelu(oracle.add(oracle.matmul(ah, bh), biash)), reps=1,
+                         keep=want)
             epart["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
                                                "full 4096^3 product, bias and GELU, one run")
+            check_parity("matmul_4096_bias_gelu", model.execute([a, b, bias])[0].numpy(),
+                         want[0], 2e-3, gemm_atol(want[0]))
         defer(eleg)
     out["matmul_4096_bias_gelu"] = epart
     log(f"matmul 4096^3 + bias + GELU (fused): {tf:.1f} TFLOP/s, {per.mean():.3f} ms")
+    bench_skinny(ca, oracle, args, out, a32, b)
+
+
+def bench_skinny(ca, oracle, args, out, a32, b):
+    K = 4096
     # B (64 MiB) is what the skinny product streams: one copy per input set
     bs = [b] + [ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64) for _ in range(args.sets - 1)]
     wall, per = timed(ca, rotating([lambda bb=bb: ca.matmul(a32, bb) for bb in bs]), args.steps,
@@ -260,10 +319,20 @@ def bench_matmul(ca, oracle, args, out):
 
 
 def bench_paged(ca, oracle, args, out):
+    """Config 5 (D = 128, the fixed-shape kernel), and the same shape at
+    D = 96, a head dim only the general kernel runs (a 3072-wide model with
+    32 heads)."""
+    from clove_amd import workloads
+
+    for D, name in ((workloads.PAGED["head_dim"], "paged_decode"), (96, "paged_decode_d96")):
+        paged_case(ca, oracle, args, out, D, name)
+
+
+def paged_case(ca, oracle, args, out, D, name):
     from clove_amd import workloads
 
     P = workloads.PAGED
-    B, H, D, bs, nb = P["num_seqs"], P["num_heads"], P["head_dim"], P["block_size"], P["pool_blocks"]
+    B, H, bs, nb = P["num_seqs"], P["num_heads"], P["block_size"], P["pool_blocks"]
     ctx, bt = workloads.paged_layout(4)
     kv = ca.empty((2, nb, bs, H, D)).fill_normal(4)
     q = ca.tensor(np.random.Generator(np.random.PCG64(4)).standard_normal((B, H * D), dtype=np.float32))
@@ -275,7 +344,7 @@ def bench_paged(ca, oracle, args, out):
     gbs = nbytes / sec / 1e9
     part = {"value": round(B / sec, 1), "unit": "tokens/s", "ms": round(per.mean(), 4),
             "gbs": round(gbs, 1), "bytes": nbytes, "context_tokens": int(ctx.sum()),
-            "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
+            "head_dim": D, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
     if not args.no_cpu:
         def leg():
             seqs = list(range(B))
@@ -286,14 +355,21 @@ def bench_paged(ca, oracle, args, out):
                 lambda p, b: kv.read(p * plane + b * blk, blk).reshape(bs, H, D), bt, ctx, seqs,
                 bs)
             qh = q.numpy()
-            t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl))
+            want = []
+            t = cpu_time(lambda: oracle.paged_attention(qh, None, None, pool, sbt, scl),
+                         keep=want)
             part["cpu_baseline"] = cpu_record(oracle, round(B / t, 2), "tokens/s",
-                                              "full config 5 decode (32 sequences, all heads) "
-                                              "on the blocks it reads, median of 3")
+                                              f"full config 5 decode at D={D} (32 sequences, "
+                                              "all heads) on the blocks it reads, median of 3")
+            got = ca.paged_attention(q, None, None, kv, tbt, tcl).numpy()
+            check_parity(name, got, want[0].reshape(got.shape), 2e-3, 1e-5)
+            kv.free()
         defer(leg)
-    out["paged_decode"] = part
-    log(f"paged decode: {B / sec:.0f} tokens/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM), "
-        f"{per.mean() * 1e3:.1f} us")
+    else:
+        kv.free()
+    out[name] = part
+    log(f"{name} (D={D}): {B / sec:.0f} tokens/s, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of "
+        f"HBM), {per.mean() * 1e3:.1f} us")
 
 
 def bench_mlp(ca, oracle, args, out):
@@ -312,9 +388,11 @@ def bench_mlp(ca, oracle, args, out):
             f"{model.num_steps} steps)", "gpu_us": round(per.mean() * 1e3, 2)}
     if not args.no_cpu:
         def leg():
-            t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5)
+            want = []
+            t = cpu_time(lambda: oracle.mlp_forward(x, w1, b1, w2, b2), reps=5, keep=want)
             part["cpu_baseline"] = cpu_record(oracle, round(t * 1e6, 1), "us/forward",
                                               "full config 1 forward, median of 5")
+            check_parity("mlp_forward", model.execute(ins)[0].numpy(), want[0], 1e-4, 1e-7)
         defer(leg)
     out["mlp_forward"] = part
     log(f"mlp plan: {wall * 1e3:.1f} us/forward wall, {per.mean() * 1e3:.1f} us GPU")
@@ -354,7 +432,9 @@ def bench_backward(ca, oracle, args, out):
                 "bytes": nbytes, "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         if oracle is not None:
             def leg(name=name, part=part, nbytes=nbytes):
-                part["cpu_baseline"] = cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes)
+                part["cpu_baseline"], want = cpu_backward(oracle, name, y, dy, x, targets, a, b,
+                                                          nbytes)
+                backward_parity(ca, name, want, y, dy, x, targets, one, a, b)
             defer(leg)
         out[name] = part
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
@@ -423,7 +503,35 @@ def bench_backward(ca, oracle, args, out):
         f"peak), {per.mean():.3f} ms")
 
 
+def backward_parity(ca, name, want, y, dy, x, targets, one, a, b):
+    """The first input set's output of a backward part against the oracle's,
+    at the bound of that op's parity test."""
+    if name == "softmax_backward":
+        got = ca.softmax_backward(y, dy).numpy()
+        # the row sum s (summed in another order) reaches dx as y * ds
+        yh, dyh = y.numpy(), dy.numpy()
+        ds = 1e-5 * np.sum(np.abs(dyh * yh), axis=-1, keepdims=True)
+        err = np.abs(got.astype(np.float64) - want)
+        bad = ~(err <= 1e-4 * np.abs(want) + yh * ds + 1e-12)
+        PARITY[name] = "ok" if not bad.any() else f"{int(bad.sum())} elements out of bound"
+        log(f"parity {name}: {PARITY[name]}")
+        return
+    got, rtol, atol = {
+        "gelu_backward": (lambda: ca.gelu_backward(a, b), 1e-5, 2e-6),
+        # sums of 4096 unit normals, in another order than the oracle's
+        "broadcast_grad": (lambda: ca.broadcast_grad(a, 4096), 1e-4, np.sqrt(4096) * 1e-5),
+        "cross_entropy": (lambda: ca.cross_entropy(x, targets), 1e-4, 0.0),
+        "cross_entropy_backward": (lambda: ca.cross_entropy_backward(x, targets, one), 1e-4,
+                                   1e-10),
+        "mse": (lambda: ca.mse(a, b), 1e-4, 0.0),
+        "mse_backward": (lambda: ca.mse_backward(a, b, one), 1e-6, 1e-30),
+    }[name]
+    got = got().numpy()
+    check_parity(name, got, np.asarray(want).reshape(got.shape), rtol, atol)
+
+
 def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
+    """(cpu_baseline record, the oracle's output) of one backward part."""
     if name in ("softmax_backward", "cross_entropy", "cross_entropy_backward"):
         th = targets.numpy()
         if name == "softmax_backward":
@@ -433,7 +541,8 @@ def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
             xs = x.numpy()
             fn = (lambda: oracle.cross_entropy(xs, th)) if name == "cross_entropy" else \
                 (lambda: oracle.cross_entropy_backward(xs, th, 1.0))
-        t = cpu_time(fn)
+        want = []
+        t = cpu_time(fn, keep=want)
         sample = "full [8192, 4096] workload, median of 3"
     else:
         ah, bh = a.numpy(), b.numpy()
@@ -441,9 +550,10 @@ def cpu_backward(oracle, name, y, dy, x, targets, a, b, nbytes):
               "broadcast_grad": lambda: oracle.bias_grad(ah, 4096),
               "mse": lambda: oracle.mse(ah, bh),
               "mse_backward": lambda: oracle.mse_backward(ah, bh, 1.0)}[name]
-        t = cpu_time(fn)
+        want = []
+        t = cpu_time(fn, keep=want)
         sample = "full [4096, 4096] workload, median of 3"
-    return cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s", sample)
+    return cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s", sample), want[0]
 
 
 def bench_attention(ca, oracle, args, out):
@@ -508,6 +618,7 @@ PART_KERNELS = {
     "layer_norm": ["layer_norm_wave_kernel<16>"],
     "matmul_skinny_32": ["gemm_strip_kernel<16, false, true>"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
+    "paged_decode_d96": ["paged_general_kernel<8, 3, true>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
     "broadcast_grad": ["bcast_grad_strip_kernel"],
@@ -541,7 +652,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--parts", default="all",
-                    help="comma list of copy,bcast,rows,matmul,paged,mlp,backward,attention or "
+                    help="comma list of copy,bcast,rows,matmul,paged,mlp,backward,attention "
+                         "(skinny: only matmul's 32x4096x4096 product) or "
                          "'all' / "
                          "'none' "
                          "(the config 2 chain always runs)")
@@ -598,10 +710,12 @@ def main():
     if oracle is not None:
         def leg():
             host = [ins[i].numpy() for i in range(4)]
-            t = cpu_time(cpu_chain(oracle, host))
+            want = []
+            t = cpu_time(cpu_chain(oracle, host), keep=want)
             result["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
                                                 "full config 2 workload, 4 unfused passes "
                                                 "(Clove's eager CPU path), median of 3")
+            check_parity("chain", ca.FusedChain(CHAIN, ins)()[0].numpy(), want[0], 1e-5, 1e-6)
         defer(leg)
 
     out = {}
@@ -628,11 +742,24 @@ def main():
                                   "ms": round(bper.mean(), 4), "bytes": bbytes,
                                   "roofline": roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s")}
         log(f"chain broadcast: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})")
+        if oracle is not None:
+            def bleg(bins=bins, part=out["chain_broadcast"], bbytes=bbytes):
+                host = [bins[i].numpy() for i in range(4)]
+                want = []
+                t = cpu_time(cpu_chain(oracle, host), keep=want)
+                part["cpu_baseline"] = cpu_record(oracle, round(bbytes / t / 1e9, 2), "GB/s",
+                                                  "full broadcast workload, 4 unfused passes, "
+                                                  "median of 3")
+                check_parity("chain_broadcast", ca.FusedChain(CHAIN, bins)()[0].numpy(), want[0],
+                             1e-5, 1e-6)
+            defer(bleg)
         del bins
     if "rows" in parts:
         bench_rows(ca, oracle, args, out)
     if "matmul" in parts:
         bench_matmul(ca, oracle, args, out)
+    elif "skinny" in parts:
+        bench_matmul(ca, None, args, out, skinny_only=True)
     if "paged" in parts:
         bench_paged(ca, oracle, args, out)
     if "mlp" in parts:
@@ -649,7 +776,19 @@ def main():
         add_part_traffic(out, args.traffic)
         result["parts"] = out
     ca.synchronize()
+    failed = sorted(k for k, v in PARITY.items() if v != "ok")
+    if oracle is None:
+        result["parity_checked"] = False
+    elif failed:
+        result["parity_checked"] = {"failed": {k: PARITY[k] for k in failed},
+                                    "passed": sorted(k for k in PARITY if k not in failed)}
+    else:
+        result["parity_checked"] = True
+        result["parity_parts"] = sorted(PARITY)
     print(json.dumps(result), flush=True)
+    if failed:
+        log("bench.py: outputs out of their parity bound: " + ", ".join(failed))
+        sys.exit(1)
 
 
 if __name__ == "__main__":

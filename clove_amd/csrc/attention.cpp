@@ -109,7 +109,10 @@ void HipBackend::flash_attention_into(const Tensor &q, const Tensor &k, const Te
                   "flash_attention: num_heads must divide the last dimension");
     const int D = (int)(X / (size_t)num_heads);
     CLOVE_REQUIRE(k::attention_supported(D), CLOVE_HIP_ERR_SHAPE,
-                  "flash_attention: head_dim " + std::to_string(D) + " (64 and 128 have kernels)");
+                  "flash_attention: head_dim " + std::to_string(D) + " (1.." +
+                      std::to_string(k::kAttnMaxHeadDim) + " have kernels)");
+    CLOVE_REQUIRE(!(flags & CLOVE_ATTN_ROPE) || D % 2 == 0, CLOVE_HIP_ERR_SHAPE,
+                  "flash_attention: RoPE needs an even head_dim");
     CLOVE_REQUIRE((flags & ~(CLOVE_ATTN_CAUSAL | CLOVE_ATTN_ROPE)) == 0, CLOVE_HIP_ERR_INVALID,
                   "flash_attention: unknown flag");
     CLOVE_REQUIRE(q_pos >= 0 && k_pos >= 0 && mask_q >= 0 && mask_k >= 0,
@@ -125,31 +128,41 @@ void HipBackend::flash_attention_into(const Tensor &q, const Tensor &k, const Te
     CLOVE_REQUIRE(B * (size_t)num_heads * ((S + 127) / 128) * 256 < (1ull << 32),
                   CLOVE_HIP_ERR_SHAPE, "flash_attention: too many query blocks for one grid");
     CLOVE_REQUIRE(out.numel >= q.numel, CLOVE_HIP_ERR_SHAPE, "flash_attention: output too small");
-    CLOVE_REQUIRE(aligned16(q.data) && aligned16(k.data) && aligned16(v.data) &&
-                      aligned16(out.data),
+    // 16-byte pieces when D % 4 == 0 (every row then starts 16-byte aligned),
+    // single floats otherwise
+    const bool vec4 = D % 4 == 0;
+    CLOVE_REQUIRE(!vec4 || (aligned16(q.data) && aligned16(k.data) && aligned16(v.data) &&
+                            aligned16(out.data)),
                   CLOVE_HIP_ERR_INVALID, "flash_attention: q, k, v must be 16-byte aligned");
     if (q.numel == 0) return;
     const float sc = scale > 0.0f ? scale : 1.0f / sqrtf((float)D);
     hipStream_t s = ctx().stream;
-    const float *kp = k.f32();
-    TensorNode kr, tab;
+    const float *kp = k.f32(), *qp = q.f32();
+    TensorNode kr, qr, tab;
     int t0 = 0;
     if (flags & CLOVE_ATTN_ROPE) {
         // k is rotated in one pass (every query block stages the same keys);
         // q is rotated inside the kernel, once per query, from the same table
+        // (in a pass of its own too when rows move as single floats)
         const int p0 = std::min(q_pos, k_pos);
         const int p1 = (int)std::max((size_t)q_pos + S, (size_t)k_pos + Sk);
         tab = rope_table_for(p0, p1 - p0, D, &t0);
         kr = new_tensor(k.shape, CLOVE_HIP_F32);
         k::rope_apply(kp, kr->f32(), B * Sk, (int)Sk, (int)X, D, k_pos, tab->f32(), t0, s);
         kp = kr->f32();
+        if (!vec4) {
+            qr = new_tensor(q.shape, CLOVE_HIP_F32);
+            k::rope_apply(qp, qr->f32(), B * S, (int)S, (int)X, D, q_pos, tab->f32(), t0, s);
+            qp = qr->f32();
+        }
     }
     // The kernel reads query s's table row at s + (its q_pos) - (its
     // tab_pos0); passing the mask offset as its q_pos and shifting the table
     // origin by the difference keeps that row at s + q_pos.
-    k::attention_prefill(q.f32(), kp, v.f32(), out.f32(), (int)B, (int)S, (int)Sk, num_heads, D,
+    const bool q_tab = tab != nullptr && vec4;
+    k::attention_prefill(qp, kp, v.f32(), out.f32(), (int)B, (int)S, (int)Sk, num_heads, D,
                          mask_q, mask_k, (flags & CLOVE_ATTN_CAUSAL) != 0, sc,
-                         tab ? tab->f32() : nullptr, t0 - (q_pos - mask_q), s);
+                         q_tab ? tab->f32() : nullptr, t0 - (q_pos - mask_q), s);
 }
 
 TensorNode HipBackend::flash_attention(const TensorNode &q_, const TensorNode &k_,

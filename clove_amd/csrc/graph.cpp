@@ -366,6 +366,13 @@ Model::Model(const Graph &g, const std::vector<int> &outs) : nodes(g.nodes), inp
         if (nodes[q].shape.size() != 2 || nodes[kx].shape.size() != 2 ||
             nodes[v].shape.size() != 2)
             continue;
+        // whole heads only: a RoPE over a hidden size with a partial last head
+        // zeroes that head's dims, which the fused step would not reproduce
+        auto whole_heads = [&](int id) {
+            const SymExpr &x = *nodes[id].shape[1];
+            return x.kind == SymExpr::CONST && x.value > 0 && x.value % hd == 0;
+        };
+        if (!whole_heads(q) || !whole_heads(kx) || !whole_heads(v)) continue;
         if (smul >= 0 && !(scale > 0.f)) continue;  // the kernel needs a positive scale
         Step st;
         st.kind = Step::ATTENTION;

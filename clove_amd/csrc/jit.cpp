@@ -18,12 +18,14 @@
 //   - indices are 64-bit and vectorised; the reference dispatches one thread
 //     per element with 32-bit indices and a `%` per operand per element.
 #include <hip/hiprtc.h>
+#include <fcntl.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <random>
 #include <sstream>
 #include <unordered_map>
 
@@ -197,12 +199,17 @@ int g_compiles = 0, g_disk_loads = 0;
 // $XDG_CACHE_HOME/clove_hip or $HOME/.cache/clove_hip, so a new process
 // loads it instead of running hipRTC again (tens to hundreds of ms per
 // chain).  The file holds the whole key -- generated source, the embedded
-// headers, the compile options and the hipRTC version -- and is used only if
-// that key matches exactly, so a changed library or toolchain never loads a
-// stale object.  Files are written to a temporary name and renamed, so a
-// reader never sees a partial one; any failure to read, load or write just
+// headers, the compile options and the hipRTC, HIP runtime and driver
+// versions -- and is used only if that key matches exactly, so a changed
+// library or toolchain never loads a stale object.  A 64-bit checksum of the
+// code bytes catches a damaged file.  Only a regular file owned by this user
+// and writable by no one else is read, and it is opened without following
+// symbolic links, so a file another user planted in a shared directory is
+// never loaded.  New directories are created 0700; files are written to a
+// fresh temporary name (O_EXCL, random suffix, 0600) and renamed, so a
+// reader never sees a partial one.  Any failure to read, load or write just
 // means compiling.
-const char kCacheMagic[8] = {'C', 'L', 'V', 'J', 'I', 'T', '0', '1'};
+const char kCacheMagic[8] = {'C', 'L', 'V', 'J', 'I', 'T', '0', '2'};
 
 std::string cache_dir() {
     const char *v = std::getenv("CLOVE_JIT_CACHE");
@@ -216,56 +223,91 @@ std::string cache_dir() {
 }
 
 std::string cache_key(const std::string &src) {
-    int maj = 0, min = 0;
+    int maj = 0, min = 0, rt = 0, drv = 0;
     hiprtcVersion(&maj, &min);
+    (void)hipRuntimeGetVersion(&rt);
+    (void)hipDriverGetVersion(&drv);
     std::string k = src;
     for (const char *h : {kAbiSrc, kDeviceSrc, kKernelSrc}) k += std::string("\x01") + h;
     for (int i = 0; i < kNumRtcOpts; ++i) k += std::string("\x02") + kRtcOpts[i];
-    k += "\x03hiprtc " + std::to_string(maj) + "." + std::to_string(min);
+    k += "\x03hiprtc " + std::to_string(maj) + "." + std::to_string(min) + " runtime " +
+         std::to_string(rt) + " driver " + std::to_string(drv) + " arch " + ctx().arch;
     return k;
 }
 
+uint64_t fnv1a(const char *p, size_t n) {
+    uint64_t h = 1469598103934665603ull;
+    for (size_t i = 0; i < n; ++i) h = (h ^ (unsigned char)p[i]) * 1099511628211ull;
+    return h;
+}
+
 std::string cache_path(const std::string &dir, const std::string &key) {
-    uint64_t h = 1469598103934665603ull;  // FNV-1a
-    for (unsigned char c : key) h = (h ^ c) * 1099511628211ull;
     char name[32];
-    std::snprintf(name, sizeof(name), "%016llx.co", (unsigned long long)h);
+    std::snprintf(name, sizeof(name), "%016llx.co",
+                  (unsigned long long)fnv1a(key.data(), key.size()));
     return dir + "/" + name;
 }
 
+bool read_all(int fd, void *dst, size_t n) {
+    char *p = static_cast<char *>(dst);
+    while (n) {
+        const ssize_t r = read(fd, p, n);
+        if (r <= 0) return false;
+        p += r;
+        n -= (size_t)r;
+    }
+    return true;
+}
+
+bool write_all(int fd, const void *src, size_t n) {
+    const char *p = static_cast<const char *>(src);
+    while (n) {
+        const ssize_t r = write(fd, p, n);
+        if (r <= 0) return false;
+        p += r;
+        n -= (size_t)r;
+    }
+    return true;
+}
+
 bool cache_read(const std::string &path, const std::string &key, std::vector<char> *code) {
-    FILE *f = std::fopen(path.c_str(), "rb");
-    if (!f) return false;
+    const int fd = open(path.c_str(), O_RDONLY | O_NOFOLLOW | O_CLOEXEC);
+    if (fd < 0) return false;
+    struct stat st;
+    bool ok = fstat(fd, &st) == 0 && S_ISREG(st.st_mode) && st.st_uid == geteuid() &&
+              (st.st_mode & (S_IWGRP | S_IWOTH)) == 0;
     char magic[8];
-    uint64_t klen = 0, clen = 0;
-    bool ok = std::fread(magic, 1, 8, f) == 8 && !std::memcmp(magic, kCacheMagic, 8) &&
-              std::fread(&klen, 8, 1, f) == 1 && klen == key.size();
+    uint64_t klen = 0, clen = 0, sum = 0;
+    ok = ok && read_all(fd, magic, 8) && !std::memcmp(magic, kCacheMagic, 8) &&
+         read_all(fd, &klen, 8) && klen == key.size();
     if (ok) {
         std::string k(klen, '\0');
-        ok = std::fread(&k[0], 1, klen, f) == klen && k == key && std::fread(&clen, 8, 1, f) == 1 &&
-             clen > 0 && clen < (256u << 20);
+        ok = read_all(fd, &k[0], klen) && k == key && read_all(fd, &clen, 8) && clen > 0 &&
+             clen < (256u << 20) && read_all(fd, &sum, 8);
         if (ok) {
             code->resize(clen);
-            ok = std::fread(code->data(), 1, clen, f) == clen;
+            ok = read_all(fd, code->data(), clen) && fnv1a(code->data(), clen) == sum;
         }
     }
-    std::fclose(f);
+    close(fd);
     return ok;
 }
 
 void cache_write(const std::string &dir, const std::string &path, const std::string &key,
                  const std::vector<char> &code) {
     for (size_t i = 1; i <= dir.size(); ++i)  // mkdir -p
-        if (i == dir.size() || dir[i] == '/') (void)mkdir(dir.substr(0, i).c_str(), 0755);
-    const std::string tmp = path + ".tmp" + std::to_string((long)getpid());
-    FILE *f = std::fopen(tmp.c_str(), "wb");
-    if (!f) return;
-    const uint64_t klen = key.size(), clen = code.size();
-    const bool ok = std::fwrite(kCacheMagic, 1, 8, f) == 8 && std::fwrite(&klen, 8, 1, f) == 1 &&
-                    std::fwrite(key.data(), 1, klen, f) == klen &&
-                    std::fwrite(&clen, 8, 1, f) == 1 &&
-                    std::fwrite(code.data(), 1, clen, f) == clen;
-    if (std::fclose(f) != 0 || !ok || std::rename(tmp.c_str(), path.c_str()) != 0)
+        if (i == dir.size() || dir[i] == '/') (void)mkdir(dir.substr(0, i).c_str(), 0700);
+    std::random_device rd;
+    char suffix[40];
+    std::snprintf(suffix, sizeof(suffix), ".tmp%ld.%08x%08x", (long)getpid(), rd(), rd());
+    const std::string tmp = path + suffix;
+    const int fd = open(tmp.c_str(), O_WRONLY | O_CREAT | O_EXCL | O_NOFOLLOW | O_CLOEXEC, 0600);
+    if (fd < 0) return;
+    const uint64_t klen = key.size(), clen = code.size(), sum = fnv1a(code.data(), clen);
+    const bool ok = write_all(fd, kCacheMagic, 8) && write_all(fd, &klen, 8) &&
+                    write_all(fd, key.data(), klen) && write_all(fd, &clen, 8) &&
+                    write_all(fd, &sum, 8) && write_all(fd, code.data(), clen);
+    if (close(fd) != 0 || !ok || std::rename(tmp.c_str(), path.c_str()) != 0)
         (void)std::remove(tmp.c_str());
 }
 

@@ -9,9 +9,11 @@
 // batched, multi-head, causal and RoPE as flags, an exact exp, any length.
 //
 // Head dim 128: one workgroup = 4 waves = 128 queries of one (batch, head);
-// each wave owns 32 queries (head dim 64 runs attention16_kernel below:
-// 16-query waves on the 16x16x4 MFMA, the same scheme otherwise).  Key blocks of 32 are staged through LDS (double-buffered, one
-// barrier per block).  RoPE is applied before the kernel, once per element
+// each wave owns 32 queries (head dim 64 runs attention16_kernel of
+// attention16.h: 16-query waves on the 16x16x4 MFMA, the same scheme
+// otherwise; every other head dim runs that kernel from
+// attention_general.hip).  Key blocks of 32 are staged through LDS
+// (double-buffered, one barrier per block).  RoPE is applied before the kernel, once per element
 // (a rotation inside it would be repeated by every query block that stages
 // the same keys).  The products run on
 // v_mfma_f32_32x32x2_f32 in TRANSPOSED form:
@@ -40,6 +42,7 @@
 #include <cmath>
 #include <cstdint>
 
+#include "attention16.h"
 #include "launch.hpp"
 #include "wave.h"
 
@@ -49,21 +52,6 @@ namespace k {
 namespace {
 
 typedef float f16v __attribute__((ext_vector_type(16)));
-
-constexpr int kBQ = 128;  // queries per workgroup (4 waves x 32)
-constexpr int kBK = 32;   // keys per block
-
-struct AttnArgs {
-    const float *q, *k, *v;
-    float *out;
-    int B, S, Sk, H;
-    int q_pos, k_pos;
-    float scale;
-    int nqb;        // query blocks per (batch, head)
-    const float2 *rope_tab;  // (cos, sin) per (position, pair) to rotate q, or null
-    int tab_pos0;            // position of rope_tab's first row
-};
-
 
 template <int D, bool CAUSAL>
 __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
@@ -295,208 +283,15 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
         }
 }
 
-// Head dim 64: 16-query waves on v_mfma_f32_16x16x4_f32, 8 waves = 128
-// queries per workgroup, the K and V tiles shared by all of them.  Half the
-// accumulators and Q registers of the 32-query form (77 VGPRs at D = 64),
-// so three workgroups share a CU: six waves per SIMD to cover one another's
+// Head dim 64 runs attention16_kernel (attention16.h): 16-query waves on
+// v_mfma_f32_16x16x4_f32, 8 waves = 128 queries per workgroup.  Half the
+// accumulators and Q registers of the 32-query form (77 VGPRs at D = 64), so
+// three workgroups share a CU: six waves per SIMD to cover one another's
 // softmax and LDS waits.  Measured at B = 1, S = 4096, H = 32, causal +
 // RoPE: 0.595-0.600 ms against 0.672-0.673 ms for attention_kernel<64>
 // (results within 1e-6 relative of it; the sums run in another order).  At
 // D = 128 (120 VGPRs, four waves per SIMD) it ran within 2% of
 // attention_kernel<128> either way and is not used there.
-// Lane (r, q) = (l % 16, l / 16) works for query r of its wave:
-//   S^T = K . Q^T per 16-key half hk, step (g, t) pairing K[hk*16 + r][16g +
-//   4q + t] with Q[r][16g + 4q + t] (one 16-byte read of K per g);
-//   element i of S^T half hk is key hk*16 + 4q + i of query r;
-//   O^T += V^T . P^T, step (hk, i) pairing V[hk*16 + 4q + i][16jd + r] with
-//   the lane's own P element i: no shuffles; element e of O^T block jd is
-//   dim 16jd + 4q + e of query r.
-template <int D, bool CAUSAL>
-__global__ void __launch_bounds__(512, 4) attention16_kernel(AttnArgs a) {
-    // pitches measured conflict-free (SQ_LDS_BANK_CONFLICT 0): a K read takes
-    // 16 rows x two 16-byte slots, a PV step 4 rows x 16 floats; D + 4 for
-    // both cost 34 M conflict cycles per launch at D = 128
-    constexpr int kPK = D + 8;
-    constexpr int kPV = D + 4;
-    constexpr int kG = D / 16;  // 16-dim groups of QK^T = 16-dim blocks of O^T
-    constexpr int kVec = kBK * D / 4 / 512;  // 16-byte tile loads per thread (K and V each)
-    static_assert(kVec >= 1, "tile smaller than the workgroup");
-    __shared__ __attribute__((aligned(16))) float sK[2][kBK * kPK];
-    __shared__ __attribute__((aligned(16))) float sV[2][kBK * kPV];
-
-    const int L = blockIdx.x;
-    const int BH = a.B * a.H;
-    const int qb = a.nqb - 1 - L / BH;
-    const int bh = L % BH;
-    const int h = bh % a.H, b = bh / a.H;
-
-    const int HD = a.H * D;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r16 = lane & 15, q4 = lane >> 4;
-    const int q0 = qb * kBQ;
-    const int qw0 = q0 + 16 * wave;
-    const int query = qw0 + r16;
-    const bool q_ok = query < a.S;
-    const float *qrow = a.q + ((size_t)b * a.S + (q_ok ? query : 0)) * HD + (size_t)h * D;
-    const float2 *trow = a.rope_tab && q_ok
-                             ? a.rope_tab + (size_t)(query + a.q_pos - a.tab_pos0) * (D / 2)
-                             : nullptr;
-    const float qscale = a.scale * 1.44269504088896341f;
-    cl_f4 qf[kG];
-#pragma unroll
-    for (int g = 0; g < kG; ++g) {
-        cl_f4 v = q_ok ? *reinterpret_cast<const cl_f4 *>(qrow + 16 * g + 4 * q4)
-                       : (cl_f4){0.f, 0.f, 0.f, 0.f};
-        if (trow) {
-            const float2 t0 = trow[8 * g + 2 * q4], t1 = trow[8 * g + 2 * q4 + 1];
-            cl_f4 r;
-            r.x = v.x * t0.x - v.y * t0.y;
-            r.y = v.x * t0.y + v.y * t0.x;
-            r.z = v.z * t1.x - v.w * t1.y;
-            r.w = v.z * t1.y + v.w * t1.x;
-            v = r;
-        }
-        qf[g] = v * qscale;
-    }
-
-    int k_end = a.Sk;
-    if (CAUSAL) {
-        const int last = min(q0 + kBQ - 1, a.S - 1) + a.q_pos - a.k_pos;
-        k_end = min(k_end, last + 1);
-    }
-    int k_wave = a.Sk;
-    if (CAUSAL) k_wave = min(k_wave, min(qw0 + 15, a.S - 1) + a.q_pos - a.k_pos + 1);
-    const int nblk = k_end > 0 ? (k_end + kBK - 1) / kBK : 0;
-
-    constexpr uint32_t kOutside = 0x80000000u;  // the host keeps Sk*H*D*4 < 2^31
-    const uint32_t kv_bytes = (uint32_t)a.Sk * (uint32_t)HD * 4u;
-    const __amdgpu_buffer_rsrc_t rsrc_k = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(a.k + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float *>(a.v + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
-    cl_f4 rk[kVec], rv[kVec];
-    auto load_tile = [&](int kb) {
-#pragma unroll
-        for (int i = 0; i < kVec; ++i) {
-            const int idx = threadIdx.x + 512 * i;
-            const int key = idx / (D / 4), dq = idx % (D / 4);
-            const int t = kb + key;
-            const uint32_t off =
-                t < a.Sk ? ((uint32_t)t * (uint32_t)HD + (uint32_t)(h * D + 4 * dq)) * 4u : kOutside;
-            rk[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off, 0, 0));
-            rv[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off, 0, 0));
-        }
-    };
-    auto store_tile = [&](int buf) {
-#pragma unroll
-        for (int i = 0; i < kVec; ++i) {
-            const int idx = threadIdx.x + 512 * i;
-            const int key = idx / (D / 4), dq = idx % (D / 4);
-            *reinterpret_cast<cl_f4 *>(&sK[buf][key * kPK + 4 * dq]) = rk[i];
-            *reinterpret_cast<cl_f4 *>(&sV[buf][key * kPV + 4 * dq]) = rv[i];
-        }
-    };
-
-    float m = -INFINITY, lsum = 0.0f;
-    cl_f4 o[kG];
-#pragma unroll
-    for (int j = 0; j < kG; ++j) o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-
-    if (nblk > 0) {
-        load_tile(0);
-        store_tile(0);
-    }
-    __syncthreads();
-    for (int blk = 0; blk < nblk; ++blk) {
-        const int kb = blk * kBK;
-        const int cur = blk & 1;
-        const bool more = blk + 1 < nblk;
-        if (more) load_tile(kb + kBK);
-
-        if (kb < k_wave) {
-            const float *K = sK[cur];
-            const float *V = sV[cur];
-            cl_f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
-            __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int g = 0; g < kG; ++g)
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk) {
-                    const cl_f4 kf =
-                        *reinterpret_cast<const cl_f4 *>(K + (16 * hk + r16) * kPK + 16 * g + 4 * q4);
-#pragma unroll
-                    for (int t = 0; t < 4; ++t)
-                        s[hk] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[t], qf[g][t], s[hk], 0, 0, 0);
-                }
-            __builtin_amdgcn_s_setprio(0);
-            bool full = kb + kBK <= a.Sk && qw0 + 16 <= a.S;
-            if (CAUSAL) full = full && kb + kBK - 1 + a.k_pos <= qw0 + a.q_pos;
-            float mloc = -INFINITY;
-            if (full) {
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[hk][i]);
-            } else {
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = kb + 16 * hk + 4 * q4 + i;
-                        bool ok = t < a.Sk && q_ok;
-                        if (CAUSAL) ok = ok && t + a.k_pos <= query + a.q_pos;
-                        s[hk][i] = ok ? s[hk][i] : -INFINITY;
-                        mloc = fmaxf(mloc, s[hk][i]);
-                    }
-            }
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-            mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-            constexpr float kSlack = 8.0f;
-            const bool grow = __any(mloc > m + kSlack);
-            if (grow) {
-                const float m_new = fmaxf(m, mloc);
-                const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
-                lsum *= alpha;
-#pragma unroll
-                for (int j = 0; j < kG; ++j) o[j] *= alpha;
-                m = m_new;
-            }
-            const float mz = m == -INFINITY ? 0.0f : m;
-            float ps = 0.0f;
-#pragma unroll
-            for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    s[hk][i] = __builtin_amdgcn_exp2f(s[hk][i] - mz);
-                    ps += s[hk][i];
-                }
-            ps += __shfl_xor(ps, 16, 64);
-            ps += __shfl_xor(ps, 32, 64);
-            lsum += ps;
-            __builtin_amdgcn_s_setprio(1);
-#pragma unroll
-            for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const float *vr = V + (16 * hk + 4 * q4 + i) * kPV + r16;
-#pragma unroll
-                    for (int jd = 0; jd < kG; ++jd)
-                        o[jd] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * jd], s[hk][i], o[jd], 0, 0, 0);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-        }
-        __builtin_amdgcn_s_setprio(0);
-        if (more) store_tile(cur ^ 1);
-        __syncthreads();
-    }
-
-    if (!q_ok) return;
-    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
-    float *orow = a.out + ((size_t)b * a.S + query) * HD + (size_t)h * D;
-#pragma unroll
-    for (int jd = 0; jd < kG; ++jd)
-        *reinterpret_cast<cl_f4 *>(orow + 16 * jd + 4 * q4) = o[jd] * inv;
-}
 
 // RoPE table: tab[p][j] = (cos, sin) of theta = (pos0 + p) / div[j], the
 // angle of pair j (dims 2j, 2j+1) at position pos0 + p (backend.rs:2818).
@@ -614,22 +409,24 @@ __global__ void __launch_bounds__(256) rope_pairs_kernel(const float *__restrict
 
 }  // namespace
 
-bool attention_supported(int head_dim) { return head_dim == 64 || head_dim == 128; }
+bool attention_supported(int head_dim) { return head_dim >= 1 && head_dim <= kAttnMaxHeadDim; }
 
 void attention_prefill(const float *q, const float *k, const float *v, float *out, int B, int S,
                        int Sk, int H, int D, int q_pos, int k_pos, bool causal, float scale,
                        const float *q_rope_tab, int tab_pos0, hipStream_t s) {
     if (B <= 0 || S <= 0 || H <= 0) return;
     AttnArgs a{q, k, v, out, B, S, Sk, H, q_pos, k_pos, scale, 0,
-               reinterpret_cast<const float2 *>(q_rope_tab), tab_pos0};
+               reinterpret_cast<const float2 *>(q_rope_tab), tab_pos0, D};
     a.nqb = (S + kBQ - 1) / kBQ;
     const unsigned grid = (unsigned)(B * H * a.nqb);
     if (D == 64) {
-        if (causal) attention16_kernel<64, true><<<grid, 512, 0, s>>>(a);
-        else attention16_kernel<64, false><<<grid, 512, 0, s>>>(a);
-    } else {
+        if (causal) attention16_kernel<64, true, false, true><<<grid, 512, 0, s>>>(a);
+        else attention16_kernel<64, false, false, true><<<grid, 512, 0, s>>>(a);
+    } else if (D == 128) {
         if (causal) attention_kernel<128, true><<<grid, 256, 0, s>>>(a);
         else attention_kernel<128, false><<<grid, 256, 0, s>>>(a);
+    } else {
+        attention_prefill_general(a, causal, grid, s);
     }
 }
 

@@ -439,6 +439,22 @@ constexpr int dma_stages(int BN) { return BN == 128 ? 2 : kDmaStages; }
 // expcnt left at their maxima, so they are not waited for).
 constexpr int vmcnt_imm(int n) { return 0x0F70 | (n & 15) | ((n >> 4) << 14); }
 
+// s_waitcnt until at most n vector-memory operations are outstanding, for an
+// n that is a constant once the caller's loops are unrolled (rounded down to
+// a multiple of 4 -- waiting for more is always safe -- and capped at 60).
+__device__ __forceinline__ void wait_vmem(int n) {
+    switch (n < 60 ? n / 4 : 15) {
+#define CLOVE_WAIT_VMEM(i) \
+    case i: __builtin_amdgcn_s_waitcnt(vmcnt_imm(4 * i)); break;
+        CLOVE_WAIT_VMEM(0) CLOVE_WAIT_VMEM(1) CLOVE_WAIT_VMEM(2) CLOVE_WAIT_VMEM(3)
+        CLOVE_WAIT_VMEM(4) CLOVE_WAIT_VMEM(5) CLOVE_WAIT_VMEM(6) CLOVE_WAIT_VMEM(7)
+        CLOVE_WAIT_VMEM(8) CLOVE_WAIT_VMEM(9) CLOVE_WAIT_VMEM(10) CLOVE_WAIT_VMEM(11)
+        CLOVE_WAIT_VMEM(12) CLOVE_WAIT_VMEM(13) CLOVE_WAIT_VMEM(14) CLOVE_WAIT_VMEM(15)
+#undef CLOVE_WAIT_VMEM
+        default: __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    }
+}
+
 // EDGE: tiles may reach past M or N, and K may end inside the last slab of
 // the last split.  Rows of A past M and columns of B past N (N % 4 == 0, so
 // a 16-byte piece is all in or all out) get the offset kOutside, past the
@@ -926,9 +942,10 @@ __global__ void __launch_bounds__(64 * W) gemm_skinny_kernel(GemmArgs g) {
 //    (no registers) that many chunks ahead, each DMA lane moving 16
 //    contiguous bytes of one row, and reads its MFMA operands from there.
 //    Within a chunk, 16-byte slot s of row r holds k-piece s ^ r, so the 16
-//    rows a read touches fall in different banks.  A group's LDS reads start
-//    after its first B register has arrived: loads complete in order, and
-//    the DMA of its chunk was issued before that B load.
+//    rows a read touches fall in different banks.  Group g + 1's A operands
+//    are read from LDS while group g's MFMAs run, after an explicit vmcnt
+//    wait that covers the DMA of its chunk (vector-memory operations
+//    complete in issue order).
 //  * Each strip starts its waves' chunk walks at a different offset
 //    (strip * 3 mod chunks): the workgroups of an XCD then read different k
 //    ranges of A at any moment instead of the same lines.
@@ -1031,26 +1048,55 @@ __global__ void __launch_bounds__(64 * kStripWaves) gemm_strip_kernel(GemmArgs g
         }
     };
     f4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    auto mma = [&](int g0, int d) {
-        // wait for this group's first B load: everything issued before it,
-        // including the DMA of its A chunk, has completed
-        asm volatile("" ::"v"(bq[d][0][0]) : "memory");
+    // A operands of two groups (slot g & 1): group g + 1's are read from LDS
+    // while group g's MFMAs run, so the LDS latency is hidden behind them
+    f4 aop[2][2];
+    auto read_a = [&](int g0) {
         const float *src = myring + ((g0 >> 1) % R) * CH + l16 * 64;
-        f4 a[2];
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             // lane (l16, q) covers k = 32 sg + 8q + 4h + (0..3) of the chunk
             const int piece = 8 * (g0 & 1) + 2 * q + h;
-            a[h] = *reinterpret_cast<const f4 *>(src + 4 * (piece ^ l16));
-        }
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t / 4][t % 4], bq[d][t][0], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t / 4][t % 4], bq[d][t][1], acc1, 0, 0, 0);
+            aop[g0 & 1][h] = *reinterpret_cast<const f4 *>(src + 4 * (piece ^ l16));
         }
     };
-    // chunk 0 first (the first B groups' waits cover it), then B, then the
-    // rest of the ring
+    auto mma = [&](int g0, int d) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            const float a = aop[g0 & 1][t / 4][t % 4];
+            acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq[d][t][0], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a, bq[d][t][1], acc1, 0, 0, 0);
+        }
+    };
+    // Issue order (the counts below follow from it; sched_barrier keeps the
+    // regions in order): prologue = DMA of chunk 0, the first D B groups, the
+    // DMA of chunks 1 .. R-1; region gi = B group gi + D and, for odd gi, the
+    // DMA of chunk gi/2 + R.  Before group g's A operands are read from LDS, an explicit
+    // vmcnt wait leaves outstanding only the vector-memory operations issued
+    // after the DMA of g's chunk (those operations, the LDS DMAs included,
+    // complete in issue order), so the read never sees a stale ring slot.
+    // The DMA went out several groups earlier, so the wait rarely stalls;
+    // the B operands are waited for register by register by the compiler,
+    // so a group's MFMAs start as its first loads arrive.
+    constexpr int kB = 8, kDma = 4;  // vector-memory instructions per B group / chunk DMA
+    auto dma_in = [&](int j) {       // DMA instructions of region j
+        return ((j & 1) && j / 2 + R < NCH) ? kDma : 0;
+    };
+    auto region = [&](int j) { return (j + D < G2 ? kB : 0) + dma_in(j); };
+    // operations issued after chunk c's DMA, up to the start of region gi
+    auto after_dma = [&](int c, int gi) {
+        int n = 0;
+        if (c < R) {
+            n = kDma * (R - 1 - c);
+            if (c == 0)
+                for (int g = 0; g < D && g < G2; ++g) n += kB;
+            for (int j = 0; j < gi; ++j) n += region(j);
+        } else {
+            // region 2(c - R) + 1 issued it; its own B loads may follow it
+            for (int j = 2 * (c - R) + 1; j < gi; ++j) n += region(j);
+        }
+        return n;
+    };
     dma(0);
 #pragma unroll
     for (int d = 0; d < D && d < G2; ++d) loadb(d, d);
@@ -1059,9 +1105,20 @@ __global__ void __launch_bounds__(64 * kStripWaves) gemm_strip_kernel(GemmArgs g
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int gi = 0; gi < G2; ++gi) {
+        // group gi + 1's A operands (group 0's too, on the first pass): its
+        // chunk's DMA must be complete; 63 or more later operations imply it
+        const int next = gi + 1 < G2 ? gi + 1 : gi;
+        const int n = after_dma(next >> 1, gi);
+        if (n < 63) wait_vmem(n);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        if (gi == 0) read_a(0);
+        if (gi + 1 < G2) read_a(gi + 1);
+        __builtin_amdgcn_sched_barrier(0);  // the reads go out before the MFMAs
         mma(gi, gi % D);
         if (gi + D < G2) loadb(gi + D, gi % D);
-        // the slot of chunk gi/2 is free once both its groups are multiplied
+        // the slot of chunk gi/2 is free: both its groups' operands are in
+        // registers (the MFMAs above waited for group gi's reads)
         if ((gi & 1) && gi / 2 + R < NCH) dma(gi / 2 + R);
         __builtin_amdgcn_sched_barrier(0);
     }

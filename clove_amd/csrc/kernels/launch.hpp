@@ -52,7 +52,11 @@ void ordered_sum(const float *x, size_t n, float sign, float div, float *out, hi
 void transpose(const float *in, float *out, size_t R, size_t C, hipStream_t s);
 
 // flash_attention.hip -- attention prefill and RoPE.  q [B, S, H*D], k, v
-// [B, Sk, H*D], out [B, S, H*D], all 16-byte aligned; D in {64, 128}.
+// [B, Sk, H*D], out [B, S, H*D]; D in [1, kAttnMaxHeadDim].  D 64 and 128
+// run fixed-shape kernels, every other D the general one; all four tensors
+// 16-byte aligned when D % 4 == 0, else 4-byte aligned with a null
+// q_rope_tab (the caller rotates q first).
+constexpr int kAttnMaxHeadDim = 256;
 bool attention_supported(int head_dim);
 // q_rope_tab: a (cos, sin) table (rope_table layout) whose rows cover
 // positions q_pos .. q_pos + S - 1 from tab_pos0, to rotate q inside the
@@ -187,7 +191,10 @@ hipError_t paged_scratch_address(float **ptr);
 size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max_ctx,
                               int part_tokens);
 int paged_part_tokens(int num_seqs, int num_heads, int capacity, int block_size, int num_cus);
-// Head dims 64/128/256 and block sizes 8/16/32 have kernels.
+// Head dims 64/128/256 with block sizes 8/16/32 run a fixed-shape kernel;
+// every other head_dim in [1, kPagedMaxHeadDim] and block size >= 1 runs
+// the general one.
+constexpr int kPagedMaxHeadDim = 1024;
 bool paged_supported(int head_dim, int block_size);
 void paged_attention(const PagedArgs &a, hipStream_t s);
 // row_floats = H * D (a multiple of 4); k_new/v_new are [B, row_floats].

@@ -401,6 +401,274 @@ __global__ void __launch_bounds__(64 * HPW) paged_heads_kernel(PagedArgs a) {
     }
 }
 
+// ---- General decode: any head_dim up to 1024, any block size ----------------
+//
+// The kernel above fixes head_dim and block size at compile time and reads
+// whole KV blocks per load step.  Clove's modules give head_dim = dim /
+// num_heads with no restriction (nn.rs:519, nn/attention.rs:47) and the lazy
+// plan takes it from q's last dimension (lazy.rs:2363-2371), so every other
+// shape runs here:
+//   * a token's head row (D floats) belongs to a group of L = 8 or 16
+//     adjacent lanes, so one wave load covers 64 / L tokens.  Lane c of a
+//     group holds NP pieces of four floats: piece j is floats 4Lj + 4c ..
+//     4Lj + 4c + 3 when D % 4 == 0 (one 16-byte load, VEC4), floats
+//     4Lj + c + L*e, e = 0..3, otherwise (four 4-byte loads).  (L, NP) is
+//     chosen per head dim to leave the fewest lanes idle (D = 96: L = 8,
+//     NP = 3, none idle); floats at or past D read as zero, so q . k and the
+//     output need no other mask.  q . k is summed over the group with DPP.
+//   * the workgroup's four waves (four heads of one sequence) walk the same
+//     tokens and share one LDS table of their physical rows, built kGenChunk
+//     tokens at a time from the block table (row = bt[t / bs] * bs + t % bs),
+//     so any block size costs one LDS read per token and partitions need not
+//     align with blocks.  The new token (t = ctx - 1 with k/v given) and
+//     tokens past the range or behind a bad table entry are marked in it.
+//   * tokens are folded TS * 64 / L at a time (one online-softmax step of the
+//     arithmetic of fold_block), two register buffers deep while both fit
+//     (NP <= 8, D <= 512), one buffer beyond.
+// A lane with no token loads the pool's first row (always inside it) and its
+// values are replaced by zero, so no load is conditional; a piece that can
+// reach past D (the last, or any when NP >= 8) has its address checked per
+// lane.
+constexpr int kGenChunk = 512;
+constexpr int kRowNone = -1;  // no token: past the range, or a bad table entry
+constexpr int kRowNew = -2;   // token ctx - 1 taken from k_new / v_new
+
+template <int L, int NP>
+struct GenShape {
+    static constexpr int T = 64 / L;  // tokens per wave load
+    // 4-token steps per fold: at most 64 floats of K and V per buffer and lane,
+    // at most 32 tokens per online-softmax step
+    static constexpr int TS0 = 8 / NP < 1 ? 1 : 8 / NP;
+    static constexpr int TS = TS0 * T > 32 ? 32 / T : TS0;
+    static constexpr bool PIPE = NP <= 8;
+};
+
+template <int L, int NP>
+struct GenRegs {
+    cl_f4 k[GenShape<L, NP>::TS][NP], v[GenShape<L, NP>::TS][NP];
+    bool in[GenShape<L, NP>::TS];
+};
+
+// Float index of piece j, component e, in lane c of its group.
+template <int L, bool VEC4>
+__device__ __forceinline__ int gen_float(int j, int e, int c) {
+    return VEC4 ? 4 * L * j + 4 * c + e : 4 * L * j + c + L * e;
+}
+
+// Loads the NP pieces of the row at `row` (null: no token) into `out`.
+template <int L, int NP, bool VEC4>
+__device__ __forceinline__ void gen_row(const float *row, const float *safe, int c, int D,
+                                        cl_f4 (&out)[NP]) {
+    const float *base = row ? row : safe;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+        // With NP < 8, general_plan picks (L, NP) only for head dims that
+        // leave fewer than L idle piece slots, so the pieces before the last
+        // are inside the row and only the last may pass D; with NP >= 8 more
+        // than one piece can, and every piece is checked.
+        const bool last = NP >= 8 || j == NP - 1;
+        if (VEC4) {
+            const int f = gen_float<L, true>(j, 0, c);
+            const bool use = !last || f < D;
+            const cl_f4 v = stream_load(use ? base + f : base);
+            out[j] = (row && use) ? v : (cl_f4){0.f, 0.f, 0.f, 0.f};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int f = gen_float<L, false>(j, e, c);
+                const bool use = !last || f < D;
+                const float v = __builtin_nontemporal_load(use ? base + f : base);
+                out[j][e] = (row && use) ? v : 0.0f;
+            }
+        }
+    }
+}
+
+// Sum over the L lanes of a group (every lane of the group gets it).
+template <int L>
+__device__ __forceinline__ float group_sum(float v) {
+    v += dpp<0xB1>(v);  // quad_perm [1,0,3,2]
+    v += dpp<0x4E>(v);  // quad_perm [2,3,0,1]
+    if (L >= 8) v += dpp<0x141>(v);   // row_half_mirror: quad q + quad q^1
+    if (L >= 16) v += dpp<0x140>(v);  // row_mirror: half h + half h^1
+    return v;
+}
+
+// Combines the token groups of the wave: every lane gets the max / sum over
+// the lanes with its index within the group.
+template <int L>
+__device__ __forceinline__ float groups_max(float v) {
+    if (L <= 4) v = fmaxf(v, dpp<0x124>(v));  // row_ror 4
+    if (L <= 8) v = fmaxf(v, dpp<0x128>(v));  // row_ror 8
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
+template <int L>
+__device__ __forceinline__ float groups_sum(float v) {
+    if (L <= 4) v += dpp<0x124>(v);
+    if (L <= 8) v += dpp<0x128>(v);
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+template <int L, int NP, bool VEC4>
+__global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
+    using Sh = GenShape<L, NP>;
+    constexpr int T = Sh::T, TS = Sh::TS;
+    __shared__ int rows_lds[kGenChunk];
+    const int part = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int H = a.num_heads, D = a.head_dim, BS = a.block_size;
+    const int h = blockIdx.x * 4 + wave;
+    const bool active = h < H;  // idle waves still take part in the barriers
+    const int grp = lane / L, c = lane % L;
+    const size_t head_off = ((size_t)b * H + (active ? h : 0)) * D;
+    const int ctx = clamp_ctx(a, b, part == 0 && threadIdx.x == 0);
+    const int t_begin = part * a.part_tokens;
+    if (t_begin >= ctx) {  // uniform over the workgroup
+        if (ctx == 0 && part == 0 && active)
+            for (int d = lane; d < D; d += 64) a.out[head_off + d] = 0.0f;
+        return;
+    }
+    const int t_end = min(t_begin + a.part_tokens, ctx);
+    const int n_parts = (ctx + a.part_tokens - 1) / a.part_tokens;
+    const int32_t *bt = a.block_tables + (size_t)b * a.max_blocks;
+    const size_t row_stride = (size_t)H * D;
+    const size_t h_off = (size_t)(active ? h : 0) * D;
+
+    cl_f4 q[NP], o[NP];
+    gen_row<L, NP, VEC4>(active ? a.q + head_off : nullptr, a.q, c, D, q);
+#pragma unroll
+    for (int j = 0; j < NP; ++j) o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
+    WaveState st{-INFINITY, 0.0f};
+
+    auto issue = [&](int t0, int cb, int ce, GenRegs<L, NP> &r) {
+#pragma unroll
+        for (int s = 0; s < TS; ++s) {
+            const int t = t0 + T * s + grp;
+            const int rw = t < ce ? rows_lds[t - cb] : kRowNone;
+            r.in[s] = rw != kRowNone;
+            const float *kp = nullptr, *vp = nullptr;
+            if (rw == kRowNew) {
+                kp = a.k_new + head_off;
+                vp = a.v_new + head_off;
+            } else if (rw >= 0) {
+                const size_t off = (size_t)rw * row_stride + h_off;
+                kp = a.k_cache + off;
+                vp = a.v_cache + off;
+            }
+            gen_row<L, NP, VEC4>(kp, a.k_cache, c, D, r.k[s]);
+            gen_row<L, NP, VEC4>(vp, a.k_cache, c, D, r.v[s]);
+        }
+    };
+    auto consume = [&](const GenRegs<L, NP> &r) {
+        float sc[TS];
+        float bm = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < TS; ++s) {
+            float d = dot4(q[0], r.k[s][0]);
+#pragma unroll
+            for (int j = 1; j < NP; ++j) d += dot4(q[j], r.k[s][j]);
+            d = group_sum<L>(d);
+            sc[s] = r.in[s] ? d * a.scale : -INFINITY;
+            bm = fmaxf(bm, sc[s]);
+        }
+        bm = groups_max<L>(bm);
+        const float m_new = fmaxf(st.m, bm);
+        const float alpha = (st.m == -INFINITY) ? 0.0f : fast_exp(st.m - m_new);
+        st.l *= alpha;
+#pragma unroll
+        for (int j = 0; j < NP; ++j) o[j] *= alpha;
+#pragma unroll
+        for (int s = 0; s < TS; ++s) {
+            const float p = r.in[s] ? fast_exp(sc[s] - m_new) : 0.0f;
+            st.l += p;
+#pragma unroll
+            for (int j = 0; j < NP; ++j) o[j] += p * r.v[s][j];
+        }
+        st.m = m_new;
+    };
+
+    const int64_t nb = a.num_blocks;
+    for (int cb = t_begin; cb < t_end; cb += kGenChunk) {
+        const int ce = min(cb + kGenChunk, t_end);
+        __syncthreads();  // every wave is done with the previous chunk's rows
+        for (int i = threadIdx.x; i < ce - cb; i += 256) {
+            const int t = cb + i;
+            int rw = kRowNone;
+            if (a.k_new != nullptr && t == ctx - 1) {
+                rw = kRowNew;
+            } else {
+                const int lb = t / BS;
+                const int64_t e = bt[lb];
+                if (e >= 0 && e < nb) {
+                    rw = (int)(e * BS + (t - lb * BS));
+                } else if (i == 0 || t - lb * BS == 0) {
+                    atomicOr(a.err_flag, kErrPagedRange);
+                }
+            }
+            rows_lds[i] = rw;
+        }
+        __syncthreads();
+        if (!active) continue;
+        constexpr int G = T * TS;  // tokens per fold
+        if (Sh::PIPE) {
+            GenRegs<L, NP> A, B;
+            int t0 = cb;
+            issue(t0, cb, ce, A);
+            for (; t0 + 2 * G < ce; t0 += 2 * G) {
+                issue(t0 + G, cb, ce, B);
+                consume(A);
+                issue(t0 + 2 * G, cb, ce, A);
+                consume(B);
+            }
+            if (t0 + G < ce) {
+                issue(t0 + G, cb, ce, B);
+                consume(A);
+                consume(B);
+            } else {
+                consume(A);
+            }
+        } else {
+            for (int t0 = cb; t0 < ce; t0 += G) {
+                GenRegs<L, NP> A;
+                issue(t0, cb, ce, A);
+                consume(A);
+            }
+        }
+    }
+    if (!active) return;
+    st.l = groups_sum<L>(st.l);
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[j][e] = groups_sum<L>(o[j][e]);
+    if (grp != 0) return;
+    if (n_parts == 1) {
+        const float inv = 1.0f / st.l;
+#pragma unroll
+        for (int j = 0; j < NP; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int f = gen_float<L, VEC4>(j, e, c);
+                if (f < D) a.out[head_off + f] = o[j][e] * inv;
+            }
+        return;
+    }
+    float *ws = a.partials + (((size_t)b * H + h) * a.max_parts + part) * (D + 2);
+#pragma unroll
+    for (int j = 0; j < NP; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int f = gen_float<L, VEC4>(j, e, c);
+            if (f < D) ws[f] = o[j][e];
+        }
+    if (c == 0) {
+        ws[D] = st.m;
+        ws[D + 1] = st.l;
+    }
+}
+
 // Merges the partitions of each (b, h) with the log-sum-exp rule:
 // out = sum_p O_p e^(M_p - M) / sum_p L_p e^(M_p - M).  One wave per (b, h);
 // sequences that fit one partition were written by the partition kernel.
@@ -538,9 +806,14 @@ hipError_t paged_scratch_address(float **ptr) {
     return e;
 }
 
-bool paged_supported(int head_dim, int block_size) {
+// Shapes the fixed-shape kernel (paged_heads_kernel) is built for.
+static bool paged_tuned(int head_dim, int block_size) {
     return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
            (block_size == 8 || block_size == 16 || block_size == 32);
+}
+
+bool paged_supported(int head_dim, int block_size) {
+    return head_dim >= 1 && head_dim <= kPagedMaxHeadDim && block_size >= 1;
 }
 
 // Partition length: long partitions stream best, but the grid should still
@@ -572,21 +845,87 @@ size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max
     return (size_t)num_seqs * num_heads * parts * (head_dim + 2);
 }
 
+// The general kernel's lane-group width L and pieces per lane NP for a head
+// dim: the instantiated (L, NP) that covers it with the fewest idle piece
+// slots (ties: the wider group).  D % 4 != 0 always takes L = 16.
+struct GenPlan {
+    int L, NP;
+};
+static GenPlan general_plan(int D) {
+    // No 4-lane groups: measured at the config-5 shape they streamed at
+    // 43-48% of HBM peak (D = 48, 80, 112), each load then touching 16
+    // cache lines, against 70-79% for 8- and 16-lane groups.
+    static const GenPlan vec4[] = {{16, 1}, {16, 2}, {16, 3}, {16, 4}, {16, 5}, {16, 6},
+                                   {16, 8}, {16, 12}, {16, 16}, {8, 1}, {8, 2}, {8, 3},
+                                   {8, 4}, {8, 5}, {8, 6}, {8, 7}};
+    static const int np16[] = {1, 2, 3, 4, 5, 6, 8, 12, 16};
+    if (D % 4 != 0) {
+        const int need = (D + 63) / 64;
+        for (int np : np16)
+            if (np >= need) return {16, np};
+        return {16, 16};
+    }
+    const int P = D / 4;
+    GenPlan best{16, 16};
+    int waste = 1 << 30;
+    for (const GenPlan &g : vec4) {
+        const int w = g.L * g.NP - P;
+        if (w >= 0 && w < waste) {  // the table lists wider groups first
+            waste = w;
+            best = g;
+        }
+    }
+    return best;
+}
+
 void paged_attention(const PagedArgs &a, hipStream_t s) {
     if (a.num_seqs <= 0 || a.num_heads <= 0) return;
     // Four heads per workgroup: measured at the benchmark shape, 2 heads
     // reached 79% and 8 heads 75-80% of HBM peak against 82% for 4.
     const dim3 grid((unsigned)((a.num_heads + 3) / 4), (unsigned)a.max_parts,
                     (unsigned)a.num_seqs);
+    // CLOVE_PAGED_GENERAL=1 sends every shape to the general kernel (tests
+    // and measurement of that kernel at the tuned shapes).
+    const char *force = std::getenv("CLOVE_PAGED_GENERAL");
+    const bool general = !paged_tuned(a.head_dim, a.block_size) || (force && *force == '1');
+    if (general) {
+        const GenPlan g = general_plan(a.head_dim);
+        const int key = g.L * 100 + g.NP;
+        if (a.head_dim % 4 != 0) {
+            switch (key) {
+#define CLOVE_PAGED_GEN1(L, NP)                                                    \
+    case L * 100 + NP: paged_general_kernel<L, NP, false><<<grid, 256, 0, s>>>(a); break;
+                CLOVE_PAGED_GEN1(16, 1) CLOVE_PAGED_GEN1(16, 2) CLOVE_PAGED_GEN1(16, 3)
+                CLOVE_PAGED_GEN1(16, 4) CLOVE_PAGED_GEN1(16, 5) CLOVE_PAGED_GEN1(16, 6)
+                CLOVE_PAGED_GEN1(16, 8) CLOVE_PAGED_GEN1(16, 12) CLOVE_PAGED_GEN1(16, 16)
+#undef CLOVE_PAGED_GEN1
+                default: return;
+            }
+        } else {
+            switch (key) {
+#define CLOVE_PAGED_GEN4(L, NP)                                                    \
+    case L * 100 + NP: paged_general_kernel<L, NP, true><<<grid, 256, 0, s>>>(a); break;
+                CLOVE_PAGED_GEN4(16, 1) CLOVE_PAGED_GEN4(16, 2) CLOVE_PAGED_GEN4(16, 3)
+                CLOVE_PAGED_GEN4(16, 4) CLOVE_PAGED_GEN4(16, 5) CLOVE_PAGED_GEN4(16, 6)
+                CLOVE_PAGED_GEN4(16, 8) CLOVE_PAGED_GEN4(16, 12) CLOVE_PAGED_GEN4(16, 16)
+                CLOVE_PAGED_GEN4(8, 1) CLOVE_PAGED_GEN4(8, 2) CLOVE_PAGED_GEN4(8, 3)
+                CLOVE_PAGED_GEN4(8, 4) CLOVE_PAGED_GEN4(8, 5) CLOVE_PAGED_GEN4(8, 6)
+                CLOVE_PAGED_GEN4(8, 7)
+#undef CLOVE_PAGED_GEN4
+                default: return;
+            }
+        }
+    } else {
 #define CLOVE_PAGED_CASE(D, BS)                                                     \
     if (a.head_dim == D && a.block_size == BS) {                                    \
         paged_heads_kernel<D, BS, 4><<<grid, 256, 0, s>>>(a);                       \
     } else
-    CLOVE_PAGED_CASE(64, 8) CLOVE_PAGED_CASE(64, 16) CLOVE_PAGED_CASE(64, 32)
-    CLOVE_PAGED_CASE(128, 8) CLOVE_PAGED_CASE(128, 16) CLOVE_PAGED_CASE(128, 32)
-    CLOVE_PAGED_CASE(256, 8) CLOVE_PAGED_CASE(256, 16) CLOVE_PAGED_CASE(256, 32)
-    { return; }
+        CLOVE_PAGED_CASE(64, 8) CLOVE_PAGED_CASE(64, 16) CLOVE_PAGED_CASE(64, 32)
+        CLOVE_PAGED_CASE(128, 8) CLOVE_PAGED_CASE(128, 16) CLOVE_PAGED_CASE(128, 32)
+        CLOVE_PAGED_CASE(256, 8) CLOVE_PAGED_CASE(256, 16) CLOVE_PAGED_CASE(256, 32)
+        { return; }
 #undef CLOVE_PAGED_CASE
+    }
     const int pairs = a.num_seqs * a.num_heads;
     if (a.max_parts > 1)
         paged_merge_kernel<<<(unsigned)((pairs + 3) / 4), 256, 0, s>>>(a);

@@ -371,10 +371,14 @@ static k::PagedArgs paged_args(const HipBackend::PagedRaw &r, size_t *ws) {
                   CLOVE_HIP_ERR_SHAPE, "context capacity exceeds 2^31 tokens");
     // grid: (head groups, partitions, sequences)
     CLOVE_REQUIRE(B < 65536, CLOVE_HIP_ERR_SHAPE, "at most 65535 sequences per launch");
-    auto aligned = [](const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    // 16-byte vector loads when head_dim % 4 == 0, 4-byte loads otherwise
+    const uintptr_t amask = D % 4 == 0 ? 15 : 3;
+    auto aligned = [amask](const void *p) { return (reinterpret_cast<uintptr_t>(p) & amask) == 0; };
     CLOVE_REQUIRE(aligned(r.q) && aligned(r.k_new) && aligned(r.v_new) && aligned(r.kv_cache) &&
                       aligned(r.out),
-                  CLOVE_HIP_ERR_INVALID, "q, k, v, kv_cache and out must be 16-byte aligned");
+                  CLOVE_HIP_ERR_INVALID,
+                  D % 4 == 0 ? "q, k, v, kv_cache and out must be 16-byte aligned"
+                             : "q, k, v, kv_cache and out must be 4-byte aligned");
     k::PagedArgs a{};
     a.q = r.q;
     a.k_new = r.k_new;
@@ -412,9 +416,10 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
                   "kv_cache must be [2, num_blocks, block_size, heads, head_dim], got " +
                       shape_str(kv.shape));
     const size_t nb = kv.shape[1], bs = kv.shape[2], H = kv.shape[3], D = kv.shape[4];
-    CLOVE_REQUIRE(k::paged_supported((int)D, (int)bs), CLOVE_HIP_ERR_SHAPE,
-                  "paged attention supports head_dim 64/128/256 and block_size 8/16/32, got " +
-                      std::to_string(D) + "/" + std::to_string(bs));
+    CLOVE_REQUIRE(k::paged_supported((int)std::min<size_t>(D, 1u << 30), (int)bs),
+                  CLOVE_HIP_ERR_SHAPE,
+                  "paged attention supports head_dim 1.." + std::to_string(k::kPagedMaxHeadDim) +
+                      " and block_size >= 1, got " + std::to_string(D) + "/" + std::to_string(bs));
     const size_t B = cl.numel;
     CLOVE_REQUIRE(bt.shape.size() == 2 && bt.shape[0] == B, CLOVE_HIP_ERR_SHAPE,
                   "block_tables must be [num_seqs, max_blocks] with num_seqs = numel(context_lens)");
@@ -451,15 +456,18 @@ void HipBackend::paged_attention_into(const Tensor &q, const Tensor *kn, const T
 // The allocation-free form: the caller's device memory, int32 indices, and
 // the partition workspace in this device's static scratch array.  Nothing
 // is allocated and nothing needs clearing (every partial the merge reads is
-// written by the same launch).  Launches on one GPU that overlap (different
-// streams) share the array and race.
+// written by the same launch).  Two calls never overlap: both run on the
+// library's current stream, and set_stream waits for the stream it
+// replaces; only replays of a captured call on two streams at once would
+// share the array concurrently (the caller orders those).
 void HipBackend::paged_attention_noalloc(const PagedRaw &r) {
     CLOVE_REQUIRE(r.num_seqs >= 0 && r.num_heads >= 1 && r.max_blocks >= 1 && r.num_blocks >= 1,
                   CLOVE_HIP_ERR_SHAPE,
                   "num_seqs >= 0, num_heads >= 1, max_blocks >= 1 and num_blocks >= 1 are required");
     CLOVE_REQUIRE(k::paged_supported(r.head_dim, r.block_size), CLOVE_HIP_ERR_SHAPE,
-                  "paged attention supports head_dim 64/128/256 and block_size 8/16/32, got " +
-                      std::to_string(r.head_dim) + "/" + std::to_string(r.block_size));
+                  "paged attention supports head_dim 1.." + std::to_string(k::kPagedMaxHeadDim) +
+                      " and block_size >= 1, got " + std::to_string(r.head_dim) + "/" +
+                      std::to_string(r.block_size));
     CLOVE_REQUIRE((r.k_new == nullptr) == (r.v_new == nullptr), CLOVE_HIP_ERR_INVALID,
                   "pass both k and v, or neither");
     if (r.num_seqs == 0) return;

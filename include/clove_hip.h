@@ -87,7 +87,8 @@ const char *clove_hip_last_error(void);
 int clove_hip_last_status(void);
 int clove_hip_synchronize(void);
 /* Use a caller-owned hipStream_t (passed as void*) for all later work;
- * NULL restores the library's own stream. */
+ * NULL restores the library's own stream.  Waits for the work already queued
+ * on the stream it replaces. */
 int clove_hip_set_stream(void *hip_stream);
 void *clove_hip_get_stream(void);
 /* Return cached free device blocks to the driver. */
@@ -177,8 +178,11 @@ CTensor clove_hip_matmul(CTensor a, CTensor b);       /* ffi.rs:134-137 */
  *   block_tables int32 [B, max_blocks] (nn.rs:535)
  *   context_lens int32 [B]
  * Returns out f32 with q's shape: out = softmax(q.K^T / sqrt(D)) V per
- * (sequence, head).  Fails with CLOVE_HIP_ERR_RANGE if a context length
- * exceeds max_blocks*block_size or a table entry used lies outside the pool. */
+ * (sequence, head).  Any head_dim D in 1..1024 and any block_size >= 1
+ * (head_dim = dim / num_heads is unrestricted in nn.rs:519); D 64/128/256
+ * with block sizes 8/16/32 run a fixed-shape kernel, the rest a general one.
+ * Fails with CLOVE_HIP_ERR_RANGE if a context length exceeds
+ * max_blocks*block_size or a table entry used lies outside the pool. */
 CTensor clove_hip_paged_attention(CTensor q, CTensor k, CTensor v, CTensor kv_cache,
                                   CTensor block_tables, CTensor context_lens);
 /* Same with an explicit softmax scale (the reference uses 1/sqrt(D),
@@ -195,13 +199,16 @@ CTensor clove_hip_paged_attention_scaled(CTensor q, CTensor k, CTensor v, CTenso
  *   k, v         f32 [num_seqs, num_heads*head_dim] new token, or both NULL
  *   kv_cache     f32 [2, num_blocks, block_size, num_heads, head_dim]
  *   block_tables int32 [num_seqs, max_blocks]; context_lens int32 [num_seqs]
- * all 16-byte aligned; scale is used as given.  The partition workspace
+ * all 16-byte aligned (4-byte when head_dim % 4 != 0); scale is used as given.  The partition workspace
  * (num_seqs*num_heads*partitions*(head_dim+2) floats when a context spans
  * more than one partition) lives in a static 16 MiB device array per GPU;
  * a shape needing more fails with CLOVE_HIP_ERR_SHAPE before any launch.
- * Nothing is allocated.  Calls on one GPU that overlap (on different
- * streams) share that array and race; calls on the library's one stream are
- * ordered.  Index errors are reported as by the other paged entries. */
+ * Nothing is allocated.  Calls made through this library never overlap:
+ * every call runs on the library's current stream, and clove_hip_set_stream
+ * waits for the stream it replaces.  Work that replays such a call outside
+ * the library (a captured graph launched on two streams at once) shares the
+ * array and races; the caller must order those replays.  Index errors are
+ * reported as by the other paged entries. */
 int clove_hip_paged_attention_noalloc(const float *q, const float *k, const float *v,
                                       const float *kv_cache, int64_t num_blocks, int block_size,
                                       int num_heads, int head_dim, const int32_t *block_tables,

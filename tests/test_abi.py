@@ -326,8 +326,12 @@ def test_plan_flash_attention_non_matches():
     q, k, v = g.input("64,128"), g.input("128,64"), g.input("64,128")
     y = g.op("matmul", g.op("softmax", g.op("matmul", g.rope(q, 64), k)), v)
     assert steps(g.compile([y])) == ["RoPE(0,64)", "MatMul+Softmax", "MatMul"]
-    # head_dim without an attention kernel (32)
-    g, _, y = attention_graph(D=32)
+    # every even head_dim up to 256 has an attention kernel (32, 80, 96 here)
+    for D in (32, 80, 96):
+        g, _, y = attention_graph(X=2 * D, D=D)
+        assert f"FlashAttention(q_pos=3,k_pos=5,head_dim={D},causal)" in g.compile([y]).describe()
+    # a hidden size that is not whole heads (RoPE zeroes the partial head)
+    g, _, y = attention_graph(X=160, D=96)
     assert "FlashAttention" not in g.compile([y]).describe()
     # the scores are requested too: they must be materialised
     g, _, y = attention_graph()

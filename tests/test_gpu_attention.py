@@ -58,6 +58,21 @@ CASES = [
     (1, 300, 700, 2, 64, 0, 0, 0),
     (2, 129, 513, 3, 128, 2, 0, 0),
     (1, 512, 512, 2, 128, 1, 0, 0),
+    # head dims without a fixed-shape kernel (the general one, tiles padded
+    # to the next multiple of 16 or 32): D % 4 == 0 with 16-byte pieces ...
+    (1, 130, 130, 2, 80, 3, 0, 0),
+    (2, 100, 257, 3, 96, 3, 157, 0),
+    (1, 200, 200, 2, 32, 1, 0, 0),
+    (1, 77, 140, 2, 112, 2, 0, 30),
+    (1, 129, 129, 2, 160, 3, 0, 0),
+    (1, 64, 64, 1, 256, 0, 0, 0),
+    (2, 50, 60, 3, 16, 3, 5, 0),
+    (1, 90, 90, 2, 200, 3, 0, 0),
+    # ... and single floats (D % 4 != 0; RoPE needs D even)
+    (1, 70, 70, 2, 50, 3, 0, 0),
+    (1, 45, 100, 3, 7, 1, 55, 0),
+    (2, 33, 33, 1, 130, 2, 0, 0),
+    (1, 20, 20, 2, 1, 0, 0, 0),
 ]
 
 
@@ -82,8 +97,12 @@ def test_flash_attention_2d_and_scale_and_errors(hip):
     # all keys in the future: zeros
     z = hip.flash_attention(tq, tk, tv, 1, q_pos=0, k_pos=100, flags=1).numpy()
     assert np.all(z == 0)
-    with pytest.raises(hip.CloveError):  # head_dim 32 has no kernel
-        hip.flash_attention(tq, tk, tv, 4)
+    x = hip.tensor(np.zeros((5, 300), np.float32))
+    with pytest.raises(hip.CloveError):  # head_dim above 256
+        hip.flash_attention(x, x, x, 1)
+    x = hip.tensor(np.zeros((5, 126), np.float32))
+    with pytest.raises(hip.CloveError):  # RoPE on an odd head_dim
+        hip.flash_attention(x, x, x, 2, flags=2)
     with pytest.raises(hip.CloveError):
         hip.flash_attention(tq, hip.tensor(k[:, :64]), tv, 1)
 
@@ -104,7 +123,10 @@ def test_flash_attention_prefill_4096_sampled(hip):
                                                           (2, 65, 200, 3, 64, 2, 135, 0),
                                                           (1, 300, 300, 1, 128, 3, 7, 7),
                                                           (1, 64, 300, 2, 128, 3, 236, 3),
-                                                          (2, 100, 333, 3, 64, 3, 400, 167)])
+                                                          (2, 100, 333, 3, 64, 3, 400, 167),
+                                                          (1, 140, 140, 2, 80, 3, 0, 0),
+                                                          (2, 65, 99, 3, 96, 3, 40, 6),
+                                                          (1, 70, 70, 2, 50, 3, 9, 9)])
 def test_attention_rope_equals_rope_then_attention(hip, B, S, Sk, H, D, flags, q_pos, k_pos):
     """The RoPE flag rotates k in a pass and q inside the kernel; both use the
     RoPE op's arithmetic and table, so the result equals rotating q and k with

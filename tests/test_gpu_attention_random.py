@@ -1,7 +1,8 @@
 """GPU parity: seeded random attention prefills against the oracle.
 
-Each case draws 1-3 batches, 1-4 heads, head_dim 64 or 128 (the two with
-kernels), 1-320 queries and 1-320 keys, every combination of the causal and
+Each case draws 1-3 batches, 1-4 heads, head_dim 64 or 128 (the fixed-shape
+kernels) or, for the general kernel, one of 16..256 including two that are
+not multiples of 4, 1-320 queries and 1-320 keys, every combination of the causal and
 RoPE flags, rotation positions q_pos / k_pos in [0, 300] (chunked prefill:
 query row i sits at q_pos + i and sees keys at k_pos + j <= q_pos + i), and
 the default scale 1/sqrt(D) or an explicit one.  Rows whose keys are all in
@@ -18,10 +19,11 @@ from conftest import assert_close, rng
 pytestmark = pytest.mark.gpu
 
 
-def random_prefill(seed):
+def random_prefill(seed, general=False):
     g = rng(seed)
     B, H = int(g.integers(1, 4)), int(g.integers(1, 5))
-    D = int(g.choice([64, 128]))
+    D = int(g.choice([16, 24, 32, 48, 80, 96, 104, 112, 144, 160, 192, 256, 50, 70])
+            if general else g.choice([64, 128]))
     S, Sk = int(g.integers(1, 321)), int(g.integers(1, 321))
     flags = int(g.integers(0, 4))
     q_pos, k_pos = int(g.integers(0, 301)), int(g.integers(0, 301))
@@ -32,8 +34,8 @@ def random_prefill(seed):
     return q, k, v, H, q_pos, k_pos, flags, scale
 
 
-def run_case(hip, seed):
-    q, k, v, H, q_pos, k_pos, flags, scale = random_prefill(seed)
+def run_case(hip, seed, general=False):
+    q, k, v, H, q_pos, k_pos, flags, scale = random_prefill(seed, general)
     got = hip.flash_attention(hip.tensor(q), hip.tensor(k), hip.tensor(v), H, q_pos, k_pos,
                               flags, scale).numpy()
     want = oracle.attention(q, k, v, H, q_pos, k_pos, flags, scale or None)
@@ -46,3 +48,8 @@ def run_case(hip, seed):
 @pytest.mark.parametrize("seed", range(24))
 def test_random_prefill(hip, seed):
     run_case(hip, 700 + seed)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_prefill_general_head_dims(hip, seed):
+    run_case(hip, 800 + seed, general=True)

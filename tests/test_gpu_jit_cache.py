@@ -3,8 +3,9 @@
 Each case runs fresh processes (the in-memory cache would hide the disk):
 the first compiles the chain with hipRTC and writes its code object, a
 later one loads it and compiles nothing, and both give the same bits.  A
-damaged file (its header, or a code object the runtime refuses) is ignored
-and rewritten; CLOVE_JIT_CACHE=0 writes nothing.
+damaged file (its header, or code bytes that fail the checksum), one that
+others may write, and one reached through a symbolic link are ignored and
+replaced; CLOVE_JIT_CACHE=0 writes nothing.
 """
 import os
 import subprocess
@@ -44,23 +45,39 @@ def test_chain_code_object_reused_across_processes(tmp_path):
     assert len(files) == 1 and not list(cache.glob("*.tmp*"))
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (0, 1) and again == first
+    assert (files[0].stat().st_mode & 0o777) == 0o600
+    assert (cache.stat().st_mode & 0o777) == 0o700
     # a damaged object is ignored: compiled again, rewritten, then reused
-    files[0].write_bytes(b"CLVJIT01 not a code object")
+    files[0].write_bytes(b"CLVJIT02 not a code object")
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (1, 0) and again == first
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (0, 1) and again == first
-    # the key matches but the code object is damaged: the runtime refuses
-    # it, so the chain is compiled again and the file rewritten
-    data = bytearray(files[0].read_bytes())
+    # the key matches but the code bytes are damaged: the checksum rejects
+    # them, so the chain is compiled again and the file rewritten
+    good = files[0].read_bytes()
+    data = bytearray(good)
     klen = int.from_bytes(data[8:16], "little")
-    code_at = 16 + klen + 8
-    data[code_at:] = bytes(len(data) - code_at)
+    code_at = 16 + klen + 16  # magic, key length, key, code length, checksum
+    data[code_at + 100] ^= 0x40
     files[0].write_bytes(bytes(data))
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (1, 0) and again == first
     compiled, loaded, again = run(env)
     assert (compiled, loaded) == (0, 1) and again == first
+    # a file others may write is never read (it may have been planted) ...
+    files[0].chmod(0o620)
+    compiled, loaded, again = run(env)
+    assert (compiled, loaded) == (1, 0) and again == first
+    assert (files[0].stat().st_mode & 0o777) == 0o600  # replaced by a private one
+    # ... nor one reached through a symbolic link
+    elsewhere = tmp_path / "planted.co"
+    elsewhere.write_bytes(good)
+    files[0].unlink()
+    files[0].symlink_to(elsewhere)
+    compiled, loaded, again = run(env)
+    assert (compiled, loaded) == (1, 0) and again == first
+    assert not files[0].is_symlink() and elsewhere.read_bytes() == good
 
 
 def test_cache_off_writes_nothing(tmp_path):

@@ -42,6 +42,78 @@ def test_head_dims_and_block_sizes(hip, D, bs):
     assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs}")
 
 
+# Head dims and block sizes without a fixed-shape kernel: the general kernel
+# (head_dim = dim / num_heads is unrestricted in nn.rs:519 and
+# nn/attention.rs:47; the lazy plan takes it from q, lazy.rs:2363-2371).
+@pytest.mark.parametrize("D", [32, 80, 96, 112, 160])
+@pytest.mark.parametrize("bs", [16, 64])
+def test_general_head_dims(hip, D, bs):
+    H, B = 3, 4
+    ctx = [1, bs + 1, 1500, 2600]
+    mb = 2600 // bs + 1
+    q, kn, vn, kv, bt, cl = make(1000 + D + bs, B, H, D, bs, B * mb + 2, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs} new token")
+    want = oracle.paged_attention(q, None, None, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs} cached")
+
+
+# Odd shapes: head dims not a multiple of 4 (4-byte loads), a head dim past
+# 512 (one register buffer), block sizes 1, 5 and 128, and more heads than a
+# multiple of the four per workgroup.
+@pytest.mark.parametrize("D,bs,H", [(1, 16, 2), (7, 5, 5), (50, 1, 3), (100, 24, 2),
+                                    (300, 128, 1), (520, 16, 2), (1024, 8, 1), (64, 48, 6)])
+def test_general_odd_shapes(hip, D, bs, H):
+    B = 3
+    ctx = [1, 777, 300]
+    mb = 777 // bs + 1
+    q, kn, vn, kv, bt, cl = make(2000 + D + bs, B, H, D, bs, B * mb + 1, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"D={D} bs={bs} H={H}")
+
+
+@pytest.mark.parametrize("D,bs", [(128, 16), (64, 8), (256, 32)])
+def test_general_kernel_at_fixed_shapes(hip, monkeypatch, D, bs):
+    # CLOVE_PAGED_GENERAL=1 sends a fixed shape to the general kernel: both
+    # must meet the bound, and partitions of 2048 tokens cover several LDS
+    # row chunks (512 tokens each)
+    H, B = 4, 3
+    ctx = [2049, 4096, 513]
+    mb = 4096 // bs
+    q, kn, vn, kv, bt, cl = make(3000 + D, B, H, D, bs, B * mb + 1, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    tuned = run(hip, q, kn, vn, kv, bt, cl)
+    monkeypatch.setenv("CLOVE_PAGED_GENERAL", "1")
+    general = run(hip, q, kn, vn, kv, bt, cl)
+    assert_close(tuned, want, RTOL, ATOL, "fixed-shape kernel")
+    assert_close(general, want, RTOL, ATOL, "general kernel")
+
+
+@pytest.mark.parametrize("part", [24, 1000, 2052])
+def test_general_partitions(hip, monkeypatch, part):
+    # partitions that end inside a block and inside an LDS row chunk
+    monkeypatch.setenv("CLOVE_PAGED_PART", str(part))
+    H, D, bs, B = 2, 96, 12, 3
+    ctx = [2053, 1000, 25]
+    mb = 2053 // bs + 1
+    q, kn, vn, kv, bt, cl = make(4000 + part, B, H, D, bs, B * mb + 3, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"part={part}")
+
+
+def test_general_bad_table_entry_is_reported_not_read(hip):
+    q, kn, vn, kv, bt, cl = make(8, 2, 2, 96, 16, 20, 4, [40, 40])
+    bt[1, 1] = 1 << 30
+    out = hip.paged_attention(hip.tensor(q), None, None, hip.tensor(kv), hip.tensor(bt),
+                              hip.tensor(cl))
+    with pytest.raises(hip.CloveError) as e:
+        hip.synchronize()
+    assert e.value.code == hip.ERR_RANGE
+    want = oracle.paged_attention(q[:1], None, None, kv, bt[:1], cl[:1]).reshape(1, 192)
+    assert_close(out.numpy()[:1], want, RTOL, ATOL, "unaffected sequence")
+    hip.synchronize()
+
+
 @pytest.mark.parametrize("D,bs,ctx", [(128, 16, [1, 2, 15, 16]), (128, 16, [17, 511, 512, 513]),
                                       (128, 16, [1024, 1535, 2049, 0]),
                                       (256, 32, [1, 16, 17, 32]), (256, 32, [33, 511, 512, 2049])])
@@ -106,8 +178,8 @@ def test_bad_table_entry_is_reported_not_read(hip):
 
 
 def test_shape_errors(hip):
-    q, kn, vn, kv, bt, cl = make(9, 2, 2, 48, 16, 20, 4, [5, 5])
-    with pytest.raises(hip.CloveError):  # head_dim 48 has no kernel
+    q, kn, vn, kv, bt, cl = make(9, 2, 1, 1025, 16, 20, 4, [5, 5])
+    with pytest.raises(hip.CloveError):  # head_dim above 1024
         run(hip, q, None, None, kv, bt, cl)
     q, kn, vn, kv, bt, cl = make(9, 2, 2, 64, 16, 20, 4, [5, 5])
     with pytest.raises(hip.CloveError):  # q with the wrong element count

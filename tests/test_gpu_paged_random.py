@@ -1,6 +1,7 @@
 """GPU parity: seeded random PagedAttention decodes against the oracle.
 
-Each case draws head_dim (64/128/256), block size (8/16/32), 1-6 sequences
+Each case draws head_dim (64/128/256, or for the general kernel one of
+8..320 including non-multiples of 4), block size (8/16/32, or 1..128), 1-6 sequences
 of 1-6 heads, context lengths in [0, 2600] with a bias toward block and
 partition edges, the new-token path or the cached one, Clove's default
 scale or an explicit one, and block tables whose entries may repeat across
@@ -21,12 +22,17 @@ pytestmark = pytest.mark.gpu
 RTOL, ATOL = 2e-3, 1e-5
 
 
-def random_decode(seed):
+def random_decode(seed, general=False):
     """Returns (q, k_new, v_new, kv, block_tables, context_lens, scale);
-    k_new/v_new and scale may be None."""
+    k_new/v_new and scale may be None.  `general` draws head dims and block
+    sizes that have no fixed-shape kernel."""
     g = rng(seed)
-    D = int(g.choice([64, 128, 256]))
-    bs = int(g.choice([8, 16, 32]))
+    if general:
+        D = int(g.choice([8, 24, 32, 40, 48, 80, 96, 100, 112, 160, 192, 320]))
+        bs = int(g.choice([1, 4, 12, 16, 64, 128]))
+    else:
+        D = int(g.choice([64, 128, 256]))
+        bs = int(g.choice([8, 16, 32]))
     B, H = int(g.integers(1, 7)), int(g.integers(1, 7))
     ctx = []
     for _ in range(B):
@@ -67,8 +73,8 @@ def random_decode(seed):
     return q, kn, vn, kv, bt, ctx, scale
 
 
-def run_case(hip, seed):
-    q, kn, vn, kv, bt, cl, scale = random_decode(seed)
+def run_case(hip, seed, general=False):
+    q, kn, vn, kv, bt, cl, scale = random_decode(seed, general)
     t = hip.tensor
     got = hip.paged_attention(t(q), t(kn) if kn is not None else None,
                               t(vn) if vn is not None else None, t(kv), t(bt), t(cl),
@@ -85,3 +91,8 @@ def run_case(hip, seed):
 @pytest.mark.parametrize("seed", range(30))
 def test_random_decode(hip, seed):
     run_case(hip, 500 + seed)
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_decode_general_shapes(hip, seed):
+    run_case(hip, 900 + seed, general=True)

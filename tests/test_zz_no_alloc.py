@@ -52,6 +52,8 @@ CASES = [
     # seed, B, H, D, bs, nb, max_blocks, ctx, new token
     (1, 8, 8, 128, 16, 8 * 257, 256, [4096, 1, 2049, 700, 4000, 16, 3000, 2048], False),
     (2, 3, 4, 64, 8, 3 * 130, 129, [1000, 5, 1030], True),
+    # a head dim and block size without a fixed-shape kernel (the general one)
+    (3, 3, 3, 96, 64, 3 * 40 + 2, 40, [2500, 64, 1999], True),
 ]
 
 
@@ -67,6 +69,72 @@ def test_noalloc_matches_allocating_entry_twice(hip):
         assert np.array_equal(got, want), f"seed {seed}: differs from the allocating entry"
         ref = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
         assert_close(got, ref, 2e-3, 1e-5, f"seed {seed} vs oracle")
+
+
+def device_free_bytes():
+    """hipMemGetInfo's free bytes on the current device."""
+    rt = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert rt.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_allocates_nothing(hip):
+    """The entry's defining property: with its inputs resident and every
+    kernel it launches already loaded (by the allocating entry), a call
+    changes neither the library's reserved bytes nor the device's free
+    bytes; again after the allocator's cache is emptied."""
+    seed, B, H, D, bs, nb, mb, ctx, _ = CASES[0]
+    q, kn, vn, kv, bt, cl = make(seed, B, H, D, bs, nb, mb, ctx)
+    scale = float(1 / np.sqrt(np.float32(D)))
+    want = allocating(hip, q, None, None, kv, bt, cl, scale)
+    t = hip.tensor
+    tq, tkv, tbt, tcl = t(q), t(kv), t(bt), t(cl)
+    out = hip.empty(q.shape)
+    p = lambda x: C.c_void_p(x.device_ptr)
+    f = hip.lib().clove_hip_paged_attention_noalloc
+    for empty_first in (False, True):
+        if empty_first:
+            hip.empty_cache()
+        hip.synchronize()
+        reserved, free = hip.memory_reserved(), device_free_bytes()
+        assert f(p(tq), None, None, p(tkv), nb, bs, H, D, p(tbt), mb, p(tcl), B, scale,
+                 p(out)) == 0, hip.last_error()
+        hip.synchronize()
+        assert hip.memory_reserved() == reserved
+        assert device_free_bytes() == free
+        assert np.array_equal(out.numpy(), want)
+
+
+def test_noalloc_across_a_stream_switch(hip):
+    """Two calls on different streams: the first on the library's stream, the
+    second on a caller-owned stream after clove_hip_set_stream, which waits
+    for the stream it replaces.  So the second call never overlaps the first
+    in the shared scratch array, and both match the allocating entry."""
+    rt = C.CDLL("libamdhip64.so")
+    stream = C.c_void_p()
+    assert rt.hipStreamCreate(C.byref(stream)) == 0
+    f = hip.lib().clove_hip_paged_attention_noalloc
+    p = lambda x: C.c_void_p(x.device_ptr)
+    try:
+        outs, wants = [], []
+        for i, (seed, B, H, D, bs, nb, mb, ctx, _) in enumerate(CASES[:2]):
+            q, kn, vn, kv, bt, cl = make(seed, B, H, D, bs, nb, mb, ctx)
+            scale = float(1 / np.sqrt(np.float32(D)))
+            wants.append(allocating(hip, q, None, None, kv, bt, cl, scale))
+            t = hip.tensor
+            tq, tkv, tbt, tcl = t(q), t(kv), t(bt), t(cl)
+            out = hip.empty(q.shape)
+            if i == 1:
+                assert hip.lib().clove_hip_set_stream(stream) == 0
+            assert f(p(tq), None, None, p(tkv), nb, bs, H, D, p(tbt), mb, p(tcl), B, scale,
+                     p(out)) == 0, hip.last_error()
+            outs.append((out, tq, tkv, tbt, tcl))  # keep the inputs alive until read
+        for (out, *_), want in zip(outs, wants):
+            assert np.array_equal(out.numpy(), want)
+    finally:
+        hip.lib().clove_hip_set_stream(None)
+        rt.hipStreamDestroy(stream)
 
 
 def test_noalloc_rejects_a_workspace_past_the_scratch(hip):
@@ -96,8 +164,8 @@ def test_noalloc_argument_errors(hip):
     cl = t(np.array([3, 3], np.int32))
     p = lambda x: C.c_void_p(x.device_ptr)
     f = hip.lib().clove_hip_paged_attention_noalloc
-    # head_dim without a kernel
-    assert f(p(q), None, None, p(kv), 4, 16, 4, 32, p(bt), 2, p(cl), 2, 0.1, p(q)) == hip.ERR_SHAPE
+    # head_dim above the largest with a kernel (1024)
+    assert f(p(q), None, None, p(kv), 4, 16, 1, 1025, p(bt), 2, p(cl), 2, 0.1, p(q)) == hip.ERR_SHAPE
     # k without v
     assert f(p(q), p(q), None, p(kv), 4, 16, 2, 64, p(bt), 2, p(cl), 2, 0.1, p(q)) == hip.ERR_INVALID
     # a misaligned pointer
