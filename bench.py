@@ -516,6 +516,15 @@ def backward_parity(ca, name, want, y, dy, x, targets, one, a, b):
         PARITY[name] = "ok" if not bad.any() else f"{int(bad.sum())} elements out of bound"
         log(f"parity {name}: {PARITY[name]}")
         return
+    if name == "mse":
+        # Clove's sequential f32 fold over 16.7M terms of ~2 ends ~3% low (its
+        # running sum's ulp reaches 2), so the loss is held to float64, as in
+        # its parity test; the oracle's output stays the CPU leg's workload
+        got = ca.mse(a, b).numpy()
+        ah, bh = a.numpy().astype(np.float64), b.numpy()
+        exact = np.mean((ah - bh) ** 2)
+        check_parity(name, got, np.full(got.shape, exact), 1e-4, 0.0)
+        return
     got, rtol, atol = {
         "gelu_backward": (lambda: ca.gelu_backward(a, b), 1e-5, 2e-6),
         # sums of 4096 unit normals, in another order than the oracle's
@@ -523,7 +532,6 @@ def backward_parity(ca, name, want, y, dy, x, targets, one, a, b):
         "cross_entropy": (lambda: ca.cross_entropy(x, targets), 1e-4, 0.0),
         "cross_entropy_backward": (lambda: ca.cross_entropy_backward(x, targets, one), 1e-4,
                                    1e-10),
-        "mse": (lambda: ca.mse(a, b), 1e-4, 0.0),
         "mse_backward": (lambda: ca.mse_backward(a, b, one), 1e-6, 1e-30),
     }[name]
     got = got().numpy()
