@@ -179,6 +179,7 @@ struct PagedArgs {
     int64_t num_blocks;    // blocks in the pool (bounds for table entries)
     int num_seqs, num_heads, head_dim, block_size, max_blocks, max_parts;
     int part_tokens;       // tokens per partition (multiple of block_size)
+    int gen_shift;         // general kernel: line-aligned pieces (set by paged_attention)
     float scale;
 };
 // The allocation-free decode's partition workspace: a static device array

@@ -456,20 +456,24 @@ __device__ __forceinline__ int gen_float(int j, int e, int c) {
 }
 
 // Loads the NP pieces of the row at `row` (null: no token) into `out`.
+// `shift` floats (a multiple of 4, VEC4 only) move the pieces back so that
+// they start on a 128-byte line (see paged_general_kernel): float f of the
+// row is then in piece slot f + shift.
 template <int L, int NP, bool VEC4>
 __device__ __forceinline__ void gen_row(const float *row, const float *safe, int c, int D,
-                                        cl_f4 (&out)[NP]) {
+                                        int shift, cl_f4 (&out)[NP]) {
     const float *base = row ? row : safe;
 #pragma unroll
     for (int j = 0; j < NP; ++j) {
-        // With NP < 8, general_plan picks (L, NP) only for head dims that
-        // leave fewer than L idle piece slots, so the pieces before the last
-        // are inside the row and only the last may pass D; with NP >= 8 more
-        // than one piece can, and every piece is checked.
-        const bool last = NP >= 8 || j == NP - 1;
+        // Unshifted with NP < 8, general_plan picks (L, NP) only for head
+        // dims that leave fewer than L idle piece slots, so the pieces
+        // before the last are inside the row and only the last may pass D;
+        // shifted, or with NP >= 8, any piece can be outside, and every
+        // piece is checked.
+        const bool last = NP >= 8 || shift != 0 || j == NP - 1;
         if (VEC4) {
-            const int f = gen_float<L, true>(j, 0, c);
-            const bool use = !last || f < D;
+            const int f = gen_float<L, true>(j, 0, c) - shift;
+            const bool use = !last || (f >= 0 && f < D);
             const cl_f4 v = stream_load(use ? base + f : base);
             out[j] = (row && use) ? v : (cl_f4){0.f, 0.f, 0.f, 0.f};
         } else {
@@ -521,6 +525,13 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
     const int H = a.num_heads, D = a.head_dim, BS = a.block_size;
     const int h = blockIdx.x * 4 + wave;
     const bool active = h < H;  // idle waves still take part in the barriers
+    // With a.gen_shift (H * D a multiple of 32 floats, so head h's rows sit
+    // at the same offset in their 128-byte lines for every token), the
+    // wave's pieces start at the line boundary before its rows: each wave
+    // load then touches whole lines, where a row that starts mid-line (D =
+    // 48, 80, 112) makes every load touch twice the lines.  q and the output
+    // use the same float-to-lane map.
+    const int shift = VEC4 && a.gen_shift ? (h * D) % 32 : 0;
     const int grp = lane / L, c = lane % L;
     const size_t head_off = ((size_t)b * H + (active ? h : 0)) * D;
     const int ctx = clamp_ctx(a, b, part == 0 && threadIdx.x == 0);
@@ -537,7 +548,7 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
     const size_t h_off = (size_t)(active ? h : 0) * D;
 
     cl_f4 q[NP], o[NP];
-    gen_row<L, NP, VEC4>(active ? a.q + head_off : nullptr, a.q, c, D, q);
+    gen_row<L, NP, VEC4>(active ? a.q + head_off : nullptr, a.q, c, D, shift, q);
 #pragma unroll
     for (int j = 0; j < NP; ++j) o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
     WaveState st{-INFINITY, 0.0f};
@@ -557,8 +568,8 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
                 kp = a.k_cache + off;
                 vp = a.v_cache + off;
             }
-            gen_row<L, NP, VEC4>(kp, a.k_cache, c, D, r.k[s]);
-            gen_row<L, NP, VEC4>(vp, a.k_cache, c, D, r.v[s]);
+            gen_row<L, NP, VEC4>(kp, a.k_cache, c, D, shift, r.k[s]);
+            gen_row<L, NP, VEC4>(vp, a.k_cache, c, D, shift, r.v[s]);
         }
     };
     auto consume = [&](const GenRegs<L, NP> &r) {
@@ -650,8 +661,8 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
         for (int j = 0; j < NP; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-                const int f = gen_float<L, VEC4>(j, e, c);
-                if (f < D) a.out[head_off + f] = o[j][e] * inv;
+                const int f = gen_float<L, VEC4>(j, e, c) - shift;
+                if (f >= 0 && f < D) a.out[head_off + f] = o[j][e] * inv;
             }
         return;
     }
@@ -660,8 +671,8 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
     for (int j = 0; j < NP; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const int f = gen_float<L, VEC4>(j, e, c);
-            if (f < D) ws[f] = o[j][e];
+            const int f = gen_float<L, VEC4>(j, e, c) - shift;
+            if (f >= 0 && f < D) ws[f] = o[j][e];
         }
     if (c == 0) {
         ws[D] = st.m;
@@ -851,7 +862,7 @@ size_t paged_workspace_floats(int num_seqs, int num_heads, int head_dim, int max
 struct GenPlan {
     int L, NP;
 };
-static GenPlan general_plan(int D) {
+static GenPlan general_plan(int D, int extra) {
     // No 4-lane groups: measured at the config-5 shape they streamed at
     // 43-48% of HBM peak (D = 48, 80, 112), each load then touching 16
     // cache lines, against 70-79% for 8- and 16-lane groups.
@@ -865,7 +876,7 @@ static GenPlan general_plan(int D) {
             if (np >= need) return {16, np};
         return {16, 16};
     }
-    const int P = D / 4;
+    const int P = D / 4 + extra;
     GenPlan best{16, 16};
     int waste = 1 << 30;
     for (const GenPlan &g : vec4) {
@@ -889,12 +900,24 @@ void paged_attention(const PagedArgs &a, hipStream_t s) {
     const char *force = std::getenv("CLOVE_PAGED_GENERAL");
     const bool general = !paged_tuned(a.head_dim, a.block_size) || (force && *force == '1');
     if (general) {
-        const GenPlan g = general_plan(a.head_dim);
+        // Line-aligned pieces need room for the largest shift of any head:
+        // 32 - gcd(D, 32) floats (D = 80 or 112: 16 floats, 4 pieces).
+        PagedArgs ga = a;
+        const int D = a.head_dim;
+        int g32 = 32, d = D;
+        while (d) {
+            const int t = g32 % d;
+            g32 = d;
+            d = t;
+        }
+        const int extra = (32 - g32) / 4;
+        ga.gen_shift = D % 4 == 0 && extra > 0 && ((int64_t)a.num_heads * D) % 32 == 0;
+        const GenPlan g = general_plan(D, ga.gen_shift ? extra : 0);
         const int key = g.L * 100 + g.NP;
         if (a.head_dim % 4 != 0) {
             switch (key) {
 #define CLOVE_PAGED_GEN1(L, NP)                                                    \
-    case L * 100 + NP: paged_general_kernel<L, NP, false><<<grid, 256, 0, s>>>(a); break;
+    case L * 100 + NP: paged_general_kernel<L, NP, false><<<grid, 256, 0, s>>>(ga); break;
                 CLOVE_PAGED_GEN1(16, 1) CLOVE_PAGED_GEN1(16, 2) CLOVE_PAGED_GEN1(16, 3)
                 CLOVE_PAGED_GEN1(16, 4) CLOVE_PAGED_GEN1(16, 5) CLOVE_PAGED_GEN1(16, 6)
                 CLOVE_PAGED_GEN1(16, 8) CLOVE_PAGED_GEN1(16, 12) CLOVE_PAGED_GEN1(16, 16)
@@ -904,7 +927,7 @@ void paged_attention(const PagedArgs &a, hipStream_t s) {
         } else {
             switch (key) {
 #define CLOVE_PAGED_GEN4(L, NP)                                                    \
-    case L * 100 + NP: paged_general_kernel<L, NP, true><<<grid, 256, 0, s>>>(a); break;
+    case L * 100 + NP: paged_general_kernel<L, NP, true><<<grid, 256, 0, s>>>(ga); break;
                 CLOVE_PAGED_GEN4(16, 1) CLOVE_PAGED_GEN4(16, 2) CLOVE_PAGED_GEN4(16, 3)
                 CLOVE_PAGED_GEN4(16, 4) CLOVE_PAGED_GEN4(16, 5) CLOVE_PAGED_GEN4(16, 6)
                 CLOVE_PAGED_GEN4(16, 8) CLOVE_PAGED_GEN4(16, 12) CLOVE_PAGED_GEN4(16, 16)
