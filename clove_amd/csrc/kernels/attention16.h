@@ -124,6 +124,8 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
     int k_wave = a.Sk;
     if (CAUSAL) k_wave = min(k_wave, min(qw0 + 15, a.S - 1) + a.q_pos - a.k_pos + 1);
     const int nblk = k_end > 0 ? (k_end + kBK - 1) / kBK : 0;
+    // this lane's query sees keys t < lim
+    const int lim = q_ok ? (CAUSAL ? min(a.Sk, query + a.q_pos - a.k_pos + 1) : a.Sk) : 0;
 
     // K and V tiles come through buffer loads over this batch's [Sk, H*D]
     // rows: a key past Sk or a dim past D gets an offset past the end and
@@ -202,26 +204,23 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
             __builtin_amdgcn_s_setprio(0);
             // A block the whole wave sees (every key < Sk and, under the causal
             // mask, at or before the wave's first query) skips the mask.
+            // The empty asm statement keeps the mask a branch: without it the
+            // compiler turns it into selects that every block pays for.
             bool full = kb + kBK <= a.Sk && qw0 + 16 <= a.S;
             if (CAUSAL) full = full && kb + kBK - 1 + a.k_pos <= qw0 + a.q_pos;
-            float mloc = -INFINITY;
-            if (full) {
+            if (!full) {
+                asm volatile("");
+                const int vis = lim - kb - 4 * q4;  // s[hk][i] visible iff 16hk + i < vis
 #pragma unroll
                 for (int hk = 0; hk < 2; ++hk)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[hk][i]);
-            } else {
-#pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int t = kb + 16 * hk + 4 * q4 + i;
-                        bool ok = t < a.Sk && q_ok;
-                        if (CAUSAL) ok = ok && t + a.k_pos <= query + a.q_pos;
-                        s[hk][i] = ok ? s[hk][i] : -INFINITY;
-                        mloc = fmaxf(mloc, s[hk][i]);
-                    }
+                    for (int i = 0; i < 4; ++i) s[hk][i] = 16 * hk + i < vis ? s[hk][i] : -INFINITY;
             }
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int hk = 0; hk < 2; ++hk)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[hk][i]);
             mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
             // Lazy rescale: the running max m moves only when some query of the

@@ -120,6 +120,8 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     int k_wave = a.Sk;
     if (CAUSAL) k_wave = min(k_wave, min(q0 + wave * 32 + 31, a.S - 1) + a.q_pos - a.k_pos + 1);
     const int nblk = k_end > 0 ? (k_end + kBK - 1) / kBK : 0;
+    // this lane's query sees keys t < lim
+    const int lim = q_ok ? (CAUSAL ? min(a.Sk, query + a.q_pos - a.k_pos + 1) : a.Sk) : 0;
 
     // K and V tiles come through buffer loads over this batch's [Sk, H*D]
     // rows: a key past Sk gets an offset past the end and reads as zeros.  A
@@ -198,23 +200,20 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
             __builtin_amdgcn_s_setprio(0);
             // A block the whole wave sees (every key < Sk and, under the causal
             // mask, at or before the wave's first query) skips the mask.
+            // The empty asm statement keeps the mask a branch: without it the
+            // compiler turns it into selects that every block pays for.
             const int qw0 = q0 + wave * 32;
             bool full = kb + kBK <= a.Sk && qw0 + 32 <= a.S;
             if (CAUSAL) full = full && kb + kBK - 1 + a.k_pos <= qw0 + a.q_pos;
-            float mloc = -INFINITY;
-            if (full) {
+            if (!full) {
+                asm volatile("");
+                const int vis = lim - kb - 4 * hh;  // s[i] visible iff 8(i/4) + i%4 < vis
 #pragma unroll
-                for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int t = kb + 8 * (i / 4) + 4 * hh + (i % 4);
-                    bool ok = t < a.Sk && q_ok;
-                    if (CAUSAL) ok = ok && t + a.k_pos <= query + a.q_pos;
-                    s[i] = ok ? s[i] : -INFINITY;
-                    mloc = fmaxf(mloc, s[i]);
-                }
+                for (int i = 0; i < 16; ++i) s[i] = 8 * (i / 4) + (i % 4) < vis ? s[i] : -INFINITY;
             }
+            float mloc = -INFINITY;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) mloc = fmaxf(mloc, s[i]);
             mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
             // Lazy rescale: the running max m moves only when some query of the
             // wave sees a score more than kSlack above it.  Scores up to
