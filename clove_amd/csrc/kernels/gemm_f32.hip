@@ -523,7 +523,10 @@ __global__ void __launch_bounds__(256)
     // EDGE: a last slab that K ends inside (K % 4 == 0) is loaded with the
     // pieces past K masked to zeros, as the register-staged kernel fills them
     const int tail_sl = EDGE && k_len % BK ? slabs - 1 : -1;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    // wave-uniform for the compiler: the DMA's LDS address (M0) is then
+    // computed on the scalar unit, not by a readfirstlane per instruction
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm0 = (wave / WN_) * WM, wn0 = (wave % WN_) * WN;
     const int l32 = lane & 31, h = lane >> 5;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(g.A, (uint32_t)((size_t)M * K * 4));
@@ -984,7 +987,10 @@ __global__ void __launch_bounds__(64 * kStripWaves) gemm_strip_kernel(GemmArgs g
     const int halves = g.tiles / g.tiles_n;
     const int strip = V / halves, mh = V % halves;
     const int n0 = strip * 32, m0 = mh * 16;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    // wave-uniform for the compiler: the DMA's LDS address (M0) is then
+    // computed on the scalar unit, not by a readfirstlane per instruction
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int l16 = lane & 15, q = lane >> 4;
     const int kb = wave * (64 * NCH);
     float *myring = ring + wave * R * CH;
