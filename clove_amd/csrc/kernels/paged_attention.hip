@@ -515,30 +515,43 @@ __device__ __forceinline__ float groups_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
-template <int L, int NP, bool VEC4>
+// HP = 2 (head pairs, D = 16 and 48 with H even): a group's row is the 2D
+// floats of heads 2p and 2p + 1, which start on a 128-byte line for every
+// token; L = 8 lanes take D / 16 pieces each, none idle, and no load touches
+// a line that another wave also reads.  Each piece belongs to one head of the
+// pair (pieces hold four floats and D % 4 == 0), so q . k, the online
+// softmax and the output are kept per head.  At the config-5 shape: D = 16
+// 38.2 -> 45.7%, D = 48 56.9 -> 61.6% of HBM.  D = 80 and 112 (five and seven
+// pieces per lane) fold 8 tokens per softmax step against 16 for the single
+// heads, twice the softmax work per token, and measured slower (48.6 / 58.7%
+// against 57.6 / 65.4%; 56.4% at D = 80 folding 16 tokens in 256 VGPRs).
+template <int L, int NP, bool VEC4, int HP = 1>
 __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
+    static_assert(HP == 1 || (HP == 2 && VEC4), "head pairs move 16-byte pieces");
     using Sh = GenShape<L, NP>;
+    using Regs = GenRegs<L, NP>;
     constexpr int T = Sh::T, TS = Sh::TS;
     __shared__ int rows_lds[kGenChunk];
     const int part = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int H = a.num_heads, D = a.head_dim, BS = a.block_size;
-    const int h = blockIdx.x * 4 + wave;
+    const int DR = HP * D;                   // floats of the row a group reads
+    const int h = HP * (blockIdx.x * 4 + wave);  // the row's first head
     const bool active = h < H;  // idle waves still take part in the barriers
     // With a.gen_shift (H * D a multiple of 32 floats, so head h's rows sit
     // at the same offset in their 128-byte lines for every token), the
     // wave's pieces start at the line boundary before its rows: each wave
     // load then touches whole lines, where a row that starts mid-line (D =
     // 48, 80, 112) makes every load touch twice the lines.  q and the output
-    // use the same float-to-lane map.
-    const int shift = VEC4 && a.gen_shift ? (h * D) % 32 : 0;
+    // use the same float-to-lane map.  (Head pairs start on a line.)
+    const int shift = HP == 1 && VEC4 && a.gen_shift ? (h * D) % 32 : 0;
     const int grp = lane / L, c = lane % L;
     const size_t head_off = ((size_t)b * H + (active ? h : 0)) * D;
     const int ctx = clamp_ctx(a, b, part == 0 && threadIdx.x == 0);
     const int t_begin = part * a.part_tokens;
     if (t_begin >= ctx) {  // uniform over the workgroup
         if (ctx == 0 && part == 0 && active)
-            for (int d = lane; d < D; d += 64) a.out[head_off + d] = 0.0f;
+            for (int d = lane; d < DR; d += 64) a.out[head_off + d] = 0.0f;
         return;
     }
     const int t_end = min(t_begin + a.part_tokens, ctx);
@@ -548,12 +561,17 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
     const size_t h_off = (size_t)(active ? h : 0) * D;
 
     cl_f4 q[NP], o[NP];
-    gen_row<L, NP, VEC4>(active ? a.q + head_off : nullptr, a.q, c, D, shift, q);
+    gen_row<L, NP, VEC4>(active ? a.q + head_off : nullptr, a.q, c, DR, shift, q);
 #pragma unroll
     for (int j = 0; j < NP; ++j) o[j] = (cl_f4){0.f, 0.f, 0.f, 0.f};
-    WaveState st{-INFINITY, 0.0f};
+    WaveState st[HP];
+#pragma unroll
+    for (int u = 0; u < HP; ++u) st[u] = WaveState{-INFINITY, 0.0f};
+    bool second[NP];  // piece j of this lane belongs to the pair's second head
+#pragma unroll
+    for (int j = 0; j < NP; ++j) second[j] = HP == 2 && gen_float<L, VEC4>(j, 0, c) >= D;
 
-    auto issue = [&](int t0, int cb, int ce, GenRegs<L, NP> &r) {
+    auto issue = [&](int t0, int cb, int ce, Regs &r) {
 #pragma unroll
         for (int s = 0; s < TS; ++s) {
             const int t = t0 + T * s + grp;
@@ -568,36 +586,61 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
                 kp = a.k_cache + off;
                 vp = a.v_cache + off;
             }
-            gen_row<L, NP, VEC4>(kp, a.k_cache, c, D, shift, r.k[s]);
-            gen_row<L, NP, VEC4>(vp, a.k_cache, c, D, shift, r.v[s]);
+            gen_row<L, NP, VEC4>(kp, a.k_cache, c, DR, shift, r.k[s]);
+            gen_row<L, NP, VEC4>(vp, a.k_cache, c, DR, shift, r.v[s]);
         }
     };
-    auto consume = [&](const GenRegs<L, NP> &r) {
-        float sc[TS];
-        float bm = -INFINITY;
+    auto consume = [&](const Regs &r) {
+        float sc[HP][TS];
+        float bm[HP];
+#pragma unroll
+        for (int u = 0; u < HP; ++u) bm[u] = -INFINITY;
 #pragma unroll
         for (int s = 0; s < TS; ++s) {
-            float d = dot4(q[0], r.k[s][0]);
+            float d[HP];
+            if constexpr (HP == 1) {
+                d[0] = dot4(q[0], r.k[s][0]);
 #pragma unroll
-            for (int j = 1; j < NP; ++j) d += dot4(q[j], r.k[s][j]);
-            d = group_sum<L>(d);
-            sc[s] = r.in[s] ? d * a.scale : -INFINITY;
-            bm = fmaxf(bm, sc[s]);
+                for (int j = 1; j < NP; ++j) d[0] += dot4(q[j], r.k[s][j]);
+            } else {
+                d[0] = d[1] = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NP; ++j) {
+                    const float t = dot4(q[j], r.k[s][j]);
+                    d[0] += second[j] ? 0.0f : t;
+                    d[1] += second[j] ? t : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < HP; ++u) {
+                d[u] = group_sum<L>(d[u]);
+                sc[u][s] = r.in[s] ? d[u] * a.scale : -INFINITY;
+                bm[u] = fmaxf(bm[u], sc[u][s]);
+            }
         }
-        bm = groups_max<L>(bm);
-        const float m_new = fmaxf(st.m, bm);
-        const float alpha = (st.m == -INFINITY) ? 0.0f : fast_exp(st.m - m_new);
-        st.l *= alpha;
+        float m_new[HP], alpha[HP];
 #pragma unroll
-        for (int j = 0; j < NP; ++j) o[j] *= alpha;
+        for (int u = 0; u < HP; ++u) {
+            bm[u] = groups_max<L>(bm[u]);
+            m_new[u] = fmaxf(st[u].m, bm[u]);
+            alpha[u] = (st[u].m == -INFINITY) ? 0.0f : fast_exp(st[u].m - m_new[u]);
+            st[u].l *= alpha[u];
+        }
+#pragma unroll
+        for (int j = 0; j < NP; ++j) o[j] *= HP == 2 && second[j] ? alpha[HP - 1] : alpha[0];
 #pragma unroll
         for (int s = 0; s < TS; ++s) {
-            const float p = r.in[s] ? fast_exp(sc[s] - m_new) : 0.0f;
-            st.l += p;
+            float p[HP];
 #pragma unroll
-            for (int j = 0; j < NP; ++j) o[j] += p * r.v[s][j];
+            for (int u = 0; u < HP; ++u) {
+                p[u] = r.in[s] ? fast_exp(sc[u][s] - m_new[u]) : 0.0f;
+                st[u].l += p[u];
+            }
+#pragma unroll
+            for (int j = 0; j < NP; ++j) o[j] += (HP == 2 && second[j] ? p[HP - 1] : p[0]) * r.v[s][j];
         }
-        st.m = m_new;
+#pragma unroll
+        for (int u = 0; u < HP; ++u) st[u].m = m_new[u];
     };
 
     const int64_t nb = a.num_blocks;
@@ -624,7 +667,7 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
         if (!active) continue;
         constexpr int G = T * TS;  // tokens per fold
         if (Sh::PIPE) {
-            GenRegs<L, NP> A, B;
+            Regs A, B;
             int t0 = cb;
             issue(t0, cb, ce, A);
             for (; t0 + 2 * G < ce; t0 += 2 * G) {
@@ -642,41 +685,55 @@ __global__ void __launch_bounds__(256) paged_general_kernel(PagedArgs a) {
             }
         } else {
             for (int t0 = cb; t0 < ce; t0 += G) {
-                GenRegs<L, NP> A;
+                Regs A;
                 issue(t0, cb, ce, A);
                 consume(A);
             }
         }
     }
     if (!active) return;
-    st.l = groups_sum<L>(st.l);
+#pragma unroll
+    for (int u = 0; u < HP; ++u) st[u].l = groups_sum<L>(st[u].l);
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) o[j][e] = groups_sum<L>(o[j][e]);
     if (grp != 0) return;
+    // float f of the row: head h + f / D, dim f % D (a piece never straddles)
     if (n_parts == 1) {
-        const float inv = 1.0f / st.l;
+        float inv[HP];
+#pragma unroll
+        for (int u = 0; u < HP; ++u) inv[u] = 1.0f / st[u].l;
 #pragma unroll
         for (int j = 0; j < NP; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int f = gen_float<L, VEC4>(j, e, c) - shift;
-                if (f >= 0 && f < D) a.out[head_off + f] = o[j][e] * inv;
+                if (f >= 0 && f < DR)
+                    a.out[head_off + f] = o[j][e] * (HP == 2 && second[j] ? inv[HP - 1] : inv[0]);
             }
         return;
     }
-    float *ws = a.partials + (((size_t)b * H + h) * a.max_parts + part) * (D + 2);
+    float *ws[HP];
+#pragma unroll
+    for (int u = 0; u < HP; ++u)
+        ws[u] = a.partials + (((size_t)b * H + h + u) * a.max_parts + part) * (D + 2);
 #pragma unroll
     for (int j = 0; j < NP; ++j)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             const int f = gen_float<L, VEC4>(j, e, c) - shift;
-            if (f >= 0 && f < D) ws[f] = o[j][e];
+            if (f >= 0 && f < DR) {
+                if (HP == 2 && second[j]) ws[HP - 1][f - D] = o[j][e];
+                else ws[0][f] = o[j][e];
+            }
         }
     if (c == 0) {
-        ws[D] = st.m;
-        ws[D + 1] = st.l;
+#pragma unroll
+        for (int u = 0; u < HP; ++u) {
+            ws[u][D] = st[u].m;
+            ws[u][D + 1] = st[u].l;
+        }
     }
 }
 
@@ -914,7 +971,17 @@ void paged_attention(const PagedArgs &a, hipStream_t s) {
         ga.gen_shift = D % 4 == 0 && extra > 0 && ((int64_t)a.num_heads * D) % 32 == 0;
         const GenPlan g = general_plan(D, ga.gen_shift ? extra : 0);
         const int key = g.L * 100 + g.NP;
-        if (a.head_dim % 4 != 0) {
+        // Head pairs (D = 16 or 48, H even): groups of 8 lanes, D / 16 pieces
+        // (CLOVE_PAGED_PAIRS=0 turns them off, for tests and measurement).
+        const char *pairs_env = std::getenv("CLOVE_PAGED_PAIRS");
+        const bool head_pairs = (D == 16 || D == 48) && a.num_heads % 2 == 0 &&
+                                !(pairs_env && *pairs_env == '0');
+        if (head_pairs) {
+            const dim3 grid2((unsigned)((a.num_heads / 2 + 3) / 4), (unsigned)a.max_parts,
+                             (unsigned)a.num_seqs);
+            if (D == 16) paged_general_kernel<8, 1, true, 2><<<grid2, 256, 0, s>>>(ga);
+            else paged_general_kernel<8, 3, true, 2><<<grid2, 256, 0, s>>>(ga);
+        } else if (a.head_dim % 4 != 0) {
             switch (key) {
 #define CLOVE_PAGED_GEN1(L, NP)                                                    \
     case L * 100 + NP: paged_general_kernel<L, NP, false><<<grid, 256, 0, s>>>(ga); break;

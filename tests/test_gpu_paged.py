@@ -101,6 +101,31 @@ def test_general_partitions(hip, monkeypatch, part):
     assert_close(run(hip, q, kn, vn, kv, bt, cl), want, RTOL, ATOL, f"part={part}")
 
 
+# Head pairs: D = 16 or 48 with an even head count runs the general kernel on
+# rows of two heads; H = 10 leaves the last workgroup with one of its four
+# pairs; small partitions exercise the per-head partials and the merge.  The
+# single-head form (CLOVE_PAGED_PAIRS=0) meets the same bound on the same
+# inputs.
+@pytest.mark.parametrize("D,bs,H,part", [(16, 16, 2, None), (48, 7, 6, None), (48, 16, 10, None),
+                                         (16, 64, 4, None), (16, 5, 2, 300), (48, 16, 4, 100)])
+def test_general_head_pairs(hip, monkeypatch, D, bs, H, part):
+    if part is not None:
+        monkeypatch.setenv("CLOVE_PAGED_PART", str(part))
+    B = 4
+    ctx = [1, bs + 1, 1500, 2600]
+    mb = 2600 // bs + 1
+    q, kn, vn, kv, bt, cl = make(5000 + D + bs + H, B, H, D, bs, B * mb + 2, mb, ctx)
+    want = oracle.paged_attention(q, kn, vn, kv, bt, cl).reshape(B, H * D)
+    pairs = run(hip, q, kn, vn, kv, bt, cl)
+    assert_close(pairs, want, RTOL, ATOL, f"D={D} bs={bs} H={H} new token")
+    monkeypatch.setenv("CLOVE_PAGED_PAIRS", "0")
+    single = run(hip, q, kn, vn, kv, bt, cl)
+    assert_close(single, want, RTOL, ATOL, f"D={D} bs={bs} H={H} single heads")
+    monkeypatch.delenv("CLOVE_PAGED_PAIRS")
+    want = oracle.paged_attention(q, None, None, kv, bt, cl).reshape(B, H * D)
+    assert_close(run(hip, q, None, None, kv, bt, cl), want, RTOL, ATOL, f"D={D} H={H} cached")
+
+
 def test_general_bad_table_entry_is_reported_not_read(hip):
     q, kn, vn, kv, bt, cl = make(8, 2, 2, 96, 16, 20, 4, [40, 40])
     bt[1, 1] = 1 << 30
