@@ -135,16 +135,34 @@ __global__ void __launch_bounds__(256, 2) attention_kernel(AttnArgs a) {
     const __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.v + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
     cl_f4 rk[kVec], rv[kVec];
+    // Each load's offset within the tile (key and dims) is fixed per lane;
+    // the block's first key enters as the scalar offset, so a block of keys
+    // all below Sk costs no per-lane arithmetic.  (kb < Sk always, and the
+    // host keeps Sk * H * D * 4 < 2^31, so the scalar offset cannot carry
+    // kOutside round.)
+    uint32_t toff[kVec];
+    int tkey[kVec];
+#pragma unroll
+    for (int i = 0; i < kVec; ++i) {
+        const int idx = threadIdx.x + 256 * i;
+        const int key = idx / (D / 4), dq = idx % (D / 4);
+        tkey[i] = key;
+        toff[i] = ((uint32_t)key * (uint32_t)HD + (uint32_t)(h * D + 4 * dq)) * 4u;
+    }
     auto load_tile = [&](int kb) {
+        const int soff = kb * HD * 4;
+        uint32_t off[kVec];
+#pragma unroll
+        for (int i = 0; i < kVec; ++i) off[i] = toff[i];
+        if (kb + kBK > a.Sk) {  // the last block: keys past Sk read as zeros
+            asm volatile("");   // (keeps this a branch, not selects every block pays for)
+#pragma unroll
+            for (int i = 0; i < kVec; ++i) off[i] = kb + tkey[i] < a.Sk ? toff[i] : kOutside;
+        }
 #pragma unroll
         for (int i = 0; i < kVec; ++i) {
-            const int idx = threadIdx.x + 256 * i;
-            const int key = idx / (D / 4), dq = idx % (D / 4);
-            const int t = kb + key;
-            const uint32_t off =
-                t < a.Sk ? ((uint32_t)t * (uint32_t)HD + (uint32_t)(h * D + 4 * dq)) * 4u : kOutside;
-            rk[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off, 0, 0));
-            rv[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off, 0, 0));
+            rk[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off[i], soff, 0));
+            rv[i] = __builtin_bit_cast(cl_f4, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off[i], soff, 0));
         }
     };
     auto store_tile = [&](int buf) {
