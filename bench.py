@@ -626,7 +626,7 @@ PART_KERNELS = {
     "layer_norm": ["layer_norm_wave_kernel<16>"],
     "matmul_skinny_32": ["gemm_strip_kernel<16, false, true>"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
-    "paged_decode_d96": ["paged_general_kernel<8, 3, true>", "paged_merge_kernel"],
+    "paged_decode_d96": ["paged_general_kernel<8, 3, true, 1>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
     "broadcast_grad": ["bcast_grad_strip_kernel"],
