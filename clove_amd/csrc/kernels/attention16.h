@@ -139,21 +139,40 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
     const __amdgpu_buffer_rsrc_t rsrc_v = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float *>(a.v + (size_t)b * a.Sk * HD), (short)0, (int)kv_bytes, 0x00020000);
     TileT rk[kPer], rv[kPer];
+    // Each load's offset within the tile (key and dims, or kOutside for a
+    // slot past the tile or a dim past D) is fixed per lane; the block's
+    // first key enters as the scalar offset, so a block of keys all below Sk
+    // costs no per-lane arithmetic.  (kb < Sk always, and the host keeps
+    // Sk * H * D * 4 < 2^31, so the scalar offset cannot carry kOutside
+    // round.)
+    uint32_t toff[kPer];
+    int tkey[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int idx = threadIdx.x + 512 * i;
+        const int key = idx / kRowElems, dim = (idx % kRowElems) * (VEC4 ? 4 : 1);
+        const bool ok = (kElems % 512 == 0 || idx < kElems) && (!GEN || dim < D);
+        tkey[i] = key;
+        toff[i] = ok ? ((uint32_t)key * (uint32_t)HD + (uint32_t)(h * D + dim)) * 4u : kOutside;
+    }
     auto load_tile = [&](int kb) {
+        const int soff = kb * HD * 4;
+        uint32_t off[kPer];
+#pragma unroll
+        for (int i = 0; i < kPer; ++i) off[i] = toff[i];
+        if (kb + kBK > a.Sk) {  // the last block: keys past Sk read as zeros
+            asm volatile("");   // (keeps this a branch, not selects every block pays for)
+#pragma unroll
+            for (int i = 0; i < kPer; ++i) off[i] = kb + tkey[i] < a.Sk ? toff[i] : kOutside;
+        }
 #pragma unroll
         for (int i = 0; i < kPer; ++i) {
-            const int idx = threadIdx.x + 512 * i;
-            const int key = idx / kRowElems, dim = (idx % kRowElems) * (VEC4 ? 4 : 1);
-            const int t = kb + key;
-            const bool ok = (kElems % 512 == 0 || idx < kElems) && t < a.Sk && (!GEN || dim < D);
-            const uint32_t off =
-                ok ? ((uint32_t)t * (uint32_t)HD + (uint32_t)(h * D + dim)) * 4u : kOutside;
             if constexpr (VEC4) {
-                rk[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off, 0, 0));
-                rv[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off, 0, 0));
+                rk[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b128(rsrc_k, (int)off[i], soff, 0));
+                rv[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b128(rsrc_v, (int)off[i], soff, 0));
             } else {
-                rk[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b32(rsrc_k, (int)off, 0, 0));
-                rv[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b32(rsrc_v, (int)off, 0, 0));
+                rk[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b32(rsrc_k, (int)off[i], soff, 0));
+                rv[i] = __builtin_bit_cast(TileT, __builtin_amdgcn_raw_buffer_load_b32(rsrc_v, (int)off[i], soff, 0));
             }
         }
     };
