@@ -2,8 +2,8 @@
 // v_mfma_f32_16x16x4_f32, shared by flash_attention.hip (head dim 64, the
 // fixed-shape build) and attention_general.hip (every other head dim).
 //
-// 8 waves = 128 queries per workgroup, the K and V tiles (32 keys, double
-// buffered through LDS, one barrier per block) shared by all of them.
+// 8 waves = 128 queries per workgroup, the K and V tiles (32 or 64 keys,
+// double buffered through LDS, one barrier per block) shared by all of them.
 // Lane (r, q) = (l % 16, l / 16) works for query r of its wave:
 //   S^T = K . Q^T per 16-key half hk, step (g, t) pairing K[hk*16 + r][16g +
 //   4q + t] with Q[r][16g + 4q + t] (one 16-byte read of K per g);
@@ -60,13 +60,20 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
     constexpr int kPK = DP + 8;
     constexpr int kPV = DP + 4;
     constexpr int kG = DP / 16;  // 16-dim groups of QK^T = 16-dim blocks of O^T
+    // keys per block: 64 at DP = 16 and 64 (half the barriers per key; at
+    // DP = 64 the 70 KiB of tiles still let two workgroups share a CU), 32
+    // elsewhere.  S = 4096, H = 32, causal + RoPE, against 32: DP = 64
+    // 0.578-0.631 against 0.604-0.667 ms (non-causal 1.034 against 1.067),
+    // DP = 16 0.203 against 0.214 ms; DP = 32 and 48 lost 3-5%.
+    constexpr int BK = (DP == 16 || DP == 64) ? 64 : kBK;
+    constexpr int HK = BK / 16;  // 16-key halves of a block
     // tile elements (16-byte pieces, or floats) and per-thread loads, K and V each
-    constexpr int kElems = VEC4 ? kBK * DP / 4 : kBK * DP;
+    constexpr int kElems = VEC4 ? BK * DP / 4 : BK * DP;
     constexpr int kPer = (kElems + 511) / 512;
     constexpr int kRowElems = VEC4 ? DP / 4 : DP;
     using TileT = typename std::conditional<VEC4, cl_f4, float>::type;
-    __shared__ __attribute__((aligned(16))) float sK[2][kBK * kPK];
-    __shared__ __attribute__((aligned(16))) float sV[2][kBK * kPV];
+    __shared__ __attribute__((aligned(16))) float sK[2][BK * kPK];
+    __shared__ __attribute__((aligned(16))) float sV[2][BK * kPV];
 
     const int D = GEN ? a.D : DP;
     const int L = blockIdx.x;
@@ -123,7 +130,7 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
     }
     int k_wave = a.Sk;
     if (CAUSAL) k_wave = min(k_wave, min(qw0 + 15, a.S - 1) + a.q_pos - a.k_pos + 1);
-    const int nblk = k_end > 0 ? (k_end + kBK - 1) / kBK : 0;
+    const int nblk = k_end > 0 ? (k_end + BK - 1) / BK : 0;
     // this lane's query sees keys t < lim
     const int lim = q_ok ? (CAUSAL ? min(a.Sk, query + a.q_pos - a.k_pos + 1) : a.Sk) : 0;
 
@@ -160,7 +167,7 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
         uint32_t off[kPer];
 #pragma unroll
         for (int i = 0; i < kPer; ++i) off[i] = toff[i];
-        if (kb + kBK > a.Sk) {  // the last block: keys past Sk read as zeros
+        if (kb + BK > a.Sk) {  // the last block: keys past Sk read as zeros
             asm volatile("");   // (keeps this a branch, not selects every block pays for)
 #pragma unroll
             for (int i = 0; i < kPer; ++i) off[i] = kb + tkey[i] < a.Sk ? toff[i] : kOutside;
@@ -198,22 +205,24 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
     }
     __syncthreads();
     for (int blk = 0; blk < nblk; ++blk) {
-        const int kb = blk * kBK;
+        const int kb = blk * BK;
         const int cur = blk & 1;
         const bool more = blk + 1 < nblk;
-        if (more) load_tile(kb + kBK);
+        if (more) load_tile(kb + BK);
 
         if (kb < k_wave) {
             const float *K = sK[cur];
             const float *V = sV[cur];
-            cl_f4 s[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            cl_f4 s[HK];
+#pragma unroll
+            for (int hk = 0; hk < HK; ++hk) s[hk] = (cl_f4){0.f, 0.f, 0.f, 0.f};
             // raised wave priority over the MFMA blocks: the other waves on
             // the SIMD do their softmax, tile loads and stores in the gaps
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int g = 0; g < kG; ++g)
 #pragma unroll
-                for (int hk = 0; hk < 2; ++hk) {
+                for (int hk = 0; hk < HK; ++hk) {
                     const cl_f4 kf =
                         *reinterpret_cast<const cl_f4 *>(K + (16 * hk + r16) * kPK + 16 * g + 4 * q4);
 #pragma unroll
@@ -225,19 +234,19 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
             // mask, at or before the wave's first query) skips the mask.
             // The empty asm statement keeps the mask a branch: without it the
             // compiler turns it into selects that every block pays for.
-            bool full = kb + kBK <= a.Sk && qw0 + 16 <= a.S;
-            if (CAUSAL) full = full && kb + kBK - 1 + a.k_pos <= qw0 + a.q_pos;
+            bool full = kb + BK <= a.Sk && qw0 + 16 <= a.S;
+            if (CAUSAL) full = full && kb + BK - 1 + a.k_pos <= qw0 + a.q_pos;
             if (!full) {
                 asm volatile("");
                 const int vis = lim - kb - 4 * q4;  // s[hk][i] visible iff 16hk + i < vis
 #pragma unroll
-                for (int hk = 0; hk < 2; ++hk)
+                for (int hk = 0; hk < HK; ++hk)
 #pragma unroll
                     for (int i = 0; i < 4; ++i) s[hk][i] = 16 * hk + i < vis ? s[hk][i] : -INFINITY;
             }
             float mloc = -INFINITY;
 #pragma unroll
-            for (int hk = 0; hk < 2; ++hk)
+            for (int hk = 0; hk < HK; ++hk)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) mloc = fmaxf(mloc, s[hk][i]);
             mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
@@ -262,7 +271,7 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
             const float mz = m == -INFINITY ? 0.0f : m;
             float ps = 0.0f;
 #pragma unroll
-            for (int hk = 0; hk < 2; ++hk)
+            for (int hk = 0; hk < HK; ++hk)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     s[hk][i] = __builtin_amdgcn_exp2f(s[hk][i] - mz);
@@ -273,7 +282,7 @@ __global__ void __launch_bounds__(512, (DP <= 128 ? 4 : 2)) attention16_kernel(A
             lsum += ps;
             __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int hk = 0; hk < 2; ++hk)
+            for (int hk = 0; hk < HK; ++hk)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const float *vr = V + (16 * hk + 4 * q4 + i) * kPV + r16;
