@@ -55,6 +55,34 @@ def test_library_exports_every_declared_symbol():
         assert getattr(lib, n).argtypes is not None, n
 
 
+def header_arities():
+    """Parameter count of every function the header declares."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(clove_hip_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_integration_rust_block_matches_the_header():
+    """The Rust `extern "C"` block a maintainer copies declares every entry
+    of the header, with the same number of parameters."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    block = doc[doc.index('extern "C" {'):]
+    block = block[:block.index("\n}")]
+    rust = {}
+    for name, params in re.findall(r"pub fn (clove_hip_\w+)\(([^)]*)\)", block, flags=re.S):
+        params = re.sub(r"//[^\n]*", "", params).strip().rstrip(",")
+        rust[name] = 0 if not params else params.count(",") + 1
+    header = header_arities()
+    assert header and set(header) == set(declared_functions())
+    assert sorted(set(header) - set(rust)) == [], "missing from INTEGRATION.md"
+    assert sorted(set(rust) - set(header)) == [], "not in the header"
+    wrong = {n: (header[n], rust[n]) for n in header if header[n] != rust[n]}
+    assert not wrong, f"parameter counts differ (header, rust): {wrong}"
+
+
 def test_calls_before_init_fail_with_status():
     """In a fresh process (in this one a GPU test may already have called
     clove_hip_init): calls before init fail with ERR_NOT_INIT."""
