@@ -19,11 +19,12 @@ from conftest import assert_close, rng
 pytestmark = pytest.mark.gpu
 
 
-def random_prefill(seed, general=False):
+def random_prefill(seed, general=False, head_dim=None):
     g = rng(seed)
     B, H = int(g.integers(1, 4)), int(g.integers(1, 5))
     D = int(g.choice([16, 24, 32, 48, 80, 96, 104, 112, 144, 160, 192, 256, 50, 70])
             if general else g.choice([64, 128]))
+    D = head_dim or D
     S, Sk = int(g.integers(1, 321)), int(g.integers(1, 321))
     flags = int(g.integers(0, 4))
     q_pos, k_pos = int(g.integers(0, 301)), int(g.integers(0, 301))
@@ -34,8 +35,8 @@ def random_prefill(seed, general=False):
     return q, k, v, H, q_pos, k_pos, flags, scale
 
 
-def run_case(hip, seed, general=False):
-    q, k, v, H, q_pos, k_pos, flags, scale = random_prefill(seed, general)
+def run_case(hip, seed, general=False, head_dim=None):
+    q, k, v, H, q_pos, k_pos, flags, scale = random_prefill(seed, general, head_dim)
     got = hip.flash_attention(hip.tensor(q), hip.tensor(k), hip.tensor(v), H, q_pos, k_pos,
                               flags, scale).numpy()
     want = oracle.attention(q, k, v, H, q_pos, k_pos, flags, scale or None)
@@ -53,3 +54,12 @@ def test_random_prefill(hip, seed):
 @pytest.mark.parametrize("seed", range(16))
 def test_random_prefill_general_head_dims(hip, seed):
     run_case(hip, 800 + seed, general=True)
+
+
+# Head dims whose 16-query kernel moves 64-key blocks (laid out for 16 or 64
+# dims): 16-byte pieces (12, 60) and single floats (14, 62), and the
+# fixed-shape 64, each over four seeded shapes and flag sets.
+@pytest.mark.parametrize("head_dim", [12, 14, 16, 60, 62, 64])
+@pytest.mark.parametrize("seed", range(4))
+def test_random_prefill_64_key_blocks(hip, head_dim, seed):
+    run_case(hip, 900 + 10 * head_dim + seed, head_dim=head_dim)
