@@ -7,7 +7,10 @@ the headline metric is quoted on), with every input already resident in HBM.
 Consecutive steps of every HBM-bound part cycle through --sets (default 3)
 identical copies of its inputs: MI355X's 256 MB last-level cache (MALL) would
 otherwise still hold part of a step's inputs from the step before, which
-reads 2-8 points of HBM peak faster than HBM itself.
+reads 2-8 points of HBM peak faster than HBM itself.  Likewise each step's
+outputs stay alive for as many steps as cover --out-mib (default 512 MiB), so
+consecutive steps write different blocks: one output block rewritten every
+step stays partly in the MALL (the config 2 chain reads ~7% faster so).
 Rank 0 prints ONE JSON line on stdout:
 
   value        whole-job algorithmic HBM GB/s of the step (5 x 64 MiB per step)
@@ -72,23 +75,53 @@ class Timing:
         return self.kernel
 
 
+# Bytes of outputs held across steps (--out-mib): set by main().
+OUT_HOLD_BYTES = 512 << 20
+
+
+def output_tensors(r):
+    """The tensors a launch returned (one, a list or tuple of them, or none)."""
+    if isinstance(r, (list, tuple)):
+        return [t for t in r if hasattr(t, "numel")]
+    return [r] if hasattr(r, "numel") else []
+
+
 def timed(ca, launch, steps, warmup):
-    """Runs `launch` warmup + steps times back to back.  Each step's output
-    is released right away, so the caching allocator hands the same block
-    back and no hipMalloc happens in the timed region; no event sits between
-    two launches."""
-    for _ in range(warmup):
-        launch()
+    """Runs `launch` warmup + steps times back to back.  Each step's outputs
+    stay alive for the next `hold` steps, enough steps that the held outputs
+    cover OUT_HOLD_BYTES (twice the 256 MB MALL by default): consecutive steps
+    then write different blocks, as they read different input sets, instead of
+    rewriting one block the MALL keeps absorbing (a 64 MiB output rewritten
+    in place reads ~7% faster than HBM takes it).  Every block is allocated
+    during the warmup, so no hipMalloc happens in the timed region; no event
+    sits between two launches."""
+    r = launch()
+    out_bytes = sum(4 * int(t.numel) for t in output_tensors(r))
+    hold = 1
+    if out_bytes >= (1 << 20) and OUT_HOLD_BYTES > 0:  # outputs the MALL could keep
+        hold = min(64, max(1, -(-OUT_HOLD_BYTES // out_bytes)))
+    # `hold` blocks rotate: a step releases the oldest outputs, then launches
+    # (with --out-mib 0, every step gets the block the step before released)
+    ring = [None] * hold
+    ring[0] = r
+    del r
+    i = 1
+    for _ in range(max(warmup, hold)):
+        ring[i % hold] = None
+        ring[i % hold] = launch()
+        i += 1
     ca.synchronize()
     ca.event_reset()
     t0 = time.perf_counter()
     e0 = ca.event_record()
     for _ in range(steps):
-        r = launch()
-        del r
+        ring[i % hold] = None
+        ring[i % hold] = launch()
+        i += 1
     e1 = ca.event_record()
     ca.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
+    ring.clear()
     return wall, Timing(wall, ca.event_elapsed(e0, e1) / steps)
 
 
@@ -670,6 +703,10 @@ def main():
                     help="identical copies of each HBM-bound part's inputs that consecutive "
                          "steps cycle through, so that no step finds its inputs in the 256 MB "
                          "last-level cache (MALL) from the step before")
+    ap.add_argument("--out-mib", type=int, default=512,
+                    help="MiB of outputs kept alive across consecutive steps, so that steps "
+                         "write different blocks and the MALL cannot absorb rewrites of one "
+                         "(0: every step reuses one output block)")
     ap.add_argument("--traffic", default=os.path.join(ROOT, "profiles", "hbm_traffic.json"),
                     help="JSON summary of the rocprof FETCH_SIZE/WRITE_SIZE passes "
                          "(bytes per launch of the chain kernel)")
@@ -677,6 +714,10 @@ def main():
 
     if args.sets < 1:
         ap.error("--sets must be at least 1")
+    if args.out_mib < 0:
+        ap.error("--out-mib must be at least 0")
+    global OUT_HOLD_BYTES
+    OUT_HOLD_BYTES = args.out_mib << 20
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
               "build (the decode path would shard by sequence and head, the rest by rows)",
@@ -712,7 +753,7 @@ def main():
         "data": "synthetic (splitmix64 normal(0,1) streams, seeds 1-4)",
         "config": {"workload": "config 2: fused chain y = gelu(a*b+c)*d, 4 x [4096,4096] f32",
                    "elements": 4096 * 4096, "bytes_per_step": nbytes,
-                   "input_sets": args.sets},
+                   "input_sets": args.sets, "output_hold_mib": args.out_mib},
         "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s", traffic),
     }
     if oracle is not None:

@@ -55,20 +55,23 @@ struct Compiled {
 std::unordered_map<std::string, Compiled> g_cache;
 
 // Launch-geometry knobs for tuning sweeps: CLOVE_CHAIN_UNROLL (vectors per
-// thread per input per iteration, default 1), CLOVE_CHAIN_BLOCK (threads per
+// thread per input per iteration, default 2), CLOVE_CHAIN_BLOCK (threads per
 // block, 64-1024 in steps of 64, default 512) and CLOVE_CHAIN_BLOCKS_PER_CU
 // (grid cap, default 32).  They change scheduling only, never the result.
-// The defaults were the fastest of a sweep with inputs cycled so the
-// last-level cache held none of them (config 2's chain): 512 x 1 gave 77.3%
-// of HBM peak, 256 x 4 74.7%, 256 x 1 76.4%, 512 x 2 76.3%, 512 x 4 71.7%,
-// 1024 x 1 77.3% (but 74.1% on the broadcast chain, against 78.4%).
+// The defaults were the fastest of a sweep with inputs and outputs cycled so
+// the last-level cache held neither (config 2's chain, one box): 512 x 2 gave
+// 76.5% of HBM peak and 77.7-79.0% on the broadcast chain, against 74.1% /
+// 75.9% for 512 x 1, 75.1% for 512 x 3, 72.5% for 512 x 4, 76.2% for
+// 1024 x 2 and 75.8% for 256 x 4; caps of 16 and 64 blocks per CU measured
+// as 32.  (Rewriting one output block every step, 512 x 1 read 79.9%: the
+// last-level cache then keeps part of the output.)
 int env_int(const char *name, int dflt, int lo, int hi) {
     const char *v = std::getenv(name);
     if (!v || !*v) return dflt;
     const int x = std::atoi(v);
     return x < lo ? lo : (x > hi ? hi : x);
 }
-int chain_unroll() { return env_int("CLOVE_CHAIN_UNROLL", 1, 1, 16); }
+int chain_unroll() { return env_int("CLOVE_CHAIN_UNROLL", 2, 1, 16); }
 int chain_block() { return (env_int("CLOVE_CHAIN_BLOCK", 512, 64, 1024) / 64) * 64; }
 int chain_blocks_per_cu() { return env_int("CLOVE_CHAIN_BLOCKS_PER_CU", 32, 1, 1024); }
 

@@ -9,8 +9,8 @@
 // Each thread streams CL_UNROLL 16-byte vectors per input per iteration
 // (all loads issued before any arithmetic), walking the index space with a
 // grid stride; a scalar loop finishes the elements past the last full vector.
-// CL_BLOCK and CL_UNROLL come from the generator (512 threads, one vector:
-// a block covers 8 KiB of each input, read by eight waves at once).
+// CL_BLOCK and CL_UNROLL come from the generator (512 threads, two vectors:
+// a block covers 16 KiB of each input, read by eight waves at once).
 #pragma once
 
 #ifndef CL_UNROLL
