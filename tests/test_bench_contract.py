@@ -44,6 +44,57 @@ def test_rotating_cycles_through_the_sets_in_order():
     assert seen == [0, 1, 2, 0, 1, 2, 0]
 
 
+class _FakeTensor:
+    """Counts live output blocks the way the library's allocator would."""
+    live = 0
+    peak = 0
+
+    def __init__(self, numel):
+        self.numel = numel
+        _FakeTensor.live += 1
+        _FakeTensor.peak = max(_FakeTensor.peak, _FakeTensor.live)
+
+    def __del__(self):
+        _FakeTensor.live -= 1
+
+
+class _FakeCa:
+    def synchronize(self):
+        pass
+
+    def event_reset(self):
+        pass
+
+    def event_record(self):
+        return 0
+
+    def event_elapsed(self, a, b):
+        return 1.0
+
+
+@pytest.mark.parametrize("out_mib,numel,blocks", [(512, 16 << 20, 8), (512, 32 << 20, 4),
+                                                  (0, 16 << 20, 1), (512, 1000, 1),
+                                                  (512, 1 << 18, 64)])
+def test_timed_rotates_output_blocks(monkeypatch, out_mib, numel, blocks):
+    """Outputs of 1 MiB or more stay alive so that `blocks` of them rotate
+    (512 MiB of 64 MiB outputs: 8), every block exists before the timed
+    steps, and all are released at the end; --out-mib 0 reuses one block."""
+    monkeypatch.setattr(bench, "OUT_HOLD_BYTES", out_mib << 20)
+    _FakeTensor.live = _FakeTensor.peak = 0
+    calls = []
+
+    def launch():
+        calls.append(_FakeTensor.live)  # blocks alive when this step allocates
+        return [_FakeTensor(numel)]
+
+    bench.timed(_FakeCa(), launch, steps=30, warmup=2)
+    assert _FakeTensor.peak == blocks
+    assert _FakeTensor.live == 0
+    timed_calls = calls[-30:]
+    assert all(c == blocks - 1 for c in timed_calls)
+    assert len(calls) - 30 >= blocks  # the warmup allocated every block
+
+
 def test_roofline_fields():
     r = bench.roofline("hbm", 6000.0, 8000.0, "GB/s", 123)
     assert r == {"bound": "hbm", "achieved": 6000.0, "peak": 8000.0, "unit": "GB/s",
