@@ -4,13 +4,16 @@
 One "step" is one pass of the fused elementwise chain y = gelu(a*b + c) * d
 over the four 16,777,216-element f32 inputs of configuration 2 (the workload
 the headline metric is quoted on), with every input already resident in HBM.
-Consecutive steps of every HBM-bound part cycle through --sets (default 3)
-identical copies of its inputs: MI355X's 256 MB last-level cache (MALL) would
-otherwise still hold part of a step's inputs from the step before, which
-reads 2-8 points of HBM peak faster than HBM itself.  Likewise each step's
-outputs stay alive for as many steps as cover --out-mib (default 512 MiB), so
-consecutive steps write different blocks: one output block rewritten every
-step stays partly in the MALL (the config 2 chain reads ~7% faster so).
+Consecutive steps of every HBM-bound part cycle through identical copies of
+its inputs: at least --sets (default 3), and as many as cover --in-mib
+(default 512 MiB, twice MI355X's 256 MB last-level cache, the MALL).  With
+fewer, the MALL still holds a step's inputs from the steps before: three
+64 MiB copies all fit in it, and the skinny matmul and the broadcast gradient
+then read 62% and 66% of HBM peak where HBM gives them 37% and 43%.
+Likewise each step's outputs stay alive for as many steps as cover --out-mib
+(default 512 MiB), so consecutive steps write different blocks: one output
+block rewritten every step stays partly in the MALL (the config 2 chain reads
+~7% faster so).
 Rank 0 prints ONE JSON line on stdout:
 
   value        whole-job algorithmic HBM GB/s of the step (5 x 64 MiB per step)
@@ -75,8 +78,17 @@ class Timing:
         return self.kernel
 
 
-# Bytes of outputs held across steps (--out-mib): set by main().
+# Bytes of outputs held across steps (--out-mib) and the least bytes of
+# inputs a part's rotation covers (--in-mib): set by main().
 OUT_HOLD_BYTES = 512 << 20
+IN_ROT_BYTES = 512 << 20
+
+
+def input_sets(args, bytes_per_set):
+    """Copies of a part's inputs its steps cycle through: --sets, or more, so
+    that the copies cover IN_ROT_BYTES (twice the 256 MB MALL by default):
+    three 64 MiB copies would all fit in the MALL and be read from there."""
+    return max(args.sets, -(-IN_ROT_BYTES // bytes_per_set))
 
 
 def output_tensors(r):
@@ -219,7 +231,7 @@ CHAIN = [("mul", -1, -2), ("add", 0, -3), ("gelu", 1), ("mul", 2, -4)]
 def bench_chain(ca, args, broadcast=False):
     n = 4096 * 4096
     sets = []
-    for _ in range(args.sets):  # identical copies (same seeds)
+    for _ in range(input_sets(args, 4 * n * (3 if broadcast else 4))):  # identical copies
         ins = [ca.empty((4096, 4096)).fill_normal(1 + i) for i in range(4)]
         if broadcast:
             ins[2] = ca.empty((4096,)).fill_normal(3)
@@ -237,7 +249,8 @@ def cpu_chain(oracle, ins_host):
 
 def bench_rows(ca, oracle, args, out):
     g = np.random.Generator(np.random.PCG64(2))
-    xs_sets = [ca.empty((8192, 4096)).fill_normal(2, 0.0, 2.0) for _ in range(args.sets)]
+    xs_sets = [ca.empty((8192, 4096)).fill_normal(2, 0.0, 2.0)
+               for _ in range(input_sets(args, 4 * 8192 * 4096))]
     x = xs_sets[0]
     gam = ca.tensor(g.uniform(0.5, 1.5, 4096).astype(np.float32))
     bet = ca.tensor(g.uniform(-0.1, 0.1, 4096).astype(np.float32))
@@ -337,7 +350,8 @@ def bench_matmul(ca, oracle, args, out, skinny_only=False):
 def bench_skinny(ca, oracle, args, out, a32, b):
     K = 4096
     # B (64 MiB) is what the skinny product streams: one copy per input set
-    bs = [b] + [ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64) for _ in range(args.sets - 1)]
+    bs = [b] + [ca.empty((K, 4096)).fill_normal(33, 0.0, 1 / 64)
+                for _ in range(input_sets(args, 4 * K * 4096) - 1)]
     wall, per = timed(ca, rotating([lambda bb=bb: ca.matmul(a32, bb) for bb in bs]), args.steps,
                       args.warmup)
     del bs[1:]
@@ -439,7 +453,8 @@ def bench_backward(ca, oracle, args, out):
     targets = ca.tensor(g.integers(0, Cc, R).astype(np.float32))
     one = ca.tensor(np.ones(1, np.float32))
     sets = []
-    for _ in range(args.sets):  # identical copies (same seeds)
+    # identical copies (same seeds), enough for the smallest input (64 MiB)
+    for _ in range(input_sets(args, 4 * N)):
         x = ca.empty((R, Cc)).fill_normal(2, 0.0, 2.0)
         sets.append({"x": x, "y": ca.softmax(x), "dy": ca.empty((R, Cc)).fill_normal(21),
                      "a": ca.empty((4096, 4096)).fill_normal(5),
@@ -473,16 +488,22 @@ def bench_backward(ca, oracle, args, out):
         log(f"{name}: {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%} of HBM peak), "
             f"{per.mean() * 1e3:.1f} us")
     del sets[1:]
-    # AdamW on a 4096x4096 parameter: reads w, g, m, v, writes w, m, v
-    w = ca.empty((4096, 4096)).fill_normal(11)
-    gw = ca.empty((4096, 4096)).fill_normal(12, 0.0, 65536.0)
-    m0 = ca.tensor(np.zeros(N, np.float32))
-    v0 = ca.tensor(np.zeros(N, np.float32))
+    # AdamW on a 4096x4096 parameter: reads w, g, m, v, writes w, m, v; the
+    # steps cycle through copies of (w, g, m, v) as the other parts cycle
+    # through input sets (each copy is updated in place)
+    copies = []
+    for _ in range(input_sets(args, 4 * 4 * N)):
+        copies.append((ca.empty((4096, 4096)).fill_normal(11),
+                       ca.empty((4096, 4096)).fill_normal(12, 0.0, 65536.0),
+                       ca.tensor(np.zeros(N, np.float32)), ca.tensor(np.zeros(N, np.float32))))
+    w, gw = copies[0][0], copies[0][1]
     step = [0]
 
     def adamw_once():
+        k = step[0]
         step[0] += 1
-        ca.adamw_step([w], [gw], [m0], [v0], step[0])
+        c = copies[k % len(copies)]
+        ca.adamw_step([c[0]], [c[1]], [c[2]], [c[3]], k // len(copies) + 1)
     wall, per = timed(ca, adamw_once, args.steps, args.warmup)
     nbytes = 28 * N
     gbs = nbytes / (per.mean() * 1e-3) / 1e9
@@ -630,7 +651,8 @@ def bench_attention(ca, oracle, args, out):
     out["flash_attention_4096"] = part
     log(f"attention prefill S=4096 H=32 D=128 causal+rope: {tf:.1f} TFLOP/s "
         f"({tf / FP32_MFMA_PEAK_TFS:.1%} of FP32 MFMA peak), {per.mean():.3f} ms")
-    xs_sets = [ca.empty((1, S, H * D)).fill_normal(34) for _ in range(args.sets)]
+    xs_sets = [ca.empty((1, S, H * D)).fill_normal(34)
+               for _ in range(input_sets(args, 4 * S * H * D))]
     x = xs_sets[0]
     wall, per = timed(ca, rotating([lambda x=x: ca.rope(x, D) for x in xs_sets]), args.steps,
                       args.warmup)
@@ -703,6 +725,10 @@ def main():
                     help="identical copies of each HBM-bound part's inputs that consecutive "
                          "steps cycle through, so that no step finds its inputs in the 256 MB "
                          "last-level cache (MALL) from the step before")
+    ap.add_argument("--in-mib", type=int, default=512,
+                    help="least MiB of inputs each HBM-bound part's input copies cover "
+                         "(more copies than --sets where a copy is small), so that the "
+                         "MALL cannot hold all of them")
     ap.add_argument("--out-mib", type=int, default=512,
                     help="MiB of outputs kept alive across consecutive steps, so that steps "
                          "write different blocks and the MALL cannot absorb rewrites of one "
@@ -716,8 +742,11 @@ def main():
         ap.error("--sets must be at least 1")
     if args.out_mib < 0:
         ap.error("--out-mib must be at least 0")
-    global OUT_HOLD_BYTES
+    if args.in_mib < 0:
+        ap.error("--in-mib must be at least 0")
+    global OUT_HOLD_BYTES, IN_ROT_BYTES
     OUT_HOLD_BYTES = args.out_mib << 20
+    IN_ROT_BYTES = args.in_mib << 20
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this backend runs on one GPU; multi-GPU runs are not part of this "
               "build (the decode path would shard by sequence and head, the rest by rows)",
@@ -753,7 +782,8 @@ def main():
         "data": "synthetic (splitmix64 normal(0,1) streams, seeds 1-4)",
         "config": {"workload": "config 2: fused chain y = gelu(a*b+c)*d, 4 x [4096,4096] f32",
                    "elements": 4096 * 4096, "bytes_per_step": nbytes,
-                   "input_sets": args.sets, "output_hold_mib": args.out_mib},
+                   "input_sets": input_sets(args, 4 * 4 * 4096 * 4096),
+                   "input_rotation_min_mib": args.in_mib, "output_hold_mib": args.out_mib},
         "roofline": roofline("hbm", achieved, HBM_PEAK_GBS, "GB/s", traffic),
     }
     if oracle is not None:
@@ -772,7 +802,8 @@ def main():
         # A plain copy through the same chain kernel (one Flatten op): the
         # practical streaming ceiling of this box, and the known-size kernel
         # that calibrates the HBM byte counters.
-        srcs = [ca.empty((4096, 4096)).fill_normal(9) for _ in range(args.sets)]
+        srcs = [ca.empty((4096, 4096)).fill_normal(9)
+                for _ in range(input_sets(args, 4 * 4096 * 4096))]
         cwall, cper = timed(ca, rotating([ca.FusedChain([("flatten", -1)], [src])
                                           for src in srcs]), args.steps, args.warmup)
         src = srcs[0]
