@@ -8,8 +8,8 @@ Consecutive steps of every HBM-bound part cycle through identical copies of
 its inputs: at least --sets (default 3), and as many as cover --in-mib
 (default 512 MiB, twice MI355X's 256 MB last-level cache, the MALL).  With
 fewer, the MALL still holds a step's inputs from the steps before: three
-64 MiB copies all fit in it, and the skinny matmul and the broadcast gradient
-then read 62% and 66% of HBM peak where HBM gives them 37% and 43%.
+64 MiB copies all fit in it, and a kernel reading 64 MiB in 128-byte column
+strips then measured 66% of HBM peak where HBM gave it 43%.
 Likewise each step's outputs stay alive for as many steps as cover --out-mib
 (default 512 MiB), so consecutive steps write different blocks: one output
 block rewritten every step stays partly in the MALL (the config 2 chain reads
@@ -679,12 +679,12 @@ PART_KERNELS = {
     "chain_broadcast": ["clove_chain_mul_add_gelu_mul_b0020"],
     "softmax": ["softmax_block_kernel<2>"],
     "layer_norm": ["layer_norm_wave_kernel<16>"],
-    "matmul_skinny_32": ["gemm_strip_kernel<16, false, true>"],
+    "matmul_skinny_32": ["gemm_skinny_kernel<1, 4, 4, 8>", "gemm_splitk_reduce"],
     "paged_decode": ["paged_heads_kernel<128, 16, 4>", "paged_merge_kernel"],
     "paged_decode_d96": ["paged_general_kernel<8, 3, true, 1>", "paged_merge_kernel"],
     "softmax_backward": ["softmax_bw_block_kernel<2>"],
     "gelu_backward": ["clove_chain_gelugrad_b00"],
-    "broadcast_grad": ["bcast_grad_strip_kernel"],
+    "broadcast_grad": ["bcast_grad_cols4_kernel", "bcast_grad_final_kernel"],
     "cross_entropy": ["cross_entropy_rows2_kernel<2>", "ordered_sum_kernel"],
     "cross_entropy_backward": ["cross_entropy_block_kernel<2, 1>"],
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],

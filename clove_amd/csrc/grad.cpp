@@ -158,13 +158,10 @@ TensorNode HipBackend::broadcast_grad(const TensorNode &g_, size_t b_numel, bool
     const Tensor &g = need(g_, "grad_out");
     CLOVE_REQUIRE(b_numel > 0, CLOVE_HIP_ERR_SHAPE, "broadcast_grad: b has no elements");
     TensorNode out = new_tensor({b_numel}, CLOVE_HIP_F32);
-    const int cus = ctx().num_cus;
-    TensorNode ws;
-    if (!k::broadcast_grad_one_pass(g.numel, b_numel, g.f32(), cus))
-        ws = new_tensor({std::max<size_t>(k::broadcast_grad_workspace(g.numel, b_numel), 1)},
-                        CLOVE_HIP_F32);
-    k::broadcast_grad(g.f32(), g.numel, b_numel, negate, ws ? ws->f32() : nullptr, out->f32(), cus,
-                      ctx().stream);
+    TensorNode ws =
+        new_tensor({std::max<size_t>(k::broadcast_grad_workspace(g.numel, b_numel), 1)},
+                   CLOVE_HIP_F32);
+    k::broadcast_grad(g.f32(), g.numel, b_numel, negate, ws->f32(), out->f32(), ctx().stream);
     return out;
 }
 

@@ -1629,23 +1629,21 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
     const bool eligible = M <= 64 && K >= 4 && K % 4 == 0 && a_aligned && b_aligned &&
                           b_bytes < (1ull << 31) && (uint64_t)M * K * 4 < (1ull << 31) &&
                           force_cfg < 0;
-    // Strip path (one launch, no workspace): M <= 32, even N, B of 4 MiB or
-    // more, K within the longest unrolled walk (4 waves x 64 chunks of 64 k)
-    // and filling at least 90% of the walk it takes (the walks come in
-    // powers of two: K = 6144 on an 8192 walk measured 43.0 us at 32 x K x
-    // 4096 against 24.1 for the skinny kernel, K = 11008 on 16384 84.5
-    // against 41.9), and between half a workgroup and three per CU (one
-    // 96 KiB workgroup fits a CU: 32 x 4096 x 50256, 3142 workgroups, 260 us
-    // against 185; 1 x 4096 x 4096, 128 workgroups, 13.0 us against 16.5).
+    // Strip path (one launch, no workspace; M <= 32, even N, K within the
+    // longest unrolled walk of 4 waves x 64 chunks of 64 k): only when forced
+    // (CLOVE_GEMM_STRIP).  Its workgroups read B in 128-byte pieces of 16 KiB
+    // rows, which HBM serves slowly: with B cycled through copies that the
+    // 256 MB last-level cache cannot hold, as a decode step's weights are,
+    // the skinny kernel is ahead at every shape measured (1, 8, 32 x 4096 x
+    // 4096: 19.0, 19.8, 21.5 us against 20.6, 22.7, 23.3; 32 x 4096 x 11008:
+    // 49.0 against 61.3).  The strip kernel led only while B stayed in that
+    // cache (32 x 4096 x 4096: 13.8 against 17.3 us).
     {
         const int halves = (M + 15) / 16, strips = (N + 31) / 32;
         int nch = 1;
         while (nch < 64 && kStripWaves * 64 * nch < K) nch *= 2;
-        const int64_t wgs = (int64_t)halves * strips;
-        const bool fits = 10 * (int64_t)K >= 9 * (int64_t)(kStripWaves * 64 * nch);
         if (eligible && !force_skinny && M <= 32 && N % 2 == 0 && K <= kStripWaves * 64 * 64 &&
-            (force_strip || (b_bytes >= (4ull << 20) && fits && 2 * wgs >= num_cus &&
-                             wgs <= 3 * (int64_t)num_cus))) {
+            force_strip) {
             p.strip = true;
             p.tiles_n = strips;
             p.tiles = halves * strips;

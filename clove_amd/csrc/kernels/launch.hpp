@@ -36,11 +36,8 @@ void cross_entropy_backward_rows(const float *logits, const float *targets, size
 // gb[j] = (negate ? -1 : 1) * sum_{i % nb == j} g[i]; part holds
 // broadcast_grad_workspace(n, nb) floats.
 size_t broadcast_grad_workspace(size_t n, size_t nb);
-// Whether broadcast_grad runs in one pass without the workspace (nb % 4 ==
-// 0, g 16-byte aligned, nb >= 16 per CU: a 32-column strip per two CUs).
-bool broadcast_grad_one_pass(size_t n, size_t nb, const float *g, int num_cus);
 void broadcast_grad(const float *g, size_t n, size_t nb, bool negate, float *part, float *gb,
-                    int num_cus, hipStream_t s);
+                    hipStream_t s);
 // out[0] = sum((p - t)^2) / n; part holds sq_diff_workspace(n) floats.
 size_t sq_diff_workspace(size_t n);
 void mse_loss(const float *p, const float *t, size_t n, float *part, float *out, hipStream_t s);

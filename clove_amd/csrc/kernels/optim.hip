@@ -49,10 +49,13 @@ __device__ __forceinline__ void adamw_elem(float &w, float g, float &m, float &v
     w -= h.lr * m_hat / (sqrtf(v_hat) + h.eps);
 }
 
-// 512-thread workgroups (83.9% of HBM peak at 4096 x 4096 against 83.0% for
-// 256).  w, m and v are read and written back with ordinary loads and stores:
-// non-temporal ones for these read-modify-write arrays measured 75.5%; the
-// gradient, read once, streams non-temporally.
+// 512-thread workgroups, every load and store non-temporal: with the steps
+// cycling through parameter copies that the 256 MB last-level cache cannot
+// hold, 4096 x 4096 took 76.9-78.0 us (75-76% of HBM peak) against 87.7-89.2
+// us with ordinary loads and stores for w, m and v and a 16-per-CU grid cap
+// (80.7 us non-temporal at that cap; caps of 24-64 and 256-thread groups
+// within 2 us).  Ordinary accesses led (83.9% against 75.5%) only while one
+// 256 MiB copy was updated every step and that cache kept part of it.
 constexpr int kAdamWThreads = 512;
 __global__ void __launch_bounds__(kAdamWThreads) adamw_kernel(AdamWArgs a) {
     const int t = blockIdx.y;
@@ -67,10 +70,10 @@ __global__ void __launch_bounds__(kAdamWThreads) adamw_kernel(AdamWArgs a) {
                        reinterpret_cast<uintptr_t>(m) | reinterpret_cast<uintptr_t>(v)) & 15) == 0;
     const uint64_t nvec = vec ? n / 4 : 0;
     for (uint64_t i = (uint64_t)blockIdx.x * kAdamWThreads + threadIdx.x; i < nvec; i += stride) {
-        cl_f4 wv = reinterpret_cast<cl_f4 *>(w)[i];
+        cl_f4 wv = __builtin_nontemporal_load(reinterpret_cast<cl_f4 *>(w) + i);
         const cl_f4 gv = __builtin_nontemporal_load(reinterpret_cast<const cl_f4 *>(g) + i);
-        cl_f4 mv = reinterpret_cast<cl_f4 *>(m)[i];
-        cl_f4 vv = reinterpret_cast<cl_f4 *>(v)[i];
+        cl_f4 mv = __builtin_nontemporal_load(reinterpret_cast<cl_f4 *>(m) + i);
+        cl_f4 vv = __builtin_nontemporal_load(reinterpret_cast<cl_f4 *>(v) + i);
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
             float wc = wv[c], mc = mv[c], vc = vv[c];
@@ -79,9 +82,9 @@ __global__ void __launch_bounds__(kAdamWThreads) adamw_kernel(AdamWArgs a) {
             mv[c] = mc;
             vv[c] = vc;
         }
-        reinterpret_cast<cl_f4 *>(w)[i] = wv;
-        reinterpret_cast<cl_f4 *>(m)[i] = mv;
-        reinterpret_cast<cl_f4 *>(v)[i] = vv;
+        __builtin_nontemporal_store(wv, reinterpret_cast<cl_f4 *>(w) + i);
+        __builtin_nontemporal_store(mv, reinterpret_cast<cl_f4 *>(m) + i);
+        __builtin_nontemporal_store(vv, reinterpret_cast<cl_f4 *>(v) + i);
     }
     for (uint64_t i = 4 * nvec + (uint64_t)blockIdx.x * kAdamWThreads + threadIdx.x; i < n;
          i += stride) {
@@ -112,9 +115,9 @@ void adamw_step(float *const *w, const float *const *g, float *const *m, float *
         a.h = h;
         if (!most) continue;
         // enough workgroups for the largest tensor (4 elements per thread per
-        // pass), capped at 16 per CU and tensor: the loop strides the rest
+        // pass), capped at 32 per CU and tensor: the loop strides the rest
         uint64_t blocks = (most / 4 + kAdamWThreads - 1) / kAdamWThreads;
-        const uint64_t cap = (uint64_t)num_cus * 16 / (uint64_t)c;
+        const uint64_t cap = (uint64_t)num_cus * 32 / (uint64_t)c;
         if (blocks > cap) blocks = cap > 0 ? cap : 1;
         if (blocks < 1) blocks = 1;
         adamw_kernel<<<dim3((unsigned)blocks, (unsigned)c), kAdamWThreads, 0, s>>>(a);

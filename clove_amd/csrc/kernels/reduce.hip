@@ -46,9 +46,14 @@ __global__ void __launch_bounds__(256) bcast_grad_cols_kernel(const float *__res
 // r + kColGroups, ... of the chunk, kColBatch loads at a time, and the
 // kColGroups row groups are then added in group order through LDS (a fixed
 // order: deterministic).  512 workgroups at 4096 x 4096 (chunks of 64
-// rows), each thread's loads in two batches of eight.  The previous form (256 threads covering
-// 1024 columns, each thread 32 rows in two batches of 16 loads) ran half as
-// many workgroups: 55% of HBM peak end to end against 57%.
+// rows), each reading 2 KiB of every row of its chunk, each thread's loads
+// in two batches of eight; bcast_grad_final_kernel then adds the 64 chunk
+// partials of each column.  With the input cycled through copies the 256 MB
+// last-level cache cannot hold: 14.6 us (57% of HBM peak) for both passes,
+// against 19-20 us for one launch of 32-column strips over the whole height
+// (128-byte pieces of 16 KiB rows; 12.7 us only while three 64 MiB copies
+// stayed in that cache).  A form of 256 threads covering 1024 columns ran
+// half as many workgroups: 55% end to end against 57%.
 constexpr int kColThreads = 512, kColQuads = 128, kColGroups = kColThreads / kColQuads;
 constexpr int kColBatch = 8;
 __global__ void __launch_bounds__(kColThreads) bcast_grad_cols4_kernel(const float *__restrict__ g,
@@ -95,74 +100,6 @@ __global__ void __launch_bounds__(kColThreads) bcast_grad_cols4_kernel(const flo
 #pragma unroll
         for (int k = 0; k < kColGroups - 1; ++k) s += grp_sum[k][ql];
         *reinterpret_cast<cl_f4 *>(part + (uint64_t)blockIdx.y * nb + 4 * q) = s;
-    }
-}
-
-// One pass, no workspace (nb % 4 == 0, g 16-byte aligned, nb >= 16 per CU):
-// a workgroup owns a 32-column strip (one 128-byte line per row) of the
-// whole height.  Thread (q, r) = (tid % 8, tid / 8) sums column quad q over
-// rows r, r + 32, ... in row order, kStripBatch loads at a time; the 8 row
-// groups of a wave are then added by a fixed butterfly (xor 8, 16, 32) and
-// the 4 waves in wave order through LDS: a fixed tree, so the result
-// repeats bit for bit.  This replaces the column-partials kernel plus the
-// final pass (whose ~4 us were a quarter of the total at 4096 x 4096).
-// Measured at [4096, 4096] -> [4096] with cold inputs: 12.1 us (69% of HBM)
-// against 14.0 us for the two passes; 16-column strips (half lines, twice
-// the workgroups) 13-15.7 us, 64-column strips 15.7 us, 128 or 1024
-// threads 14.7-15.1 us, 512 threads 14.1 us, non-temporal loads 17.7 us;
-// batches of 4, 6 and 16 loads 13.6-14.0, 13.1-13.4 and 33 us against
-// 12.7-12.9 us for 8 (more requests in flight per CU return later).
-constexpr int kStripThreads = 256, kStripQuads = 8, kStripGroups = kStripThreads / kStripQuads;
-constexpr int kStripBatch = 8;
-__global__ void __launch_bounds__(kStripThreads) bcast_grad_strip_kernel(
-    const float *__restrict__ g, uint64_t n, uint64_t nb, float sign, int per_xcd, int strips,
-    float *__restrict__ gb) {
-    constexpr int kWaves = kStripThreads / 64;
-    __shared__ cl_f4 wsum[kWaves][kStripQuads];
-    const int L = blockIdx.x;
-    const int V = (L % 8) * per_xcd + L / 8;
-    if (V >= strips) return;
-    const int ql = threadIdx.x % kStripQuads, rg = threadIdx.x / kStripQuads;
-    const uint64_t nq = nb / 4;
-    const uint64_t q = (uint64_t)V * kStripQuads + ql;
-    const bool live = q < nq;
-    const uint64_t rows = (n + nb - 1) / nb;
-    const uint64_t full = n / nb;  // rows wholly inside n
-    const cl_f4 *g4 = reinterpret_cast<const cl_f4 *>(g);
-    cl_f4 s = {0.f, 0.f, 0.f, 0.f};
-    if (live) {
-        uint64_t r = rg;
-        for (; r + (uint64_t)(kStripBatch - 1) * kStripGroups < full;
-             r += (uint64_t)kStripBatch * kStripGroups) {
-            cl_f4 v[kStripBatch];
-#pragma unroll
-            for (int u = 0; u < kStripBatch; ++u) v[u] = g4[(r + (uint64_t)u * kStripGroups) * nq + q];
-#pragma unroll
-            for (int u = 0; u < kStripBatch; ++u) s += v[u];
-        }
-        for (; r < rows; r += kStripGroups) {
-            if (r < full) {
-                s += g4[r * nq + q];
-            } else {  // the last, partial row
-                const uint64_t i = r * nb + 4 * q;
-#pragma unroll
-                for (int c = 0; c < 4; ++c)
-                    if (i + c < n) s[c] += g[i + c];
-            }
-        }
-    }
-#pragma unroll
-    for (int m = kStripQuads; m < 64; m <<= 1)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) s[c] += __shfl_xor(s[c], m, 64);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane < kStripQuads) wsum[wave][lane] = s;
-    __syncthreads();
-    if (threadIdx.x < kStripQuads && live) {
-        cl_f4 t = wsum[0][threadIdx.x];
-#pragma unroll
-        for (int w = 1; w < kWaves; ++w) t += wsum[w][threadIdx.x];
-        *reinterpret_cast<cl_f4 *>(gb + 4 * q) = t * sign;
     }
 }
 
@@ -414,21 +351,9 @@ size_t broadcast_grad_workspace(size_t n, size_t nb) {
     return ((n + per - 1) / per) * nb;
 }
 
-bool broadcast_grad_one_pass(size_t n, size_t nb, const float *g, int num_cus) {
-    return nb % 4 == 0 && (reinterpret_cast<uintptr_t>(g) & 15) == 0 && n >= nb &&
-           nb >= 16 * (size_t)num_cus && nb < (1ull << 33);
-}
-
 void broadcast_grad(const float *g, size_t n, size_t nb, bool negate, float *part, float *gb,
-                    int num_cus, hipStream_t s) {
+                    hipStream_t s) {
     if (nb == 0) return;
-    if (broadcast_grad_one_pass(n, nb, g, num_cus)) {
-        const int strips = (int)((nb / 4 + kStripQuads - 1) / kStripQuads);
-        const int per = (strips + 7) / 8;
-        bcast_grad_strip_kernel<<<(unsigned)(8 * per), kStripThreads, 0, s>>>(
-            g, n, nb, negate ? -1.0f : 1.0f, per, strips, gb);
-        return;
-    }
     size_t chunks;
     if (nb >= 64) {
         const size_t rows = (n + nb - 1) / nb;
