@@ -83,11 +83,11 @@ def test_config4_full(hip):
 
 
 # The strip path (M <= 32, even N, K % 4 == 0): one launch, a workgroup per
-# 16-row half of a 32-column strip over the whole K.  The plan picks it when
-# B >= 4 MiB and the strips fill the chip (32 x 4096 x 4096: config 4's
-# skinny case); CLOVE_GEMM_STRIP forces it on the edge shapes here: K equal
-# to the unrolled walk (256, 4096, 16384) or not (k past K masked), partial
-# strips (N % 32 != 0), one or two row halves, partial halves.
+# 16-row half of a 32-column strip over the whole K.  The plan takes it only
+# when CLOVE_GEMM_STRIP forces it (with B cold in HBM the skinny kernel is
+# faster), as on the edge shapes here: K equal to the unrolled walk (256,
+# 4096, 16384) or not (k past K masked), partial strips (N % 32 != 0), one or
+# two row halves, partial halves.
 @pytest.mark.parametrize("m,k,n", [(1, 4, 2), (5, 12, 34), (16, 256, 64), (17, 300, 96),
                                    (31, 2052, 130), (32, 4096, 512), (32, 256, 2),
                                    (20, 16384, 64), (32, 4104, 94), (9, 8188, 4098),
@@ -377,11 +377,11 @@ def test_planner_tile_and_split_choices(hip, m, k, n):
 
 
 @pytest.mark.parametrize("m,k,n", [
-    (1, 4096, 4096),      # strip kernel at half a workgroup per CU
-    (32, 6144, 4096),     # a K the strip kernel's walks do not fit: skinny
-    (32, 4096, 14336),    # more strips than three per CU: skinny
+    (1, 4096, 4096),      # skinny kernel, one row in a 32-row block
+    (32, 6144, 4096),     # skinny kernel, K past 4096
+    (32, 4096, 14336),    # skinny kernel, wide N
     (16, 4096, 50257),    # odd N: skinny with one column block per wave
-    (32, 4096, 11008)])   # strip kernel, 688 workgroups
+    (32, 4096, 11008)])   # skinny kernel, N a multiple of 128 but not 4096
 def test_decode_shapes_as_planned(hip, m, k, n):
     """Decode-sized products on the paths the plan picks for them, against
     the oracle; a repeated call gives the same bits."""
