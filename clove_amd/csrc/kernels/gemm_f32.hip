@@ -1631,9 +1631,10 @@ GemmPlan gemm_plan(int M, int N, int K, int num_cus, int force_cfg, bool a_align
                           force_cfg < 0;
     // Strip path (one launch, no workspace; M <= 32, even N, K within the
     // longest unrolled walk of 4 waves x 64 chunks of 64 k): only when forced
-    // (CLOVE_GEMM_STRIP).  Its workgroups read B in 128-byte pieces of 16 KiB
-    // rows, which HBM serves slowly: with B cycled through copies that the
-    // 256 MB last-level cache cannot hold, as a decode step's weights are,
+    // (CLOVE_GEMM_STRIP).  Only one of each strip's two 16-row halves pulls
+    // B from HBM (the other reads it from its XCD's L2), so 128 workgroups
+    // carry the read: with B cycled through copies that the 256 MB
+    // last-level cache cannot hold, as a decode step's weights are,
     // the skinny kernel is ahead at every shape measured (1, 8, 32 x 4096 x
     // 4096: 19.0, 19.8, 21.5 us against 20.6, 22.7, 23.3; 32 x 4096 x 11008:
     // 49.0 against 61.3).  The strip kernel led only while B stayed in that

@@ -51,9 +51,10 @@ __global__ void __launch_bounds__(256) bcast_grad_cols_kernel(const float *__res
 // partials of each column.  With the input cycled through copies the 256 MB
 // last-level cache cannot hold: 14.6 us (57% of HBM peak) for both passes,
 // against 19-20 us for one launch of 32-column strips over the whole height
-// (128-byte pieces of 16 KiB rows; 12.7 us only while three 64 MiB copies
-// stayed in that cache).  A form of 256 threads covering 1024 columns ran
-// half as many workgroups: 55% end to end against 57%.
+// (128 workgroups, too few to pull 64 MiB from HBM at full rate; 12.7 us
+// only while three 64 MiB copies stayed in that cache).  A form of 256
+// threads covering 1024 columns ran half as many workgroups: 55% end to end
+// against 57%.
 constexpr int kColThreads = 512, kColQuads = 128, kColGroups = kColThreads / kColQuads;
 constexpr int kColBatch = 8;
 __global__ void __launch_bounds__(kColThreads) bcast_grad_cols4_kernel(const float *__restrict__ g,
