@@ -40,9 +40,10 @@ Rank 0 prints ONE JSON line on stdout:
   parity_checked  true when every checked part's output (one more launch
                of its first input set after all timings, the timed steps'
                bits: the kernels are deterministic) is within its parity
-               bound of the oracle's output, computed by its CPU leg; else
-               the failing parts, and the exit status is 1.  parity_parts
-               names the parts checked.
+               bound of the oracle's output, computed by its CPU leg (AdamW:
+               one step from zero moments on copies, bit for bit; attention:
+               the leg's sampled query rows); else the failing parts, and
+               the exit status is 1.  parity_parts names the parts checked.
 Everything else goes to stderr.  This backend runs on one GPU: --gpus > 1
 exits with a message.
 """
@@ -513,7 +514,15 @@ def bench_backward(ca, oracle, args, out):
         def leg(part=part, nbytes=nbytes):
             wh, gh = w.numpy(), gw.numpy()
             zh = np.zeros(N, np.float32)
-            t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1))
+            want = []
+            t = cpu_time(lambda: oracle.adamw(wh, gh, zh, zh, 1), keep=want)
+            # one more step, from zero moments on fresh copies of the
+            # parameter and gradient the oracle stepped, bit for bit
+            tw, tm, tv = ca.tensor(wh), ca.tensor(zh), ca.tensor(zh)
+            ca.adamw_step([tw], [ca.tensor(gh)], [tm], [tv], 1)
+            check_parity("adamw_4096x4096",
+                         np.concatenate([t_.numpy().ravel() for t_ in (tw, tm, tv)]),
+                         np.concatenate([h.ravel() for h in want[0]]), 0.0, 0.0)
             part["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
                                               "full 16.7M-element parameter, one step, "
                                               "median of 3")
@@ -548,7 +557,11 @@ def bench_backward(ca, oracle, args, out):
     if oracle is not None:
         def leg(part=part):
             ah, bh, dch = a.numpy(), b.numpy(), dc.numpy()
-            t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch), reps=1)
+            want = []
+            t = cpu_time(lambda: oracle.matmul_backward(ah, bh, dch), reps=1, keep=want)
+            da, db = ca.matmul_backward(a, b, dc)
+            check_parity("matmul_backward_4096", np.stack([da.numpy(), db.numpy()]),
+                         np.stack(want[0]), 2e-3, gemm_atol(np.stack(want[0])))
             part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
                                               "full grad_a and grad_b at 4096^3, one run")
         defer(leg)
@@ -638,9 +651,13 @@ def bench_attention(ca, oracle, args, out):
             rows = [255 + 256 * i for i in range(16)]  # mean visible keys ~ S/2, as over all rows
             t_rope = cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(0, 0)), reps=1)
             t_rows = 0.0
+            want = []
             for r in rows:
                 t_rows += cpu_time(lambda: oracle.attention(qh, kh, vh, H, rows=(r, r + 1)),
-                                   reps=1)
+                                   reps=1, keep=want)
+            got = ca.flash_attention(q, k, v, H).numpy()
+            check_parity("flash_attention_4096", np.stack([got[:, r] for r in rows]),
+                         np.stack([w[:, r] for w, r in zip(want, rows)]), 2e-3, 1e-5)
             t_rows = max(t_rows - len(rows) * t_rope, 0.0)
             t = t_rope + t_rows * S / len(rows)
             part["cpu_baseline"] = cpu_record(oracle, round(flops / t / 1e12, 5), "TFLOP/s",
@@ -664,7 +681,9 @@ def bench_attention(ca, oracle, args, out):
     if oracle is not None:
         def leg2():
             xs = x.numpy()
-            t = cpu_time(lambda: oracle.rope(xs, D))
+            want = []
+            t = cpu_time(lambda: oracle.rope(xs, D), keep=want)
+            check_parity("rope", ca.rope(x, D).numpy(), want[0], 1e-5, 1e-6 * S / 64)
             out["rope"]["cpu_baseline"] = cpu_record(oracle, round(nbytes / t / 1e9, 2), "GB/s",
                                                      f"full [{S}, {H * D}] workload, median of 3")
         defer(leg2)
