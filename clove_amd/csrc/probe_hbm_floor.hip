@@ -6,7 +6,8 @@
 // launch (512 MiB: the last-level cache cannot keep them).  Each workgroup
 // sums W contiguous bytes of every row of its row range and stores its
 // partial column sums (no combine), for W from a 128-byte piece to the whole
-// 16 KiB row, at 128 to 512 workgroups; it prints the time per launch and
+// 16 KiB row, at 128 to 512 workgroups (128 also with 512 threads each:
+// twice the loads in flight per CU); it prints the time per launch and
 // the read rate against the 8 TB/s peak.  With three copies instead (192
 // MiB, all of them in the cache) the same launches read far faster.
 // Part 2: the cost of a dependent second launch: a writer of n floats
@@ -160,6 +161,7 @@ int main() {
     // rows of partials of 4096 floats, at most 4 MiB
     const StripCase cases[] = {
         {"128 B pieces, 128 workgroups", launch_strips<8, 256>, 1},
+        {"128 B pieces, 128 x 512 thr.", launch_strips<8, 512>, 1},
         {"128 B pieces, 256 workgroups", launch_strips<8, 256>, 2},
         {"512 B pieces, 256 workgroups", launch_strips<32, 256>, 8},
         {"2 KiB pieces, 256 workgroups", launch_strips<128, 256>, 32},
