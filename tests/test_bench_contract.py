@@ -126,3 +126,20 @@ def test_committed_traffic_summary_covers_every_part(name):
         kernels = json.load(f)["kernels"]
     missing = [k for k in bench.PART_KERNELS[name] if k not in kernels]
     assert not missing, f"{name}: {missing} not in profiles/hbm_traffic.json"
+
+
+def test_check_parity_records_pass_and_failure(monkeypatch):
+    """A part within |g - c| <= atol + rtol |c| is "ok"; one element past the
+    bound, a shape mismatch or a NaN is reported as a failure."""
+    monkeypatch.setattr(bench, "PARITY", {})
+    want = [1.0, -2.0, 100.0]
+    bench.check_parity("inside", [1.0 + 1.2e-6, -2.0, 100.0 - 1e-4], want, 1e-6, 5e-7)
+    bench.check_parity("outside", [1.0, -2.0 - 1e-3, 100.0], want, 1e-6, 5e-7)
+    bench.check_parity("shape", [1.0, -2.0], want, 1e-6, 5e-7)
+    bench.check_parity("nan", [1.0, float("nan"), 100.0], want, 1e-6, 5e-7)
+    bench.check_parity("exact", [1.0, -2.0, 100.0], want, 0.0, 0.0)
+    assert bench.PARITY["inside"] == "ok"
+    assert bench.PARITY["exact"] == "ok"
+    assert bench.PARITY["outside"].startswith("1 of 3 elements")
+    assert bench.PARITY["shape"].startswith("shape")
+    assert bench.PARITY["nan"].startswith("1 of 3 elements")
