@@ -81,3 +81,46 @@ def test_layer_norm_short_gamma_rejected(hip):
     x = hip.tensor(np.ones((2, 8), np.float32))
     with pytest.raises(hip.CloveError):
         hip.layer_norm(x, hip.tensor(np.ones(4, np.float32)), hip.tensor(np.ones(8, np.float32)))
+
+
+def special_rows(cols, seed):
+    """Rows a softmax must keep finite by subtracting the row max (entries of
+    +-1000 and 88.7, past exp's range), rows with -inf entries (masked
+    positions), and rows whose result is NaN in the reference (all -inf, a
+    +inf entry, a NaN entry)."""
+    g = rng(seed)
+    x = g.normal(0, 2, (8, cols)).astype(np.float32)
+    x[0, ::3] = 1000.0
+    x[1, :] = -1000.0
+    x[1, cols // 2] = -999.0
+    x[2, ::2] = 88.7
+    x[3, 1::2] = -np.inf
+    x[4, :] = -np.inf
+    x[5, cols - 1] = np.inf
+    x[6, cols // 3] = np.nan
+    return x
+
+
+@pytest.mark.parametrize("cols", [64, 1000, 4096])
+def test_softmax_special_values(hip, cols):
+    x = special_rows(cols, cols)
+    got = hip.softmax(hip.tensor(x)).numpy()
+    want = oracle.softmax(x)
+    assert np.array_equal(np.isnan(got), np.isnan(want)), f"softmax {cols}: NaN positions"
+    ok = ~np.isnan(want)
+    assert_close(got[ok], want[ok], 1e-4, 1e-9, f"softmax special rows x{cols}")
+    assert np.all(got[3, 1::2] == 0.0)  # masked entries are exactly zero
+
+
+@pytest.mark.parametrize("cols", [64, 1000, 4096])
+def test_layer_norm_offset_and_tiny_rows(hip, cols):
+    """Rows on a common offset (mean 3, spread 1: the two-pass variance keeps
+    the offset out of the spread) and rows on a tiny scale (spread 1e-3, a
+    variance of 1e-6 below eps = 1e-5, so eps sets the scale)."""
+    g = rng(cols + 7)
+    x = np.concatenate([3.0 + g.normal(0, 1, (4, cols)),
+                        g.normal(0, 1e-3, (4, cols))]).astype(np.float32)
+    gam = g.uniform(0.5, 1.5, cols).astype(np.float32)
+    bet = g.uniform(-0.1, 0.1, cols).astype(np.float32)
+    got = hip.layer_norm(hip.tensor(x), hip.tensor(gam), hip.tensor(bet)).numpy()
+    assert_close(got, oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm rows x{cols}")
