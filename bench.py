@@ -709,6 +709,9 @@ PART_KERNELS = {
     "mse": ["sq_diff_partial_kernel<true>", "ordered_sum_kernel"],
     "mse_backward": ["mse_backward_kernel<true>"],
     "rope": ["rope_rows_kernel<true>"],
+    # the 4096x4096 parameter's launches (the MLP's small ones run the same
+    # kernel at a smaller grid and are summarised apart)
+    "adamw_4096x4096": ["adamw_kernel (4096x4096)"],
 }
 
 
