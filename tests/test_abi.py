@@ -77,7 +77,7 @@ def test_integration_rust_block_matches_the_header():
         rust[name] = 0 if not params else params.count(",") + 1
     header = header_arities()
     assert header and set(header) == set(declared_functions())
-    assert sorted(set(header) - set(rust)) == [], "missing from INTEGRATION.md"
+    assert sorted(set(header) - set(rust)) == [], "missing from the Rust extern block"
     assert sorted(set(rust) - set(header)) == [], "not in the header"
     wrong = {n: (header[n], rust[n]) for n in header if header[n] != rust[n]}
     assert not wrong, f"parameter counts differ (header, rust): {wrong}"
