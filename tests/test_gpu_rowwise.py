@@ -124,3 +124,22 @@ def test_layer_norm_offset_and_tiny_rows(hip, cols):
     bet = g.uniform(-0.1, 0.1, cols).astype(np.float32)
     got = hip.layer_norm(hip.tensor(x), hip.tensor(gam), hip.tensor(bet)).numpy()
     assert_close(got, oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm rows x{cols}")
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_rows(hip, seed):
+    """Seeded shapes across the kernel families: widths up to 1024 (a wave
+    per row), multiples of 4 up to 32768 (a workgroup per row, every vector
+    count), and other widths past 1024 (the loop kernels); rows 1-299."""
+    g = rng(3000 + seed)
+    rows = int(g.integers(1, 300))
+    cols = int([g.integers(1, 1025), 4 * g.integers(257, 8193), g.integers(1025, 20000)][
+        int(g.integers(0, 3))])
+    x = g.normal(0, 2, (rows, cols)).astype(np.float32)
+    what = f"seed {seed}: {rows}x{cols}"
+    assert_close(hip.softmax(hip.tensor(x)).numpy(), oracle.softmax(x), 1e-4, 1e-9,
+                 f"softmax {what}")
+    gam = g.uniform(0.5, 1.5, cols).astype(np.float32)
+    bet = g.uniform(-0.1, 0.1, cols).astype(np.float32)
+    got = hip.layer_norm(hip.tensor(x), hip.tensor(gam), hip.tensor(bet)).numpy()
+    assert_close(got, oracle.layer_norm(x, gam, bet), 1e-4, 1e-5, f"layer_norm {what}")
