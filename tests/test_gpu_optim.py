@@ -65,3 +65,25 @@ def test_adamw_errors(hip):
         hip.adamw_step([a], [b], [a], [a], 1)
     with pytest.raises(hip.CloveError):
         hip.adamw_step([a], [a], [a], [a], 0)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_adamw_random_bit_exact(hip, seed):
+    """Seeded launches of 1-16 parameter tensors of random sizes (the most
+    one launch carries), random hyperparameters and gradient scales, three
+    steps each, bit for bit against the oracle."""
+    g = rng(4000 + seed)
+    sizes = [int(g.choice([g.integers(1, 64), g.integers(64, 5000), g.integers(5000, 300000)]))
+             for _ in range(int(g.integers(1, 17)))]
+    hyper = dict(lr=float(np.float32(g.uniform(1e-4, 0.1))),
+                 beta1=float(np.float32(g.uniform(0.8, 0.95))),
+                 beta2=float(np.float32(g.uniform(0.9, 0.9999))),
+                 eps=float(np.float32(10 ** g.uniform(-9, -5))),
+                 weight_decay=float(np.float32(g.uniform(0, 0.1))),
+                 loss_scale=float(np.float32(2 ** int(g.integers(0, 17)))),
+                 clip=float(np.float32(g.uniform(0.1, 2.0))))
+    tw, tm, tv, ws, ms, vs = run_steps(hip, sizes, 3, 4100 + seed, **hyper)
+    for i in range(len(sizes)):
+        assert np.array_equal(tw[i].numpy(), ws[i]), f"seed {seed} w[{i}] ({sizes[i]}) {hyper}"
+        assert np.array_equal(tm[i].numpy(), ms[i]), f"seed {seed} m[{i}]"
+        assert np.array_equal(tv[i].numpy(), vs[i]), f"seed {seed} v[{i}]"
